@@ -1,0 +1,262 @@
+/*
+ * stark_qmm.h -- C ABI of the MI355X (gfx950) quantized matrix-product path.
+ *
+ * This is the drop-in boundary for the reference engine's quantized matmul
+ * operators. Every entry point names the reference interface it replaces
+ * (paths relative to the reference root, `crates/stark-engine/src/` written
+ * as `src/`). Conventions follow the reference's own C bridge
+ * (vendor/glm-exl3-bridge/include/stark_glm.h:11-31): a status enum, an ABI
+ * version constant, opaque handles, plain pointers and sizes.
+ *
+ * Memory: all tensor pointers are DEVICE pointers owned by the caller and
+ * borrowed for the duration of the (stream-ordered) call. The library never
+ * frees caller memory. `stream` is a hipStream_t passed as void* (NULL = the
+ * default stream). Work is asynchronous on that stream unless an entry point
+ * says otherwise.
+ *
+ * Threading: a handle is not reentrant (the reference keeps each kernel object
+ * behind a Mutex, src/encodable_block/linear/matmul.rs:42); distinct handles
+ * may be used concurrently.
+ */
+#ifndef STARK_QMM_H
+#define STARK_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STARK_QMM_ABI_VERSION 1u
+
+typedef uint32_t stark_qmm_status;
+enum {
+    STARK_QMM_OK = 0,
+    /* hybrid Error::Invalid (src/engine/hybrid/weight_metal.rs:435-537) and malformed arguments */
+    STARK_QMM_INVALID_ARGUMENT = 1,
+    STARK_QMM_ABI_MISMATCH = 2,
+    /* MatmulError::UnsupportedDataType (src/backends/common/kernel/matmul/error.rs:12) */
+    STARK_QMM_UNSUPPORTED_DATA_TYPE = 3,
+    /* MatmulError::UnsupportedGroupSize (error.rs:14) */
+    STARK_QMM_UNSUPPORTED_GROUP_SIZE = 4,
+    /* MatmulError::UnsupportedDOp (error.rs:16-19) */
+    STARK_QMM_UNSUPPORTED_D_OP = 5,
+    /* MatmulError::UnsupportedLayout (error.rs:20-23), e.g. an undersized codes buffer */
+    STARK_QMM_UNSUPPORTED_LAYOUT = 6,
+    /* MatmulError::IncompatibleA (error.rs:24-28) */
+    STARK_QMM_INCOMPATIBLE_A = 7,
+    /* hybrid Error::Unsupported */
+    STARK_QMM_UNSUPPORTED = 8,
+    STARK_QMM_OUT_OF_MEMORY = 9,
+    /* MatmulError::BackendError (error.rs:29-30): a HIP call failed */
+    STARK_QMM_DEVICE_FAILURE = 10,
+    /* caller workspace smaller than the size query returned */
+    STARK_QMM_WORKSPACE_TOO_SMALL = 11
+};
+
+/* Data types. The numbers are the GGUF kind ids the hybrid engine already uses
+ * for plane dtypes (src/engine/hybrid/weight_metal.rs:486-490). */
+enum { STARK_QMM_F32 = 0, STARK_QMM_F16 = 1, STARK_QMM_BF16 = 30 };
+
+/* QuantParamsLayout (src/backends/common/kernel/matmul/mod.rs:19-25). */
+enum { STARK_QMM_LAYOUT_OUTPUT_GROUP = 0, /* [N, G] */
+       STARK_QMM_LAYOUT_GROUP_OUTPUT = 1  /* [G, round_up_4(N)] */ };
+
+/* QuantizedCorrection (src/backends/common/kernel/matmul/matmul_b.rs:24-29). */
+enum { STARK_QMM_CORRECTION_SYMMETRIC = 0, STARK_QMM_CORRECTION_BIASES = 1, STARK_QMM_CORRECTION_ZERO_POINTS = 2 };
+
+/* QuantizationMode (src/backends/common/gpu_types/quantization.rs:9-23). */
+enum { STARK_QMM_MODE_U4 = 0, STARK_QMM_MODE_I8 = 1, STARK_QMM_MODE_U8 = 2, STARK_QMM_MODE_U5 = 3,
+       STARK_QMM_MODE_U6 = 4, STARK_QMM_MODE_U3 = 5 };
+
+/* Hybrid packed kinds (src/engine/hybrid/weights.rs:2565-2584). */
+enum { STARK_QMM_KIND_Q8_0 = 8, STARK_QMM_KIND_Q4_K = 12 };
+
+/* ------------------------------------------------------------------ */
+/* Generic engine operator: trait MatmulKernel                         */
+/* (src/backends/common/kernel/matmul/kernel.rs:15-79)                 */
+/* ------------------------------------------------------------------ */
+
+typedef struct stark_qmm_kernel stark_qmm_kernel;
+
+/* QuantParams (src/backends/common/kernel/matmul/mod.rs:33-41). */
+typedef struct stark_qmm_quant_params {
+    uint32_t layout;      /* STARK_QMM_LAYOUT_* */
+    uint32_t row_count;   /* N of the stored planes */
+    uint32_t group_count; /* G = K / group_size */
+    uint32_t materialize_affine_input_sum; /* MLXSpec flag (src/config/weight_matrix/mlx_spec.rs:10-12) */
+} stark_qmm_quant_params;
+
+/* MatmulB (src/backends/common/kernel/matmul/matmul_b.rs:6-22). `codes == NULL`
+ * selects MatmulB::FullPrecision with `values` in the kernel's weights dtype. */
+typedef struct stark_qmm_b {
+    const void* values;        /* FullPrecision only */
+    const void* codes;         /* packed codes, [N, K*bits/8] bytes */
+    uint64_t codes_size;       /* bytes available at codes (validated as reference.rs:62-71) */
+    const void* scales;        /* weights dtype, plane per params.layout */
+    uint32_t correction;       /* STARK_QMM_CORRECTION_* */
+    const void* correction_data; /* biases (weights dtype) or packed zero points (u8) */
+    stark_qmm_quant_params params;
+    uint32_t mode;             /* STARK_QMM_MODE_* */
+    uint32_t group_size;
+    uint32_t signed_codes;
+} stark_qmm_b;
+
+/* MatmulDOps (src/backends/common/kernel/matmul/d_ops.rs:3-9). */
+typedef struct stark_qmm_d_ops {
+    float ab_scale;           /* 1.0 for none */
+    uint32_t accumulate;      /* d = ... + d */
+    const void* bias;         /* [N] in the weights dtype, or NULL */
+    const void* rht_factors;  /* output RHT: must be NULL (STARK_QMM_UNSUPPORTED_D_OP) */
+    uint32_t has_soft_cap;
+    float soft_cap;
+} stark_qmm_d_ops;
+
+/* MatmulArguments (src/backends/common/kernel/matmul/arguments.rs:7-25). */
+typedef struct stark_qmm_args {
+    uint32_t struct_size;     /* sizeof(stark_qmm_args) */
+    const void* a;            /* MatmulA::FullPrecision values [M, K] in the input dtype */
+    uint64_t a_offset;        /* element offset into a */
+    stark_qmm_b b;
+    uint32_t b_leading_dimension; /* FullPrecision B only; 0 = default */
+    uint32_t b_transpose;     /* must be 1 for quantized B (the only layout the path uses) */
+    void* d;                  /* [M, N] in the output dtype */
+    stark_qmm_d_ops d_ops;
+    const uint32_t* gather_indices; /* [M*N] weight row per output, or NULL */
+    uint32_t m, n, k;
+} stark_qmm_args;
+
+/* Replaces MatmulKernel::new (kernel.rs:18-23; CPU twin
+ * src/backends/cpu/kernel/matmul/kernel.rs:31-56): F32/F16/BF16 only. */
+stark_qmm_status stark_qmm_create(uint32_t weights_dtype, uint32_t input_dtype, uint32_t output_dtype,
+                                  stark_qmm_kernel** out);
+
+/* Replaces MatmulKernel::encode (kernel.rs:51-62; Metal dispatch
+ * src/backends/metal/kernel/matmul/mod.rs:551-613). Chooses the GEMV/verify
+ * path for M <= 16 and the MFMA dequant-GEMM for larger M. */
+stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kernel, const stark_qmm_args* args, void* stream);
+
+/* Independent products with one submission, in the manner of the hybrid
+ * engine's Weights::matvec_many (src/engine/hybrid/weights.rs:1323-1388): every
+ * args[i] is validated as stark_qmm_encode would, then all eligible GEMV
+ * products share one launch per (bits, M class). Outputs must not alias inputs
+ * of other entries. */
+stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kernel, const stark_qmm_args* args, uint32_t count,
+                                       void* stream);
+
+/* Replaces MatmulKernel::set_reference_accumulation (kernel.rs:34-37): when
+ * enabled, every M uses the GEMV/verify kernels (f32 dequant semantics). */
+stark_qmm_status stark_qmm_set_reference_accumulation(stark_qmm_kernel* kernel, uint32_t enabled);
+
+void stark_qmm_destroy(stark_qmm_kernel* kernel);
+
+uint32_t stark_qmm_abi_version(void);
+/* Text for a status code; never NULL. */
+const char* stark_qmm_status_string(stark_qmm_status status);
+
+/* ------------------------------------------------------------------ */
+/* Hybrid engine operator: weight_metal::mapped_many                   */
+/* (src/engine/hybrid/weight_metal.rs:376-392, 539-545)                */
+/* ------------------------------------------------------------------ */
+
+/* MatrixFormat (weight_metal.rs:376-383). */
+enum { STARK_QMM_FORMAT_PACKED = 0, STARK_QMM_FORMAT_AFFINE = 1 };
+
+/* MappedMatrix: one matrix view. Affine planes are [rows, G] (native MLX). */
+typedef struct stark_qmm_mapped_matrix {
+    const void* codes;
+    uint64_t codes_length;  /* bytes */
+    const void* scales;     /* affine only */
+    const void* biases;     /* affine only */
+    uint64_t plane_length;  /* bytes of each plane; 0 for packed */
+} stark_qmm_mapped_matrix;
+
+/* MappedOperation (weight_metal.rs:385-392). inputs: [batches, columns] f32
+ * where batches = matrix_count, or rows / rows_per_batch when rows_per_batch
+ * != 0 (a single matrix). Output: [matrix_count * rows] f32. */
+typedef struct stark_qmm_mapped_op {
+    const stark_qmm_mapped_matrix* matrices; /* HOST array of matrix views */
+    uint32_t matrix_count;
+    const float* inputs;    /* device */
+    uint64_t input_length;  /* floats */
+    uint64_t rows, columns, rows_per_batch;
+    uint32_t format;        /* STARK_QMM_FORMAT_* */
+    uint32_t packed_kind;   /* STARK_QMM_KIND_* for packed */
+    uint32_t scale_dtype;   /* affine: STARK_QMM_F32 / F16 / BF16 */
+    uint32_t bits;          /* affine: 4 or 8 */
+    uint32_t group;         /* affine: 32, 64 or 128 */
+} stark_qmm_mapped_op;
+
+/* Replaces mapped_many (weight_metal.rs:539-545): validates every operation as
+ * parameters_for_input does (weight_metal.rs:442-537; at most 64 ops), runs all
+ * of them in one launch per format, and -- like the reference -- returns only
+ * after the work completes. A non-finite input makes the call return
+ * STARK_QMM_INVALID_ARGUMENT (weight_metal.rs:435-440); outputs are then
+ * unspecified. outputs[i] is a device pointer with room for
+ * matrix_count * rows floats. */
+stark_qmm_status stark_qmm_mapped_many(const stark_qmm_mapped_op* ops, uint32_t op_count, float* const* outputs,
+                                       void* stream);
+
+/* Asynchronous form of stark_qmm_mapped_many: no host wait. The finite check
+ * ORs 1 into *status_word (device u32, caller-zeroed) when any input is not
+ * finite. */
+stark_qmm_status stark_qmm_mapped_many_async(const stark_qmm_mapped_op* ops, uint32_t op_count,
+                                             float* const* outputs, uint32_t* status_word, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* MoE kernels (src/backends/cpu/kernel/moe.rs; Metal                   */
+/* src/backends/metal/kernel/moe.metal)                                 */
+/* ------------------------------------------------------------------ */
+
+/* MoeRoute (moe.rs:23-85, moe.metal:13-50): softmax over experts, repeated
+ * argmax top-k (ties to the lowest id), renormalised weights. */
+stark_qmm_status stark_qmm_moe_route(const float* logits, uint32_t* ids, float* weights, uint32_t rows,
+                                     uint32_t experts, uint32_t active, uint32_t round_weights,
+                                     uint32_t round_logits, void* stream);
+
+/* MoeAdjustRoutes (moe.rs:147-184, moe.metal:88-104). */
+stark_qmm_status stark_qmm_moe_adjust_routes(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
+                                             uint32_t experts, uint32_t active, uint32_t sort_ids, void* stream);
+
+/* MoeGatherRows (moe.rs:87-107, moe.metal:52-63). */
+stark_qmm_status stark_qmm_moe_gather_rows(const uint32_t* ids, uint32_t* indices, uint32_t route_offset,
+                                           uint32_t rows_per_expert, uint32_t experts, uint32_t length,
+                                           void* stream);
+
+/* MoeAccumulate (moe.rs:109-145, moe.metal:65-86). input/output are bf16. */
+stark_qmm_status stark_qmm_moe_accumulate(const void* input, const float* weights, float* accumulator,
+                                          void* output, uint32_t length, uint32_t weight_offset,
+                                          uint32_t output_offset, uint32_t initialize, uint32_t finalize,
+                                          uint32_t round_product, uint32_t round_accumulator, void* stream);
+
+/* RoutedExperts::encode_scaled (src/encodable_block/mlp/routed.rs:154-257) as
+ * one fused device pipeline: route -> (optional) adjust -> expert-index
+ * compaction (counting sort into expert-major slots, after
+ * vendor/lily-core/src/kernels/metal/moe.metal:905-1036) -> grouped gate/up
+ * matvec with SiLU gating -> grouped down matvec -> weighted accumulation.
+ * Banks flatten [experts, rows, cols] (routed.rs:1-5): up [E*2*hidden, model]
+ * with rows [value(hidden) | gate(hidden)] per expert, down [E*model, hidden].
+ * Both banks are 4- or 8-bit affine with BF16 scale/bias planes. */
+typedef struct stark_qmm_routed_args {
+    uint32_t struct_size;
+    const void* input;          /* [rows, model] bf16 */
+    const float* router_logits; /* [rows, experts] f32 */
+    const float* expert_scales; /* [experts] f32 or NULL */
+    stark_qmm_b up;             /* bank [experts*2*hidden, model] */
+    stark_qmm_b down;           /* bank [experts*model, hidden] */
+    void* output;               /* [rows, model] bf16 */
+    uint32_t rows, model, hidden, experts, active;
+    uint32_t round_logits_bf16, round_weights_bf16, round_products_bf16, round_accumulator_bf16, sort_expert_ids;
+    void* workspace;            /* device, >= stark_qmm_routed_experts_workspace_size() bytes */
+    uint64_t workspace_size;
+} stark_qmm_routed_args;
+
+uint64_t stark_qmm_routed_experts_workspace_size(uint32_t rows, uint32_t model, uint32_t hidden, uint32_t experts,
+                                                 uint32_t active);
+stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,354 @@
+"""numpy/ctypes wrapper over the C oracle (oracle/stark_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, and only as the checker. The product package
+(stark_amd) never imports this module.
+
+Every wrapped function restates a reference function; the citations live in
+stark_oracle.c next to each definition.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libstark_oracle.so")
+
+F32, F16, BF16 = 0, 1, 30
+OUTPUT_GROUP, GROUP_OUTPUT = 0, 1
+SYMMETRIC, BIASES, ZERO_POINTS = 0, 1, 2
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class MatmulArgs(C.Structure):
+    _fields_ = [
+        ("a", C.c_void_p), ("a_offset", C.c_size_t),
+        ("b_values", C.c_void_p), ("b_leading_dimension", C.c_uint32),
+        ("codes", C.c_void_p), ("codes_size", C.c_size_t),
+        ("scales", C.c_void_p), ("correction", C.c_int), ("correction_data", C.c_void_p),
+        ("layout", C.c_int), ("row_count", C.c_uint32), ("group_count", C.c_uint32),
+        ("materialize_affine_input_sum", C.c_int), ("bits", C.c_int), ("group_size", C.c_uint32),
+        ("signed_codes", C.c_int), ("b_transpose", C.c_int),
+        ("d", C.c_void_p), ("ab_scale", C.c_float), ("accumulate", C.c_int), ("bias", C.c_void_p),
+        ("has_soft_cap", C.c_int), ("soft_cap", C.c_float),
+        ("gather_indices", C.c_void_p), ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32),
+        ("weights_dt", C.c_int), ("input_dt", C.c_int), ("output_dt", C.c_int),
+    ]
+
+
+def _declare(l):
+    vp, sz, u32, u16, u8, i32, f = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint16, C.c_uint8, C.c_int, C.c_float
+    sig = {
+        "so_bf16_to_f32": (f, [u16]), "so_f32_to_bf16": (u16, [f]),
+        "so_f16_to_f32": (f, [u16]), "so_f32_to_f16": (u16, [f]),
+        "so_f32_to_bf16_n": (None, [vp, vp, sz]), "so_bf16_to_f32_n": (None, [vp, vp, sz]),
+        "so_f32_to_f16_n": (None, [vp, vp, sz]), "so_f16_to_f32_n": (None, [vp, vp, sz]),
+        "so_packed_code": (u8, [vp, i32, sz]),
+        "so_quant_strides": (None, [i32, u32, u32, u32, vp, vp]),
+        "so_matmul": (i32, [C.POINTER(MatmulArgs)]),
+        "so_matmul_parallel": (i32, [C.POINTER(MatmulArgs), i32]),
+        "so_reference_affine_linear_bf16": (None, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]),
+        "so_block_layout": (i32, [u32, vp, vp]),
+        "so_scale_min": (None, [vp, i32, vp, vp]),
+        "so_decode_block": (i32, [u32, vp, sz, vp, sz]),
+        "so_hybrid_packed_matvec": (i32, [u32, vp, sz, sz, vp, vp]),
+        "so_hybrid_affine_matvec": (i32, [vp, vp, vp, i32, i32, sz, sz, sz, vp, vp]),
+        "so_moe_route": (None, [vp, vp, vp, u32, u32, u32, u32, u32]),
+        "so_moe_gather_rows": (None, [vp, vp, u32, u32, u32, u32]),
+        "so_moe_accumulate": (None, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]),
+        "so_moe_adjust_routes": (None, [vp, vp, vp, u32, u32, u32, u32]),
+        "so_gated_silu_bf16": (None, [vp, vp, u32, u32]),
+        "so_quantize_affine": (None, [vp, sz, sz, i32, sz, i32, vp, vp, vp]),
+        "so_quantize_q8_0": (None, [vp, sz, sz, vp]),
+        "so_quantize_q4_k": (None, [vp, sz, sz, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(l, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+# ----------------------------------------------------------------- conversions
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().so_f32_to_bf16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().so_bf16_to_f32_n(_p(h), _p(out), h.size)
+    return out
+
+
+def f32_to_f16(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().so_f32_to_f16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def f16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().so_f16_to_f32_n(_p(h), _p(out), h.size)
+    return out
+
+
+def to_dtype_bits(x, dt) -> np.ndarray:
+    """f32 values -> storage array of dtype id `dt` (uint16 bits or float32)."""
+    if dt == F32:
+        return np.ascontiguousarray(x, dtype=np.float32)
+    return f32_to_bf16(x) if dt == BF16 else f32_to_f16(x)
+
+
+def from_dtype_bits(x, dt) -> np.ndarray:
+    if dt == F32:
+        return np.asarray(x, dtype=np.float32)
+    return bf16_to_f32(x) if dt == BF16 else f16_to_f32(x)
+
+
+def packed_code(codes, bits: int, index: int) -> int:
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    return int(lib().so_packed_code(_p(codes), bits, index))
+
+
+def quant_strides(layout: int, row_count: int, group_count: int, packing_divisor: int = 1):
+    os_, gs = C.c_uint32(), C.c_uint32()
+    lib().so_quant_strides(layout, row_count, group_count, packing_divisor, C.byref(os_), C.byref(gs))
+    return os_.value, gs.value
+
+
+# ----------------------------------------------------------------- matmul
+
+def matmul(*, a, m, n, k, codes=None, scales=None, correction=BIASES, correction_data=None,
+           layout=OUTPUT_GROUP, row_count=None, group_count=None, bits=4, group_size=64,
+           signed_codes=False, materialize=False, b_values=None, b_leading_dimension=0, b_transpose=True,
+           d=None, ab_scale=1.0, accumulate=False, bias=None, soft_cap=None, gather=None,
+           weights_dt=BF16, input_dt=BF16, output_dt=BF16, a_offset=0, threads=0):
+    """MatmulCpuKernel::encode restated. Arrays are storage arrays (uint16 bits
+    for bf16/f16, float32 for f32). Returns (status, d)."""
+    keep = []
+
+    def arr(x, dtype=None):
+        if x is None:
+            return None
+        x = np.ascontiguousarray(x, dtype=dtype) if dtype is not None else np.ascontiguousarray(x)
+        keep.append(x)
+        return x
+
+    out_np = np.float32 if output_dt == F32 else np.uint16
+    if d is None:
+        d = np.zeros(m * n, out_np)
+    d = np.ascontiguousarray(d, dtype=out_np).copy()
+    args = MatmulArgs()
+    args.a = _p(arr(a))
+    args.a_offset = a_offset
+    args.b_values = _p(arr(b_values))
+    args.b_leading_dimension = b_leading_dimension
+    c = arr(codes, np.uint8)
+    args.codes = _p(c)
+    args.codes_size = 0 if c is None else c.size
+    args.scales = _p(arr(scales))
+    args.correction = correction
+    args.correction_data = _p(arr(correction_data))
+    args.layout = layout
+    args.row_count = n if row_count is None else row_count
+    args.group_count = (k // group_size if group_size else 0) if group_count is None else group_count
+    args.materialize_affine_input_sum = int(materialize)
+    args.bits = bits
+    args.group_size = group_size
+    args.signed_codes = int(signed_codes)
+    args.b_transpose = int(b_transpose)
+    args.d = _p(d)
+    args.ab_scale = ab_scale
+    args.accumulate = int(accumulate)
+    args.bias = _p(arr(bias))
+    args.has_soft_cap = int(soft_cap is not None)
+    args.soft_cap = 0.0 if soft_cap is None else soft_cap
+    args.gather_indices = _p(arr(gather, np.uint32))
+    args.m, args.n, args.k = m, n, k
+    args.weights_dt, args.input_dt, args.output_dt = weights_dt, input_dt, output_dt
+    if threads:
+        st = lib().so_matmul_parallel(C.byref(args), threads)
+    else:
+        st = lib().so_matmul(C.byref(args))
+    return st, d
+
+
+def reference_affine_linear_bf16(input_bits, codes, scales, biases, m, n, k, bits=4, indices=None,
+                                 bank_rows=None, sos=None, sgs=None, f32_out=False):
+    G = k // 64
+    if sos is None:
+        sos, sgs = G, 1
+    bank_rows = n if bank_rows is None else bank_rows
+    input_bits = np.ascontiguousarray(input_bits, np.uint16)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    scales = np.ascontiguousarray(scales, np.uint16)
+    biases = np.ascontiguousarray(biases, np.uint16)
+    idx = None if indices is None else np.ascontiguousarray(indices, np.uint32)
+    ob = None if f32_out else np.zeros(m * n, np.uint16)
+    of = np.zeros(m * n, np.float32) if f32_out else None
+    lib().so_reference_affine_linear_bf16(_p(input_bits), _p(codes), _p(scales), _p(biases), _p(idx), _p(ob),
+                                          _p(of), m, n, k, bank_rows, bits, sos, sgs)
+    return of if f32_out else ob
+
+
+# ----------------------------------------------------------------- GGUF
+
+def block_layout(kind: int):
+    e, b = C.c_size_t(), C.c_size_t()
+    if lib().so_block_layout(kind, C.byref(e), C.byref(b)):
+        raise ValueError(f"unsupported kind {kind}")
+    return e.value, b.value
+
+
+def scale_min(scales12, index):
+    s = np.ascontiguousarray(scales12, np.uint8)
+    a, b = C.c_uint8(), C.c_uint8()
+    lib().so_scale_min(_p(s), index, C.byref(a), C.byref(b))
+    return a.value, b.value
+
+
+def decode_block(kind: int, block_bytes) -> np.ndarray:
+    e, _ = block_layout(kind)
+    b = np.ascontiguousarray(block_bytes, np.uint8)
+    out = np.zeros(e, np.float32)
+    st = lib().so_decode_block(kind, _p(b), b.size, _p(out), e)
+    if st:
+        raise ValueError("invalid quantization block size")
+    return out
+
+
+def decode_rows(kind: int, data, rows: int, cols: int) -> np.ndarray:
+    e, bb = block_layout(kind)
+    data = np.ascontiguousarray(data, np.uint8).reshape(rows, cols // e * bb)
+    out = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        for b in range(cols // e):
+            out[r, b * e:(b + 1) * e] = decode_block(kind, data[r, b * bb:(b + 1) * bb])
+    return out
+
+
+def hybrid_packed_matvec(kind, data, rows, cols, x) -> np.ndarray:
+    data = np.ascontiguousarray(data, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(rows, np.float32)
+    st = lib().so_hybrid_packed_matvec(kind, _p(data), rows, cols, _p(x), _p(out))
+    if st:
+        raise ValueError(f"status {st}")
+    return out
+
+
+def hybrid_affine_matvec(codes, scales, biases, scale_dt, bits, group, rows, cols, x) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, np.uint8)
+    scales = np.ascontiguousarray(scales)
+    biases = np.ascontiguousarray(biases)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(rows, np.float32)
+    st = lib().so_hybrid_affine_matvec(_p(codes), _p(scales), _p(biases), scale_dt, bits, group, rows, cols,
+                                       _p(x), _p(out))
+    if st:
+        raise ValueError(f"status {st}")
+    return out
+
+
+# ----------------------------------------------------------------- MoE
+
+def moe_route(logits, rows, experts, active, round_weights=False, round_logits=False):
+    logits = np.ascontiguousarray(logits, np.float32)
+    ids = np.zeros(rows * active, np.uint32)
+    w = np.zeros(rows * active, np.float32)
+    lib().so_moe_route(_p(logits), _p(ids), _p(w), rows, experts, active, int(round_weights), int(round_logits))
+    return ids, w
+
+
+def moe_gather_rows(ids, route_offset, rows_per_expert, experts, length):
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = np.zeros(length, np.uint32)
+    lib().so_moe_gather_rows(_p(ids), _p(out), route_offset, rows_per_expert, experts, length)
+    return out
+
+
+def moe_accumulate(input_bits, weights, accumulator, output, length, weight_offset, output_offset, initialize,
+                   finalize, round_product, round_accumulator):
+    """In-place on accumulator (float32) and output (uint16 bf16 bits)."""
+    lib().so_moe_accumulate(_p(np.ascontiguousarray(input_bits, np.uint16)),
+                            _p(np.ascontiguousarray(weights, np.float32)), _p(accumulator), _p(output), length,
+                            weight_offset, output_offset, int(initialize), int(finalize), int(round_product),
+                            int(round_accumulator))
+
+
+def moe_adjust_routes(ids, weights, scales, rows, experts, active, sort_ids):
+    """In-place on ids (uint32) and weights (float32)."""
+    lib().so_moe_adjust_routes(_p(ids), _p(weights), _p(np.ascontiguousarray(scales, np.float32)), rows, experts,
+                               active, int(sort_ids))
+
+
+def gated_silu_bf16(projected_bits, hidden, batch):
+    p = np.ascontiguousarray(projected_bits, np.uint16)
+    out = np.zeros(batch * hidden, np.uint16)
+    lib().so_gated_silu_bf16(_p(p), _p(out), hidden, batch)
+    return out
+
+
+# ----------------------------------------------------------------- generators
+
+def quantize_affine(w, bits=4, group=64, layout=OUTPUT_GROUP):
+    """Returns (codes u8 [rows, cols*bits/8], scales bf16 bits, biases bf16 bits)."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    G = cols // group
+    codes = np.zeros((rows, cols * bits // 8), np.uint8)
+    if layout == OUTPUT_GROUP:
+        shape = (rows, G)
+    else:
+        shape = (G, (rows + 3) // 4 * 4)
+    scales = np.zeros(shape, np.uint16)
+    biases = np.zeros(shape, np.uint16)
+    lib().so_quantize_affine(_p(w), rows, cols, bits, group, layout, _p(codes), _p(scales), _p(biases))
+    return codes, scales, biases
+
+
+def quantize_q8_0(w):
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    out = np.zeros((rows, cols // 32 * 34), np.uint8)
+    lib().so_quantize_q8_0(_p(w), rows, cols, _p(out))
+    return out
+
+
+def quantize_q4_k(w):
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    out = np.zeros((rows, cols // 256 * 144), np.uint8)
+    lib().so_quantize_q4_k(_p(w), rows, cols, _p(out))
+    return out

@@ -1,0 +1,124 @@
+/*
+ * stark_oracle.h -- CPU restatement of the reference's quantized-matmul semantics.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP path
+ * and the CPU baseline timed by bench.py. Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load it. The product library
+ * (stark_amd/libstark_qmm.so) never links or calls it.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * the reference repository root). Compiled with -ffp-contract=off so that each
+ * `a * b + c` rounds twice, as Rust does (Rust never contracts to FMA unless
+ * `mul_add` is written, and the restated code marks those places).
+ */
+#ifndef STARK_ORACLE_H
+#define STARK_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype ids follow the GGUF kind numbers the hybrid engine uses for planes. */
+enum { SO_F32 = 0, SO_F16 = 1, SO_BF16 = 30 };
+enum { SO_LAYOUT_OUTPUT_GROUP = 0, SO_LAYOUT_GROUP_OUTPUT = 1 };
+enum { SO_CORR_SYMMETRIC = 0, SO_CORR_BIASES = 1, SO_CORR_ZERO_POINTS = 2 };
+
+/* half 2.7.1 conversions (Cargo.lock:897-899). */
+float so_bf16_to_f32(uint16_t h);
+uint16_t so_f32_to_bf16(float f);
+float so_f16_to_f32(uint16_t h);
+uint16_t so_f32_to_f16(float f);
+void so_f32_to_bf16_n(const float* src, uint16_t* dst, size_t n);
+void so_bf16_to_f32_n(const uint16_t* src, float* dst, size_t n);
+void so_f32_to_f16_n(const float* src, uint16_t* dst, size_t n);
+void so_f16_to_f32_n(const uint16_t* src, float* dst, size_t n);
+
+/* backends/cpu/kernel/matmul/reference.rs:91-104 */
+uint8_t so_packed_code(const uint8_t* codes, int bits, size_t index);
+
+/* Plane strides derived as backends/common/kernel/matmul/mod.rs:109-156 does. */
+void so_quant_strides(int layout, uint32_t row_count, uint32_t group_count, uint32_t packing_divisor,
+                      uint32_t* output_stride, uint32_t* group_stride);
+
+typedef struct so_matmul_args {
+    /* A: FullPrecision values (+offset elements) in input_dt */
+    const void* a;
+    size_t a_offset;
+    /* B: full precision when codes == NULL (values in weights_dt, row-major
+     * [n, ld] if b_transpose else [k, ld]; ld 0 selects k or n) */
+    const void* b_values;
+    uint32_t b_leading_dimension;
+    /* B: quantized */
+    const uint8_t* codes;
+    size_t codes_size;
+    const void* scales;      /* weights_dt */
+    int correction;          /* SO_CORR_* */
+    const void* correction_data; /* biases (weights_dt) or zero points (packed u8) */
+    int layout;
+    uint32_t row_count, group_count;
+    int materialize_affine_input_sum;
+    int bits;
+    uint32_t group_size;
+    int signed_codes;
+    int b_transpose;
+    /* D */
+    void* d;
+    float ab_scale;
+    int accumulate;
+    const void* bias;        /* weights_dt, indexed by output column */
+    int has_soft_cap;
+    float soft_cap;
+    const uint32_t* gather_indices; /* [m*n] or NULL */
+    uint32_t m, n, k;
+    int weights_dt, input_dt, output_dt;
+} so_matmul_args;
+
+/* Status: 0 ok, 1 unsupported layout (undersized codes / policy), 2 unsupported dtype. */
+int so_matmul(const so_matmul_args* args);
+/* Row-parallel variant (OpenMP over output columns); identical arithmetic per output. */
+int so_matmul_parallel(const so_matmul_args* args, int threads);
+
+/* backends/cpu/kernel/matmul/vision.rs:249-336 (BF16-effective reference dot). */
+void so_reference_affine_linear_bf16(const uint16_t* input, const uint8_t* weights, const uint16_t* scales,
+                                     const uint16_t* biases, const uint32_t* indices, uint16_t* bf16_output,
+                                     float* f32_output, uint32_t m, uint32_t n, uint32_t k, uint32_t bank_rows,
+                                     uint32_t bits, uint32_t scale_output_stride, uint32_t scale_group_stride);
+
+/* engine/hybrid/weights.rs:2565-2584, 2908-2921, 2923-3012 (kinds 0,1,30,8,12,13). */
+int so_block_layout(uint32_t kind, size_t* elements, size_t* bytes);
+void so_scale_min(const uint8_t* scales, int index, uint8_t* scale, uint8_t* min);
+int so_decode_block(uint32_t kind, const uint8_t* bytes, size_t nbytes, float* output, size_t count);
+/* weights.rs:2533-2550: per row decode_values(...) . input, f32 sequential sum. */
+int so_hybrid_packed_matvec(uint32_t kind, const uint8_t* bytes, size_t rows, size_t columns, const float* input,
+                            float* output);
+/* weights.rs:1284-1309 affine_row . input (OutputGroup [N,G] planes). */
+int so_hybrid_affine_matvec(const uint8_t* codes, const void* scales, const void* biases, int scale_dt, int bits,
+                            size_t group, size_t rows, size_t columns, const float* input, float* output);
+
+/* backends/cpu/kernel/moe.rs */
+void so_moe_route(const float* logits, uint32_t* ids, float* weights, uint32_t rows, uint32_t experts,
+                  uint32_t active, uint32_t round_weights, uint32_t round_logits);
+void so_moe_gather_rows(const uint32_t* ids, uint32_t* indices, uint32_t route_offset, uint32_t rows_per_expert,
+                        uint32_t experts, uint32_t length);
+void so_moe_accumulate(const uint16_t* input, const float* weights, float* accumulator, uint16_t* output,
+                       uint32_t length, uint32_t weight_offset, uint32_t output_offset, uint32_t initialize,
+                       uint32_t finalize, uint32_t round_product, uint32_t round_accumulator);
+void so_moe_adjust_routes(uint32_t* ids, float* weights, const float* scales, uint32_t rows, uint32_t experts,
+                          uint32_t active, uint32_t sort_ids);
+/* backends/cpu/kernel/gated_act_mul/gated_act_mul.rs (interleaved, SiLU, bf16):
+ * row layout [value(hidden) | gate(hidden)], out = bf16(value * bf16(silu(gate))). */
+void so_gated_silu_bf16(const uint16_t* projected, uint16_t* out, uint32_t hidden, uint32_t batch);
+
+/* Test-input generators (not part of the parity contract: parity is defined on decode). */
+void so_quantize_affine(const float* w, size_t rows, size_t cols, int bits, size_t group, int layout,
+                        uint8_t* codes, uint16_t* scales, uint16_t* biases);
+void so_quantize_q8_0(const float* w, size_t rows, size_t cols, uint8_t* out);
+void so_quantize_q4_k(const float* w, size_t rows, size_t cols, uint8_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,236 @@
+// C ABI of the quantized matrix-product path (include/stark_qmm.h).
+//
+// Argument validation mirrors the reference so that a caller sees the same
+// error for the same bad input:
+// * MatmulCpuKernel::new dtype check (crates/stark-engine/src/backends/cpu/kernel/matmul/kernel.rs:37-41)
+// * validate_affine_input_sum_policy (crates/stark-engine/src/backends/common/kernel/matmul/arguments.rs:36-61)
+// * WeightData::from_b codes-size check (crates/stark-engine/src/backends/cpu/kernel/matmul/reference.rs:62-71)
+// * MappedOperation::parameters_for_input (crates/stark-engine/src/engine/hybrid/weight_metal.rs:442-537)
+#include <new>
+#include <vector>
+
+#include "qmm_common.h"
+
+struct stark_qmm_kernel {
+    uint32_t w_dt, x_dt, d_dt;
+    uint32_t reference_accumulation;
+};
+
+namespace {
+
+using namespace qmm;
+
+bool dtype_ok(uint32_t dt) { return dt == STARK_QMM_F32 || dt == STARK_QMM_F16 || dt == STARK_QMM_BF16; }
+
+int mode_bits(uint32_t mode) {
+    switch (mode) {
+    case STARK_QMM_MODE_U4: return 4;
+    case STARK_QMM_MODE_I8:
+    case STARK_QMM_MODE_U8: return 8;
+    case STARK_QMM_MODE_U5: return 5;
+    case STARK_QMM_MODE_U6: return 6;
+    case STARK_QMM_MODE_U3: return 3;
+    default: return -1;
+    }
+}
+
+// QuantParams::strides (crates/stark-engine/src/backends/common/kernel/matmul/mod.rs:131-156).
+void quant_strides(uint32_t layout, uint32_t rows, uint32_t groups, uint32_t pd, uint32_t* os, uint32_t* gs) {
+    if (layout == STARK_QMM_LAYOUT_OUTPUT_GROUP) {
+        *os = (groups + pd - 1) / pd * pd;
+        *gs = 1;
+    } else {
+        *os = 1;
+        *gs = (rows + 3u) / 4u * 4u;
+    }
+}
+
+stark_qmm_status build_affine_op(const stark_qmm_kernel* kr, const stark_qmm_b& b, uint32_t m, uint32_t n, uint32_t k,
+                                 const void* x, void* d, const stark_qmm_d_ops& dops, const uint32_t* gather,
+                                 AffineOp* op, int* bits_out) {
+    const int bits = mode_bits(b.mode);
+    if (bits < 0) return STARK_QMM_INVALID_ARGUMENT;
+    if (b.group_size == 0) return STARK_QMM_UNSUPPORTED_GROUP_SIZE;
+    if (b.params.layout > STARK_QMM_LAYOUT_GROUP_OUTPUT || b.correction > STARK_QMM_CORRECTION_ZERO_POINTS)
+        return STARK_QMM_INVALID_ARGUMENT;
+    // reference.rs:62-71: n*k*bits/8 (rounded up) bytes must be present
+    const unsigned __int128 need = ((unsigned __int128)n * k * (unsigned)bits + 7) / 8;
+    if (need > b.codes_size) return STARK_QMM_UNSUPPORTED_LAYOUT;
+    if (!b.scales) return STARK_QMM_INVALID_ARGUMENT;
+    if (b.correction != STARK_QMM_CORRECTION_SYMMETRIC && !b.correction_data) return STARK_QMM_INVALID_ARGUMENT;
+    if (b.correction == STARK_QMM_CORRECTION_ZERO_POINTS && 8 % bits) return STARK_QMM_UNSUPPORTED_LAYOUT;
+    AffineOp o{};
+    o.codes = (const uint8_t*)b.codes;
+    o.scales = b.scales;
+    o.corr = b.correction_data;
+    o.x = x;
+    o.d = d;
+    o.bias = dops.bias;
+    o.gather = gather;
+    o.n = n;
+    o.k = k;
+    o.m = m;
+    quant_strides(b.params.layout, b.params.row_count, b.params.group_count, 1, &o.os, &o.gs);
+    if (b.correction == STARK_QMM_CORRECTION_ZERO_POINTS)
+        quant_strides(b.params.layout, b.params.row_count, b.params.group_count, 8u / bits, &o.zos, &o.zgs);
+    o.group_size = b.group_size;
+    o.corr_kind = b.correction;
+    o.w_dt = kr->w_dt;
+    o.x_dt = kr->x_dt;
+    o.d_dt = kr->d_dt;
+    o.flags = (dops.accumulate ? FLAG_ACCUMULATE : 0u) | (dops.has_soft_cap ? FLAG_SOFT_CAP : 0u) |
+              (b.signed_codes ? FLAG_SIGNED : 0u);
+    o.ab_scale = dops.ab_scale;
+    o.soft_cap = dops.soft_cap;
+    const uint64_t rowbits = (uint64_t)k * (uint64_t)bits;
+    o.bank_rows = k == 0 ? n : (uint32_t)std::min<uint64_t>(0xffffffffull, b.codes_size * 8ull / rowbits);
+    *op = o;
+    *bits_out = bits;
+    return STARK_QMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t stark_qmm_abi_version(void) { return STARK_QMM_ABI_VERSION; }
+
+const char* stark_qmm_status_string(stark_qmm_status s) {
+    switch (s) {
+    case STARK_QMM_OK: return "ok";
+    case STARK_QMM_INVALID_ARGUMENT: return "invalid argument";
+    case STARK_QMM_ABI_MISMATCH: return "ABI mismatch";
+    case STARK_QMM_UNSUPPORTED_DATA_TYPE: return "unsupported data type";
+    case STARK_QMM_UNSUPPORTED_GROUP_SIZE: return "unsupported group size";
+    case STARK_QMM_UNSUPPORTED_D_OP: return "unsupported D-transform op";
+    case STARK_QMM_UNSUPPORTED_LAYOUT: return "unsupported B layout";
+    case STARK_QMM_INCOMPATIBLE_A: return "incompatible A operand";
+    case STARK_QMM_UNSUPPORTED: return "unsupported";
+    case STARK_QMM_OUT_OF_MEMORY: return "out of memory";
+    case STARK_QMM_DEVICE_FAILURE: return "device failure";
+    case STARK_QMM_WORKSPACE_TOO_SMALL: return "workspace too small";
+    default: return "unknown status";
+    }
+}
+
+stark_qmm_status stark_qmm_create(uint32_t w_dt, uint32_t x_dt, uint32_t d_dt, stark_qmm_kernel** out) {
+    if (!out) return STARK_QMM_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (!dtype_ok(w_dt) || !dtype_ok(x_dt) || !dtype_ok(d_dt)) return STARK_QMM_UNSUPPORTED_DATA_TYPE;
+    stark_qmm_kernel* k = new (std::nothrow) stark_qmm_kernel{w_dt, x_dt, d_dt, 0};
+    if (!k) return STARK_QMM_OUT_OF_MEMORY;
+    *out = k;
+    return STARK_QMM_OK;
+}
+
+void stark_qmm_destroy(stark_qmm_kernel* k) { delete k; }
+
+stark_qmm_status stark_qmm_set_reference_accumulation(stark_qmm_kernel* k, uint32_t enabled) {
+    if (!k) return STARK_QMM_INVALID_ARGUMENT;
+    k->reference_accumulation = enabled ? 1u : 0u;
+    return STARK_QMM_OK;
+}
+
+stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kr, const stark_qmm_args* args, void* stream_ptr) {
+    if (!kr || !args) return STARK_QMM_INVALID_ARGUMENT;
+    if (args->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
+    hipStream_t stream = (hipStream_t)stream_ptr;
+    const stark_qmm_b& b = args->b;
+    const stark_qmm_d_ops& dops = args->d_ops;
+    if (dops.rht_factors) return STARK_QMM_UNSUPPORTED_D_OP;
+    const uint32_t m = args->m, n = args->n, k = args->k;
+    const size_t xsz = kr->x_dt == STARK_QMM_F32 ? 4 : 2;
+    const void* x = args->a ? (const uint8_t*)args->a + args->a_offset * xsz : nullptr;
+
+    if (!b.codes) {
+        // MatmulB::FullPrecision
+        if (b.params.materialize_affine_input_sum) return STARK_QMM_UNSUPPORTED_LAYOUT;
+        if (!b.values || (!x && m && n && k) || (!args->d && m && n)) return STARK_QMM_INVALID_ARGUMENT;
+        DenseOp o{};
+        o.w = b.values;
+        o.x = x;
+        o.d = args->d;
+        o.bias = dops.bias;
+        o.gather = args->gather_indices;
+        o.n = n;
+        o.k = k;
+        o.m = m;
+        o.transpose = args->b_transpose ? 1u : 0u;
+        o.ld = args->b_leading_dimension ? args->b_leading_dimension : (args->b_transpose ? k : n);
+        o.w_dt = kr->w_dt;
+        o.x_dt = kr->x_dt;
+        o.d_dt = kr->d_dt;
+        o.flags = (dops.accumulate ? FLAG_ACCUMULATE : 0u) | (dops.has_soft_cap ? FLAG_SOFT_CAP : 0u);
+        o.ab_scale = dops.ab_scale;
+        o.soft_cap = dops.soft_cap;
+        o.bank_rows = 0xffffffffu;
+        return launch_dense_gemv(o, stream);
+    }
+
+    // validate_affine_input_sum_policy (arguments.rs:36-61)
+    const bool materialize = b.params.materialize_affine_input_sum != 0;
+    if (materialize) {
+        const uint32_t gs = b.group_size;
+        if (kr->w_dt != STARK_QMM_BF16 || kr->x_dt != STARK_QMM_BF16 || kr->d_dt != STARK_QMM_BF16 ||
+            b.mode != STARK_QMM_MODE_U4 || b.correction != STARK_QMM_CORRECTION_BIASES || b.signed_codes ||
+            !args->b_transpose || !(gs == 16 || gs == 32 || gs == 64 || gs == 128) || (k % 4) != 0)
+            return STARK_QMM_UNSUPPORTED_LAYOUT;
+    }
+    AffineOp op;
+    int bits;
+    stark_qmm_status st = build_affine_op(kr, b, m, n, k, x, args->d, dops, args->gather_indices, &op, &bits);
+    if (st != STARK_QMM_OK) return st;
+    if (m == 0 || n == 0) return STARK_QMM_OK;
+    if (!args->d || (!x && k)) return STARK_QMM_INVALID_ARGUMENT;
+    if (materialize && m == 1) return launch_affine_materialized(op, stream);
+    if (affine_fast_eligible(op, bits)) return launch_affine_gemv(&op, 1, bits, stream);
+    return launch_affine_generic(op, bits, stream);
+}
+
+stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_args* args, uint32_t count,
+                                       void* stream_ptr) {
+    if (!kr || (!args && count)) return STARK_QMM_INVALID_ARGUMENT;
+    hipStream_t stream = (hipStream_t)stream_ptr;
+    std::vector<AffineOp> fast4, fast8;
+    std::vector<size_t> rest;
+    const size_t xsz = kr->x_dt == STARK_QMM_F32 ? 4 : 2;
+    for (uint32_t i = 0; i < count; ++i) {
+        const stark_qmm_args* a = &args[i];
+        if (a->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
+        if (a->d_ops.rht_factors) return STARK_QMM_UNSUPPORTED_D_OP;
+        if (!a->b.codes || a->b.params.materialize_affine_input_sum || a->m == 0 || a->n == 0) {
+            rest.push_back(i);
+            continue;
+        }
+        const void* x = a->a ? (const uint8_t*)a->a + a->a_offset * xsz : nullptr;
+        AffineOp op;
+        int bits;
+        stark_qmm_status st = build_affine_op(kr, a->b, a->m, a->n, a->k, x, a->d, a->d_ops, a->gather_indices, &op, &bits);
+        if (st != STARK_QMM_OK) return st;
+        if (!a->d || (!x && a->k)) return STARK_QMM_INVALID_ARGUMENT;
+        if (!affine_fast_eligible(op, bits) || op.gather) {
+            rest.push_back(i);
+        } else if (bits == 4) {
+            fast4.push_back(op);
+        } else {
+            fast8.push_back(op);
+        }
+    }
+    // Group by M class so one launch never mixes one- and two-row kernels.
+    for (auto* v : {&fast4, &fast8}) {
+        const int bits = v == &fast4 ? 4 : 8;
+        std::vector<AffineOp> one, many;
+        for (const AffineOp& o : *v) (o.m == 1 ? one : many).push_back(o);
+        stark_qmm_status st = launch_affine_gemv(one.data(), (uint32_t)one.size(), bits, stream);
+        if (st != STARK_QMM_OK) return st;
+        st = launch_affine_gemv(many.data(), (uint32_t)many.size(), bits, stream);
+        if (st != STARK_QMM_OK) return st;
+    }
+    for (size_t i : rest) {
+        stark_qmm_status st = stark_qmm_encode(kr, &args[i], stream_ptr);
+        if (st != STARK_QMM_OK) return st;
+    }
+    return STARK_QMM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,156 @@
+// Shared device/host helpers for the gfx950 quantized matrix-product kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/stark_qmm.h"
+
+#define QMM_DEVICE __device__ __forceinline__
+
+namespace qmm {
+
+// ---------------------------------------------------------------- numerics
+
+QMM_DEVICE float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// f32 -> bf16 round-to-nearest-even with quiet-NaN forcing; the same rule the
+// reference's `half` crate applies when writing bf16 outputs.
+QMM_DEVICE uint16_t f32_to_bf16_bits(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+    uint32_t lsb = (x >> 16) & 1u;
+    return (uint16_t)((x + 0x7fffu + lsb) >> 16);
+}
+
+QMM_DEVICE float f16_bits_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// v_cvt_f16_f32: round-to-nearest-even, overflow to infinity.
+QMM_DEVICE uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Load element `i` of a dtype-tagged array as f32.
+QMM_DEVICE float load_as_f32(const void* p, uint32_t dt, size_t i) {
+    if (dt == STARK_QMM_F32) return ((const float*)p)[i];
+    uint32_t h = ((const uint16_t*)p)[i];
+    return dt == STARK_QMM_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+QMM_DEVICE void store_from_f32(void* p, uint32_t dt, size_t i, float v) {
+    if (dt == STARK_QMM_F32) {
+        ((float*)p)[i] = v;
+    } else if (dt == STARK_QMM_BF16) {
+        ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+    } else {
+        ((uint16_t*)p)[i] = f32_to_f16_bits(v);
+    }
+}
+
+// Full 64-lane sum; every lane receives the total.
+QMM_DEVICE float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load of weight codes that are read exactly once per launch.
+QMM_DEVICE u32x4 load_stream(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+
+// D = a.lo*b.lo + a.hi*b.hi + c (products exact for bf16, f32 accumulate).
+QMM_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                           false);
+}
+
+}  // namespace qmm
+
+// ------------------------------------------------------------------ host side
+
+#define QMM_HIP_CHECK(expr)                                   \
+    do {                                                      \
+        hipError_t qmm_err_ = (expr);                         \
+        if (qmm_err_ != hipSuccess) return STARK_QMM_DEVICE_FAILURE; \
+    } while (0)
+
+namespace qmm {
+
+// Epilogue and correction flags shared by the matvec kernels.
+enum : uint32_t {
+    FLAG_ACCUMULATE = 1u << 0,
+    FLAG_SOFT_CAP = 1u << 1,
+    FLAG_SIGNED = 1u << 2,
+};
+
+// One affine matrix product d[m, n] = sum_k a[m, k] * (s * q + bias_term).
+struct AffineOp {
+    const uint8_t* codes;    // [N, K*bits/8]
+    const void* scales;      // plane in w_dt
+    const void* corr;        // biases (w_dt) / zero points (u8) / NULL
+    const void* x;           // [M, K] in x_dt
+    void* d;                 // [M, N] in d_dt
+    const void* bias;        // [N] in w_dt or NULL
+    const uint32_t* gather;  // [M*N] or NULL
+    uint32_t n, k, m;
+    uint32_t os, gs;         // scale/bias plane strides (elements)
+    uint32_t zos, zgs;       // zero-point strides (nibbles for 4-bit, bytes for 8-bit)
+    uint32_t group_size;
+    uint32_t corr_kind;      // STARK_QMM_CORRECTION_*
+    uint32_t w_dt, x_dt, d_dt;
+    uint32_t flags;
+    float ab_scale, soft_cap;
+    uint32_t bank_rows;      // weight rows present in the codes buffer (gather bound)
+    uint32_t block_begin;    // first blockIdx.x of this op inside a batched launch
+};
+
+constexpr int kMaxBatchOps = 8;
+
+struct AffineBatch {
+    AffineOp op[kMaxBatchOps];
+    uint32_t count;
+};
+
+// Launch helpers implemented in qmv_affine.hip.
+stark_qmm_status launch_affine_gemv(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream);
+stark_qmm_status launch_affine_generic(const AffineOp& op, int bits, hipStream_t stream);
+bool affine_fast_eligible(const AffineOp& op, int bits);
+stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stream);
+// Full-precision B operand (MatmulB::FullPrecision).
+struct DenseOp {
+    const void* w;           // [N, ld] (transpose) or [K, ld]
+    const void* x;           // [M, K]
+    void* d;                 // [M, N]
+    const void* bias;
+    const uint32_t* gather;
+    uint32_t n, k, m, ld, transpose;
+    uint32_t w_dt, x_dt, d_dt, flags;
+    float ab_scale, soft_cap;
+    uint32_t bank_rows;
+};
+stark_qmm_status launch_dense_gemv(const DenseOp& op, hipStream_t stream);
+
+// GGUF packed-block matvec (kinds 8 = Q8_0, 12 = Q4_K).
+struct GgufOp {
+    const uint8_t* blocks;   // [N, K/block * block_bytes]
+    uint32_t kind;
+    const void* x;           // [M, K] in x_dt (f32 on the hybrid path)
+    void* d;                 // [M, N] in d_dt
+    uint32_t n, k, m;
+    uint32_t x_dt, d_dt;     // 0/0 means f32/f32
+    uint32_t block_begin;
+};
+struct GgufBatch {
+    GgufOp op[kMaxBatchOps];
+    uint32_t count;
+};
+bool gguf_supported(uint32_t kind);
+stark_qmm_status launch_gguf_gemv(const GgufOp* ops, uint32_t count, hipStream_t stream);
+
+// Largest M the GEMV kernel handles in one weight pass.
+constexpr uint32_t kGemvMaxM = 2;
+
+}  // namespace qmm

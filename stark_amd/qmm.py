@@ -1,0 +1,431 @@
+"""Python mirror of the reference's quantized-matmul operator API over the C ABI.
+
+The classes keep the reference's names and argument meaning:
+
+* ``MatmulKernel`` -- trait MatmulKernel
+  (crates/stark-engine/src/backends/common/kernel/matmul/kernel.rs:15-79)
+* ``MatmulArguments`` / ``QuantizedB`` / ``QuantParams`` / ``MatmulDOps`` --
+  crates/stark-engine/src/backends/common/kernel/matmul/{arguments.rs:7-25,
+  matmul_b.rs:6-29, mod.rs:19-41, d_ops.rs:3-9}
+* ``MatmulError`` -- crates/stark-engine/src/backends/common/kernel/matmul/error.rs:10-31
+* ``mapped_many`` -- crates/stark-engine/src/engine/hybrid/weight_metal.rs:539-545
+* ``moe_*`` -- crates/stark-engine/src/backends/cpu/kernel/moe.rs
+
+Tensors are torch tensors on the GPU (torch is used only for device memory
+and the current stream); every call goes through libstark_qmm.so. There is no
+CPU fallback: if the library cannot be loaded the import fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libstark_qmm.so")
+
+# ---------------------------------------------------------------- constants
+
+OK = 0
+INVALID_ARGUMENT = 1
+ABI_MISMATCH = 2
+UNSUPPORTED_DATA_TYPE = 3
+UNSUPPORTED_GROUP_SIZE = 4
+UNSUPPORTED_D_OP = 5
+UNSUPPORTED_LAYOUT = 6
+INCOMPATIBLE_A = 7
+UNSUPPORTED = 8
+OUT_OF_MEMORY = 9
+DEVICE_FAILURE = 10
+WORKSPACE_TOO_SMALL = 11
+
+F32, F16, BF16 = 0, 1, 30
+OUTPUT_GROUP, GROUP_OUTPUT = 0, 1
+SYMMETRIC, BIASES, ZERO_POINTS = 0, 1, 2
+MODE_U4, MODE_I8, MODE_U8, MODE_U5, MODE_U6, MODE_U3 = 0, 1, 2, 3, 4, 5
+KIND_Q8_0, KIND_Q4_K = 8, 12
+FORMAT_PACKED, FORMAT_AFFINE = 0, 1
+
+_TORCH_DT = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}
+
+
+class MatmulError(RuntimeError):
+    def __init__(self, status: int, where: str = ""):
+        self.status = status
+        super().__init__(f"{where}: {status_string(status)} ({status})")
+
+
+# ---------------------------------------------------------------- ctypes ABI
+
+class _QuantParams(C.Structure):
+    _fields_ = [("layout", C.c_uint32), ("row_count", C.c_uint32), ("group_count", C.c_uint32),
+                ("materialize_affine_input_sum", C.c_uint32)]
+
+
+class _B(C.Structure):
+    _fields_ = [("values", C.c_void_p), ("codes", C.c_void_p), ("codes_size", C.c_uint64),
+                ("scales", C.c_void_p), ("correction", C.c_uint32), ("correction_data", C.c_void_p),
+                ("params", _QuantParams), ("mode", C.c_uint32), ("group_size", C.c_uint32),
+                ("signed_codes", C.c_uint32)]
+
+
+class _DOps(C.Structure):
+    _fields_ = [("ab_scale", C.c_float), ("accumulate", C.c_uint32), ("bias", C.c_void_p),
+                ("rht_factors", C.c_void_p), ("has_soft_cap", C.c_uint32), ("soft_cap", C.c_float)]
+
+
+class _Args(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("a", C.c_void_p), ("a_offset", C.c_uint64), ("b", _B),
+                ("b_leading_dimension", C.c_uint32), ("b_transpose", C.c_uint32), ("d", C.c_void_p),
+                ("d_ops", _DOps), ("gather_indices", C.c_void_p), ("m", C.c_uint32), ("n", C.c_uint32),
+                ("k", C.c_uint32)]
+
+
+class _MappedMatrix(C.Structure):
+    _fields_ = [("codes", C.c_void_p), ("codes_length", C.c_uint64), ("scales", C.c_void_p),
+                ("biases", C.c_void_p), ("plane_length", C.c_uint64)]
+
+
+class _MappedOp(C.Structure):
+    _fields_ = [("matrices", C.POINTER(_MappedMatrix)), ("matrix_count", C.c_uint32), ("inputs", C.c_void_p),
+                ("input_length", C.c_uint64), ("rows", C.c_uint64), ("columns", C.c_uint64),
+                ("rows_per_batch", C.c_uint64), ("format", C.c_uint32), ("packed_kind", C.c_uint32),
+                ("scale_dtype", C.c_uint32), ("bits", C.c_uint32), ("group", C.c_uint32)]
+
+
+class _RoutedArgs(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("input", C.c_void_p), ("router_logits", C.c_void_p),
+                ("expert_scales", C.c_void_p), ("up", _B), ("down", _B), ("output", C.c_void_p),
+                ("rows", C.c_uint32), ("model", C.c_uint32), ("hidden", C.c_uint32), ("experts", C.c_uint32),
+                ("active", C.c_uint32), ("round_logits_bf16", C.c_uint32), ("round_weights_bf16", C.c_uint32),
+                ("round_products_bf16", C.c_uint32), ("round_accumulator_bf16", C.c_uint32),
+                ("sort_expert_ids", C.c_uint32), ("workspace", C.c_void_p), ("workspace_size", C.c_uint64)]
+
+
+# Every symbol include/stark_qmm.h declares, with its ctypes signature.
+SIGNATURES = {
+    "stark_qmm_abi_version": (C.c_uint32, []),
+    "stark_qmm_status_string": (C.c_char_p, [C.c_uint32]),
+    "stark_qmm_create": (C.c_uint32, [C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_void_p)]),
+    "stark_qmm_encode": (C.c_uint32, [C.c_void_p, C.POINTER(_Args), C.c_void_p]),
+    "stark_qmm_encode_many": (C.c_uint32, [C.c_void_p, C.POINTER(_Args), C.c_uint32, C.c_void_p]),
+    "stark_qmm_set_reference_accumulation": (C.c_uint32, [C.c_void_p, C.c_uint32]),
+    "stark_qmm_destroy": (None, [C.c_void_p]),
+    "stark_qmm_mapped_many": (C.c_uint32, [C.POINTER(_MappedOp), C.c_uint32, C.POINTER(C.c_void_p), C.c_void_p]),
+    "stark_qmm_mapped_many_async": (C.c_uint32, [C.POINTER(_MappedOp), C.c_uint32, C.POINTER(C.c_void_p),
+                                                 C.c_void_p, C.c_void_p]),
+    "stark_qmm_moe_route": (C.c_uint32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,
+                                         C.c_uint32, C.c_uint32, C.c_void_p]),
+    "stark_qmm_moe_adjust_routes": (C.c_uint32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
+                                                 C.c_uint32, C.c_uint32, C.c_void_p]),
+    "stark_qmm_moe_gather_rows": (C.c_uint32, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,
+                                               C.c_uint32, C.c_void_p]),
+    "stark_qmm_moe_accumulate": (C.c_uint32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32,
+                                              C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                              C.c_uint32, C.c_void_p]),
+    "stark_qmm_routed_experts_workspace_size": (C.c_uint64, [C.c_uint32] * 5),
+    "stark_qmm_routed_experts": (C.c_uint32, [C.POINTER(_RoutedArgs), C.c_void_p]),
+}
+
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def lib():
+    """Load libstark_qmm.so, building it first if it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            from . import build as _build
+            _build.build()
+        l = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        if l.stark_qmm_abi_version() != 1:
+            raise RuntimeError("libstark_qmm ABI mismatch")
+        _lib = l
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().stark_qmm_status_string(status).decode()
+
+
+def _check(status: int, where: str):
+    if status != OK:
+        raise MatmulError(status, where)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("stark_qmm operands must be GPU tensors")
+    return t.data_ptr()
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+# ---------------------------------------------------------------- operator API
+
+@dataclass
+class QuantParams:
+    layout: int
+    row_count: int
+    group_count: int
+    materialize_affine_input_sum: bool = False
+
+
+@dataclass
+class QuantizedB:
+    codes: torch.Tensor
+    scales: torch.Tensor
+    params: QuantParams
+    mode: int = MODE_U4
+    group_size: int = 64
+    correction: int = BIASES
+    correction_data: Optional[torch.Tensor] = None
+    signed_codes: bool = False
+
+
+@dataclass
+class FullPrecisionB:
+    values: torch.Tensor
+
+
+@dataclass
+class MatmulDOps:
+    ab_scale: float = 1.0
+    accumulate: bool = False
+    bias: Optional[torch.Tensor] = None
+    rht_factors: Optional[torch.Tensor] = None
+    soft_cap: Optional[float] = None
+
+
+@dataclass
+class MatmulArguments:
+    a: torch.Tensor
+    b: object  # QuantizedB | FullPrecisionB
+    d: torch.Tensor
+    m: int
+    n: int
+    k: int
+    a_offset: int = 0
+    b_leading_dimension: int = 0
+    b_transpose: bool = True
+    d_transform: MatmulDOps = field(default_factory=MatmulDOps)
+    gather_indices: Optional[torch.Tensor] = None
+
+
+def _fill_b(dst: _B, b) -> None:
+    if isinstance(b, FullPrecisionB):
+        dst.values = _ptr(b.values)
+        dst.codes = None
+        return
+    dst.codes = _ptr(b.codes)
+    dst.codes_size = _nbytes(b.codes)
+    dst.scales = _ptr(b.scales)
+    dst.correction = b.correction
+    dst.correction_data = _ptr(b.correction_data)
+    dst.params.layout = b.params.layout
+    dst.params.row_count = b.params.row_count
+    dst.params.group_count = b.params.group_count
+    dst.params.materialize_affine_input_sum = int(b.params.materialize_affine_input_sum)
+    dst.mode = b.mode
+    dst.group_size = b.group_size
+    dst.signed_codes = int(b.signed_codes)
+
+
+def _args(a: MatmulArguments) -> _Args:
+    s = _Args()
+    s.struct_size = C.sizeof(_Args)
+    s.a = _ptr(a.a)
+    s.a_offset = a.a_offset
+    _fill_b(s.b, a.b)
+    s.b_leading_dimension = a.b_leading_dimension
+    s.b_transpose = int(a.b_transpose)
+    s.d = _ptr(a.d)
+    t = a.d_transform
+    s.d_ops.ab_scale = t.ab_scale
+    s.d_ops.accumulate = int(t.accumulate)
+    s.d_ops.bias = _ptr(t.bias)
+    s.d_ops.rht_factors = _ptr(t.rht_factors)
+    s.d_ops.has_soft_cap = int(t.soft_cap is not None)
+    s.d_ops.soft_cap = 0.0 if t.soft_cap is None else t.soft_cap
+    s.gather_indices = _ptr(a.gather_indices)
+    s.m, s.n, s.k = a.m, a.n, a.k
+    return s
+
+
+class MatmulKernel:
+    """trait MatmulKernel (kernel.rs:15-79) over stark_qmm_create/encode."""
+
+    def __init__(self, weights_data_type: int, input_data_type: int, output_data_type: int):
+        h = C.c_void_p()
+        _check(lib().stark_qmm_create(weights_data_type, input_data_type, output_data_type, C.byref(h)),
+               "MatmulKernel::new")
+        self._h = h
+        self.weights_data_type = weights_data_type
+        self.input_data_type = input_data_type
+        self.output_data_type = output_data_type
+
+    def set_reference_accumulation(self, enabled: bool = True) -> None:
+        _check(lib().stark_qmm_set_reference_accumulation(self._h, int(enabled)), "set_reference_accumulation")
+
+    def encode(self, arguments: MatmulArguments, stream=None) -> None:
+        s = _args(arguments)
+        _check(lib().stark_qmm_encode(self._h, C.byref(s), _stream(stream)), "MatmulKernel::encode")
+
+    def encode_many(self, arguments: Sequence[MatmulArguments], stream=None) -> None:
+        arr = (_Args * len(arguments))(*[_args(a) for a in arguments])
+        _check(lib().stark_qmm_encode_many(self._h, arr, len(arguments), _stream(stream)), "encode_many")
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().stark_qmm_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- hybrid engine
+
+@dataclass
+class MappedMatrix:
+    codes: torch.Tensor
+    scales: Optional[torch.Tensor] = None
+    biases: Optional[torch.Tensor] = None
+
+
+@dataclass
+class MappedOperation:
+    """MappedOperation (weight_metal.rs:385-392); format is ("packed", kind) or
+    ("affine", scale_dtype, bits, group)."""
+    matrices: Sequence[MappedMatrix]
+    inputs: torch.Tensor
+    rows: int
+    columns: int
+    format: tuple
+    rows_per_batch: int = 0
+
+
+def _mapped_structs(operations):
+    ops = (_MappedOp * len(operations))()
+    keep = []
+    for i, op in enumerate(operations):
+        mats = (_MappedMatrix * len(op.matrices))()
+        for j, mm in enumerate(op.matrices):
+            mats[j].codes = _ptr(mm.codes)
+            mats[j].codes_length = _nbytes(mm.codes)
+            mats[j].scales = _ptr(mm.scales)
+            mats[j].biases = _ptr(mm.biases)
+            mats[j].plane_length = 0 if mm.scales is None else _nbytes(mm.scales)
+        keep.append(mats)
+        o = ops[i]
+        o.matrices = mats
+        o.matrix_count = len(op.matrices)
+        o.inputs = _ptr(op.inputs)
+        o.input_length = op.inputs.numel()
+        o.rows, o.columns, o.rows_per_batch = op.rows, op.columns, op.rows_per_batch
+        if op.format[0] == "packed":
+            o.format = FORMAT_PACKED
+            o.packed_kind = op.format[1]
+        else:
+            o.format = FORMAT_AFFINE
+            o.scale_dtype, o.bits, o.group = op.format[1], op.format[2], op.format[3]
+    return ops, keep
+
+
+def mapped_many(operations: Sequence[MappedOperation], stream=None) -> list:
+    """weight_metal::mapped_many: returns one f32 tensor per operation; raises
+    MatmulError(INVALID_ARGUMENT) for invalid shapes or non-finite inputs."""
+    ops, keep = _mapped_structs(operations)
+    outs = [torch.empty(len(op.matrices) * op.rows, dtype=torch.float32, device=op.inputs.device)
+            for op in operations]
+    ptrs = (C.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    _check(lib().stark_qmm_mapped_many(ops, len(operations), ptrs, _stream(stream)), "mapped_many")
+    del keep
+    return outs
+
+
+# ---------------------------------------------------------------- MoE
+
+def moe_route(logits: torch.Tensor, rows: int, experts: int, active: int, round_weights=False,
+              round_logits=False, stream=None):
+    ids = torch.empty(rows * active, dtype=torch.int32, device=logits.device)
+    w = torch.empty(rows * active, dtype=torch.float32, device=logits.device)
+    _check(lib().stark_qmm_moe_route(_ptr(logits), _ptr(ids), _ptr(w), rows, experts, active, int(round_weights),
+                                     int(round_logits), _stream(stream)), "moe_route")
+    return ids, w
+
+
+def moe_adjust_routes(ids, weights, scales, rows, experts, active, sort_ids, stream=None):
+    _check(lib().stark_qmm_moe_adjust_routes(_ptr(ids), _ptr(weights), _ptr(scales), rows, experts, active,
+                                             int(sort_ids), _stream(stream)), "moe_adjust_routes")
+
+
+def moe_gather_rows(ids, route_offset, rows_per_expert, experts, length, stream=None):
+    out = torch.empty(length, dtype=torch.int32, device=ids.device)
+    _check(lib().stark_qmm_moe_gather_rows(_ptr(ids), _ptr(out), route_offset, rows_per_expert, experts, length,
+                                           _stream(stream)), "moe_gather_rows")
+    return out
+
+
+def moe_accumulate(inp, weights, accumulator, output, length, weight_offset, output_offset, initialize, finalize,
+                   round_product, round_accumulator, stream=None):
+    _check(lib().stark_qmm_moe_accumulate(_ptr(inp), _ptr(weights), _ptr(accumulator), _ptr(output), length,
+                                          weight_offset, output_offset, int(initialize), int(finalize),
+                                          int(round_product), int(round_accumulator), _stream(stream)),
+           "moe_accumulate")
+
+
+def routed_experts_workspace_size(rows, model, hidden, experts, active) -> int:
+    return int(lib().stark_qmm_routed_experts_workspace_size(rows, model, hidden, experts, active))
+
+
+def routed_experts(input: torch.Tensor, router_logits: torch.Tensor, up: QuantizedB, down: QuantizedB, rows: int,
+                   model: int, hidden: int, experts: int, active: int, expert_scales=None, round_logits=False,
+                   round_weights=False, round_products=False, round_accumulator=False, sort_expert_ids=False,
+                   workspace: Optional[torch.Tensor] = None, output: Optional[torch.Tensor] = None, stream=None):
+    """RoutedExperts::encode_scaled (routed.rs:154-257) as one device pipeline."""
+    need = routed_experts_workspace_size(rows, model, hidden, experts, active)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=input.device)
+    if output is None:
+        output = torch.empty(rows * model, dtype=torch.bfloat16, device=input.device)
+    s = _RoutedArgs()
+    s.struct_size = C.sizeof(_RoutedArgs)
+    s.input = _ptr(input)
+    s.router_logits = _ptr(router_logits)
+    s.expert_scales = _ptr(expert_scales)
+    _fill_b(s.up, up)
+    _fill_b(s.down, down)
+    s.output = _ptr(output)
+    s.rows, s.model, s.hidden, s.experts, s.active = rows, model, hidden, experts, active
+    s.round_logits_bf16, s.round_weights_bf16 = int(round_logits), int(round_weights)
+    s.round_products_bf16, s.round_accumulator_bf16 = int(round_products), int(round_accumulator)
+    s.sort_expert_ids = int(sort_expert_ids)
+    s.workspace = _ptr(workspace)
+    s.workspace_size = _nbytes(workspace)
+    _check(lib().stark_qmm_routed_experts(C.byref(s), _stream(stream)), "routed_experts")
+    return output

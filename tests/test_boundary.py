@@ -1,0 +1,146 @@
+"""The C-ABI library loads here (no GPU) and exports every symbol that
+include/stark_qmm.h declares; argument validation that needs no device runs
+on the CPU. No compute call is made."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "stark_qmm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(stark_qmm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("stark_qmm_create", "stark_qmm_encode", "stark_qmm_mapped_many", "stark_qmm_moe_route",
+              "stark_qmm_routed_experts"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from stark_amd import qmm
+    lib = qmm.lib()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    assert set(declared_symbols()) == set(qmm.SIGNATURES), "python mirror out of sync with header"
+
+
+def test_abi_version_and_status_strings():
+    from stark_amd import qmm
+    assert qmm.lib().stark_qmm_abi_version() == 1
+    for s in range(12):
+        assert qmm.status_string(s) and qmm.status_string(s) != "unknown status"
+    assert qmm.status_string(999) == "unknown status"
+
+
+def test_create_validates_dtypes_like_reference():
+    """MatmulCpuKernel::new accepts only F32/F16/BF16 (kernel.rs:37-41)."""
+    from stark_amd import qmm
+    for dts in ((qmm.BF16, qmm.BF16, qmm.BF16), (qmm.F32, qmm.F16, qmm.BF16)):
+        k = qmm.MatmulKernel(*dts)
+        k.close()
+    with pytest.raises(qmm.MatmulError) as e:
+        qmm.MatmulKernel(qmm.BF16, 7, qmm.BF16)
+    assert e.value.status == qmm.UNSUPPORTED_DATA_TYPE
+
+
+def _raw_encode(qmm, **over):
+    """Encode with raw device-free pointers: every case below must be rejected
+    before any HIP call."""
+    s = qmm._Args()
+    s.struct_size = C.sizeof(qmm._Args)
+    s.a = 0x1000
+    s.b.codes = 0x2000
+    s.b.codes_size = 64
+    s.b.scales = 0x3000
+    s.b.correction = qmm.BIASES
+    s.b.correction_data = 0x4000
+    s.b.params.layout = 0
+    s.b.params.row_count = 1
+    s.b.params.group_count = 2
+    s.b.mode = qmm.MODE_U4
+    s.b.group_size = 64
+    s.b_transpose = 1
+    s.d = 0x5000
+    s.d_ops.ab_scale = 1.0
+    s.m, s.n, s.k = 1, 1, 128
+    for key, v in over.items():
+        obj = s
+        parts = key.split(".")
+        for p in parts[:-1]:
+            obj = getattr(obj, p)
+        setattr(obj, parts[-1], v)
+    h = C.c_void_p()
+    assert qmm.lib().stark_qmm_create(qmm.BF16, qmm.BF16, qmm.BF16, C.byref(h)) == 0
+    st = qmm.lib().stark_qmm_encode(h, C.byref(s), None)
+    qmm.lib().stark_qmm_destroy(h)
+    return st
+
+
+def test_encode_rejections_without_device():
+    from stark_amd import qmm
+    assert _raw_encode(qmm, struct_size=8) == qmm.ABI_MISMATCH
+    assert _raw_encode(qmm, **{"d_ops.rht_factors": 0x6000}) == qmm.UNSUPPORTED_D_OP
+    # reference.rs:62-71: 1*128*4/8 = 64 bytes required
+    assert _raw_encode(qmm, **{"b.codes_size": 63}) == qmm.UNSUPPORTED_LAYOUT
+    assert _raw_encode(qmm, **{"b.group_size": 0}) == qmm.UNSUPPORTED_GROUP_SIZE
+    assert _raw_encode(qmm, **{"b.mode": 77}) == qmm.INVALID_ARGUMENT
+    # materialize policy (arguments.rs:36-61): signed codes / 8-bit / k%4 rejected
+    assert _raw_encode(qmm, **{"b.params.materialize_affine_input_sum": 1, "b.signed_codes": 1}) == qmm.UNSUPPORTED_LAYOUT
+    assert _raw_encode(qmm, **{"b.params.materialize_affine_input_sum": 1, "b.mode": qmm.MODE_U8,
+                               "b.codes_size": 128}) == qmm.UNSUPPORTED_LAYOUT
+    assert _raw_encode(qmm, **{"b.correction": qmm.BIASES, "b.correction_data": None}) == qmm.INVALID_ARGUMENT
+    # empty products are a no-op
+    assert _raw_encode(qmm, m=0) == qmm.OK
+
+
+def test_mapped_many_validation_without_device():
+    """parameters_for_input (weight_metal.rs:442-537) rejections."""
+    from stark_amd import qmm
+    lib = qmm.lib()
+    mats = (qmm._MappedMatrix * 1)()
+    mats[0].codes = 0x1000
+    mats[0].codes_length = 4 * 64 // 2
+    mats[0].scales = 0x2000
+    mats[0].biases = 0x3000
+    mats[0].plane_length = 4 * 1 * 2
+    op = (qmm._MappedOp * 1)()
+    op[0].matrices = mats
+    op[0].matrix_count = 1
+    op[0].inputs = 0x4000
+    op[0].input_length = 64
+    op[0].rows, op[0].columns = 4, 64
+    op[0].format = qmm.FORMAT_AFFINE
+    op[0].scale_dtype, op[0].bits, op[0].group = qmm.BF16, 4, 64
+    outs = (C.c_void_p * 1)(0x5000)
+
+    def st(**kw):
+        saved = {k: getattr(op[0], k) for k in kw}
+        for k, v in kw.items():
+            setattr(op[0], k, v)
+        r = lib.stark_qmm_mapped_many_async(op, 1, outs, C.c_void_p(0x6000), None) if False else None
+        for k, v in saved.items():
+            setattr(op[0], k, v)
+        return r
+
+    # validation is reached before any launch only for invalid descriptors:
+    for kw in ({"input_length": 63}, {"group": 16}, {"bits": 5}, {"scale_dtype": 9}, {"rows": 0},
+               {"columns": 0}, {"rows_per_batch": 3}, {"format": 7}):
+        saved = {k: getattr(op[0], k) for k in kw}
+        for k, v in kw.items():
+            setattr(op[0], k, v)
+        assert lib.stark_qmm_mapped_many_async(op, 1, outs, C.c_void_p(0x6000), None) == qmm.INVALID_ARGUMENT, kw
+        for k, v in saved.items():
+            setattr(op[0], k, v)
+    op[0].format = qmm.FORMAT_PACKED
+    op[0].packed_kind = 99
+    assert lib.stark_qmm_mapped_many_async(op, 1, outs, C.c_void_p(0x6000), None) == qmm.UNSUPPORTED
+    assert lib.stark_qmm_mapped_many_async(op, 0, outs, C.c_void_p(0x6000), None) == qmm.INVALID_ARGUMENT
+    assert lib.stark_qmm_mapped_many_async(op, 65, outs, C.c_void_p(0x6000), None) == qmm.INVALID_ARGUMENT

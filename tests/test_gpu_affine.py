@@ -1,0 +1,242 @@
+"""GPU parity of the affine (MLX-style) quantized matmul path against the CPU
+oracle (restating MatmulCpuKernel::encode,
+crates/stark-engine/src/backends/cpu/kernel/matmul/kernel.rs:58-303), through the
+C ABI (stark_qmm_encode / stark_qmm_encode_many)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from tests import helpers as H
+from tests.tolerances import check
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KAT = json.load(open(os.path.join(HERE, "golden", "kat_vectors.json")))
+
+
+def np_dtype(dt):
+    return np.float32 if dt == H.F32 else np.uint16
+
+
+def torch_empty(n, dt):
+    return torch.zeros(n, dtype=torch.float32 if dt == H.F32 else torch.int16, device="cuda")
+
+
+def run_case(Q, O, *, m, n, k, bits=4, gs=64, layout=0, correction=1, w_dt=H.BF16, x_dt=H.BF16, d_dt=H.BF16,
+             signed=False, gather=None, bank_rows=None, ab_scale=1.0, accumulate=False, with_bias=False,
+             soft_cap=None, seed=0, quantizer=True, label=""):
+    rng = np.random.default_rng(seed)
+    rows = n if bank_rows is None else bank_rows
+    W = H.affine_weights(O, rng, rows, k, bits, gs, layout, correction, w_dt, quantizer=quantizer)
+    x = H.activations(O, rng, m, k, x_dt)
+    prior = H.store(O, rng.normal(0, 1, m * n).astype(np.float32), d_dt) if accumulate else None
+    bias = H.store(O, rng.normal(0, 0.5, n).astype(np.float32), w_dt) if with_bias else None
+    G = k // gs
+    mode = {4: Q.MODE_U4, 8: Q.MODE_U8}.get(bits, {3: Q.MODE_U3, 5: Q.MODE_U5, 6: Q.MODE_U6}.get(bits))
+    st, want = O.matmul(a=x, m=m, n=n, k=k, codes=W["codes"], scales=W["scales"], correction=correction,
+                        correction_data=W["corr"], layout=layout, row_count=rows, group_count=G, bits=bits,
+                        group_size=gs, signed_codes=signed, d=prior, ab_scale=ab_scale, accumulate=accumulate,
+                        bias=bias, soft_cap=soft_cap, gather=gather, weights_dt=w_dt, input_dt=x_dt, output_dt=d_dt,
+                        threads=8)
+    assert st == 0
+    d = H.to_dev(prior) if prior is not None else torch_empty(m * n, d_dt)
+    args = Q.MatmulArguments(
+        a=H.to_dev(x), m=m, n=n, k=k, d=d,
+        b=Q.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                       params=Q.QuantParams(layout, rows, G), mode=mode, group_size=gs, correction=correction,
+                       correction_data=None if W["corr"] is None else H.to_dev(W["corr"]), signed_codes=signed),
+        d_transform=Q.MatmulDOps(ab_scale=ab_scale, accumulate=accumulate,
+                                 bias=None if bias is None else H.to_dev(bias), soft_cap=soft_cap),
+        gather_indices=None if gather is None else H.to_dev(np.asarray(gather, np.uint32)))
+    kern = Q.MatmulKernel(w_dt, x_dt, d_dt)
+    kern.encode(args)
+    torch.cuda.synchronize()
+    got = H.load(O, H.from_dev(d, np_dtype(d_dt)), d_dt)
+    mag = H.dequant_magnitude(O, W["codes"], W["scales"], W["corr"], rows, k, bits, gs, layout, correction, w_dt, x,
+                              x_dt, m, gather=gather, signed=signed, out_n=n)
+    if accumulate or with_bias:
+        mag = mag * abs(ab_scale) + 4.0
+    check(got, H.load(O, want, d_dt), mag=mag, label=label or f"m{m} n{n} k{k} b{bits} g{gs}")
+    return got, H.load(O, want, d_dt)
+
+
+# --------------------------------------------------------------- headline shapes
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("d_dt", [H.BF16, H.F32])
+def test_config0_w4_matvec(qmm, oracle, layout, d_dt):
+    """N=3072, K=1024, W4 g64, M=1."""
+    run_case(qmm, oracle, m=1, n=3072, k=1024, layout=layout, d_dt=d_dt, seed=1)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+def test_qwen3_8b_shapes_small_m(qmm, oracle, m):
+    """Config-1 widths at reduced N (full-size runs are in bench/property tests)."""
+    for n, k in ((256, 4096), (96, 12288)):
+        run_case(qmm, oracle, m=m, n=n, k=k, layout=1, seed=m * 7 + k)
+
+
+@pytest.mark.parametrize("k", [32, 96, 2048, 4160, 8192 + 512])
+def test_partial_passes_and_tails(qmm, oracle, k):
+    run_case(qmm, oracle, m=2, n=45, k=k, gs=32, seed=k)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 128), (8, 16), (8, 32), (8, 64), (8, 128)])
+def test_bits_and_groups(qmm, oracle, bits, gs):
+    run_case(qmm, oracle, m=1, n=70, k=1024, bits=bits, gs=gs, seed=bits * gs)
+    run_case(qmm, oracle, m=5, n=33, k=2048, bits=bits, gs=gs, layout=1, seed=bits * gs + 1)
+
+
+@pytest.mark.parametrize("correction", [0, 1, 2])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("signed", [False, True])
+def test_corrections_layouts_signed(qmm, oracle, correction, layout, signed):
+    for bits in (4, 8):
+        run_case(qmm, oracle, m=2, n=37, k=512, bits=bits, layout=layout, correction=correction, signed=signed,
+                 quantizer=False, seed=correction * 4 + layout * 2 + signed + bits)
+
+
+@pytest.mark.parametrize("x_dt", [H.BF16, H.F16, H.F32])
+@pytest.mark.parametrize("w_dt", [H.BF16, H.F16, H.F32])
+@pytest.mark.parametrize("d_dt", [H.BF16, H.F16, H.F32])
+def test_dtypes(qmm, oracle, x_dt, w_dt, d_dt):
+    run_case(qmm, oracle, m=1, n=40, k=512, w_dt=w_dt, x_dt=x_dt, d_dt=d_dt, quantizer=False, seed=x_dt + w_dt + d_dt)
+
+
+def test_d_ops(qmm, oracle):
+    run_case(qmm, oracle, m=3, n=50, k=1024, ab_scale=0.75, accumulate=True, with_bias=True, soft_cap=4.0,
+             d_dt=H.F32, seed=3)
+    run_case(qmm, oracle, m=1, n=50, k=1024, ab_scale=2.0, with_bias=True, seed=4)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_gather(qmm, oracle, m):
+    """gather_indices remap output (m, n) to weight row gather[m*n+n]
+    (kernel.rs:172-176); a row outside the codes buffer gives NaN."""
+    rng = np.random.default_rng(20 + m)
+    bank, n, k = 200, 64, 1024
+    g = rng.integers(0, bank, m * n).astype(np.uint32)
+    run_case(qmm, oracle, m=m, n=n, k=k, gather=g, bank_rows=bank, seed=m)
+
+
+def test_gather_out_of_bank_is_nan(qmm, oracle):
+    rng = np.random.default_rng(0)
+    bank, n, k = 64, 32, 512
+    W = H.affine_weights(oracle, rng, bank, k)
+    x = H.activations(oracle, rng, 1, k)
+    g = np.arange(n, dtype=np.uint32)
+    g[5] = 1000
+    d = torch_empty(n, H.F32)
+    args = qmm.MatmulArguments(a=H.to_dev(x), m=1, n=n, k=k, d=d, gather_indices=H.to_dev(g),
+                               b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                                                params=qmm.QuantParams(0, bank, k // 64),
+                                                correction_data=H.to_dev(W["corr"])))
+    qmm.MatmulKernel(H.BF16, H.BF16, H.F32).encode(args)
+    out = d.cpu().numpy()
+    assert np.isnan(out[5]) and not np.isnan(np.delete(out, 5)).any()
+
+
+# --------------------------------------------------------------- exact-value cases
+
+def test_packed_tail_kats_on_gpu(qmm, oracle):
+    """reference.rs:240-245 run through the GPU generic path: exact outputs."""
+    for c in KAT["packed_tails"]["cases"]:
+        k, n, bits = c["k"], c["n"], c["bits"]
+        d = torch_empty(n, H.F32)
+        args = qmm.MatmulArguments(
+            a=torch.ones(k, dtype=torch.float32, device="cuda"), m=1, n=n, k=k, d=d,
+            b=qmm.QuantizedB(codes=H.to_dev(np.array(c["codes"], np.uint8)),
+                             scales=torch.ones(n, dtype=torch.float32, device="cuda"),
+                             params=qmm.QuantParams(0, n, 1), mode=qmm.MODE_U8 if bits == 8 else qmm.MODE_U4,
+                             group_size=k, correction=qmm.SYMMETRIC))
+        qmm.MatmulKernel(H.F32, H.F32, H.F32).encode(args)
+        assert d.cpu().tolist() == c["expected"]
+    # undersized codes -> UnsupportedLayout, nothing launched
+    args = qmm.MatmulArguments(
+        a=torch.ones(2, dtype=torch.float32, device="cuda"), m=1, n=1, k=2, d=torch_empty(1, H.F32),
+        b=qmm.QuantizedB(codes=torch.zeros(1, dtype=torch.uint8, device="cuda"),
+                         scales=torch.ones(1, dtype=torch.float32, device="cuda"), params=qmm.QuantParams(0, 1, 1),
+                         mode=qmm.MODE_U8, group_size=2, correction=qmm.SYMMETRIC))
+    with pytest.raises(qmm.MatmulError) as e:
+        qmm.MatmulKernel(H.F32, H.F32, H.F32).encode(args)
+    assert e.value.status == qmm.UNSUPPORTED_LAYOUT
+
+
+@pytest.mark.parametrize("bits", [3, 5, 6])
+def test_odd_bit_widths_generic(qmm, oracle, bits):
+    run_case(qmm, oracle, m=2, n=17, k=192, bits=bits, gs=64, correction=1, quantizer=False, seed=bits)
+
+
+@pytest.mark.parametrize("case", KAT["materialized_affine_input_sum"]["cases"],
+                         ids=lambda c: c["scenario"] + str(c["materialize"]))
+def test_materialized_affine_input_sum_on_gpu(qmm, oracle, case):
+    """affine_input_sum_test.rs:133-196: the CPU-backend exact values. The
+    non-materialized 'quad' case runs the fast GEMV; its exact value holds
+    because every partial sum there is exactly representable."""
+    from tests.test_oracle_kats import materialized_case
+    a = materialized_case(oracle, case["scenario"], case["materialize"])
+    n, k = a["n"], a["k"]
+    d = torch_empty(n, H.BF16)
+    args = qmm.MatmulArguments(
+        a=H.to_dev(a["a"]), m=1, n=n, k=k, d=d,
+        b=qmm.QuantizedB(codes=H.to_dev(a["codes"]), scales=H.to_dev(a["scales"]),
+                         params=qmm.QuantParams(0, n, k // 64, case["materialize"]), group_size=64,
+                         correction_data=H.to_dev(a["correction_data"])))
+    qmm.MatmulKernel(H.BF16, H.BF16, H.BF16).encode(args)
+    got = oracle.bf16_to_f32(H.from_dev(d, np.uint16))
+    assert np.all(got == case["expected_all"]), got[:4]
+
+
+def test_error_paths(qmm, oracle):
+    rng = np.random.default_rng(1)
+    W = H.affine_weights(oracle, rng, 8, 128)
+    base = dict(a=H.to_dev(H.activations(oracle, rng, 1, 128)), m=1, n=8, k=128, d=torch_empty(8, H.F32))
+
+    def b(**kw):
+        args = dict(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]), params=qmm.QuantParams(0, 8, 2),
+                    correction_data=H.to_dev(W["corr"]))
+        args.update(kw)
+        return qmm.QuantizedB(**args)
+
+    k = qmm.MatmulKernel(H.BF16, H.BF16, H.F32)
+    with pytest.raises(qmm.MatmulError) as e:
+        k.encode(qmm.MatmulArguments(b=b(), d_transform=qmm.MatmulDOps(rht_factors=torch.zeros(8, device="cuda")),
+                                     **base))
+    assert e.value.status == qmm.UNSUPPORTED_D_OP
+    with pytest.raises(qmm.MatmulError) as e:
+        k.encode(qmm.MatmulArguments(b=b(params=qmm.QuantParams(0, 8, 2, True)), **base))
+    assert e.value.status == qmm.UNSUPPORTED_LAYOUT  # materialize needs bf16 output
+    with pytest.raises(qmm.MatmulError) as e:
+        k.encode(qmm.MatmulArguments(b=b(group_size=0), **base))
+    assert e.value.status == qmm.UNSUPPORTED_GROUP_SIZE
+    with pytest.raises(qmm.MatmulError) as e:
+        qmm.MatmulKernel(H.BF16, H.BF16, 2)
+    assert e.value.status == qmm.UNSUPPORTED_DATA_TYPE
+
+
+def test_encode_many_matches_single(qmm, oracle):
+    """stark_qmm_encode_many: one launch for several independent products
+    (the config-1 layer set at reduced N) equals one encode per product."""
+    rng = np.random.default_rng(9)
+    shapes = [(256, 4096), (64, 4096), (64, 4096), (256, 4096), (512, 4096), (512, 4096), (256, 12288)]
+    kern = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    many, single = [], []
+    for n, k in shapes:
+        W = H.affine_weights(oracle, rng, n, k, layout=1)
+        x = H.to_dev(H.activations(oracle, rng, 1, k))
+        mk = lambda d: qmm.MatmulArguments(
+            a=x, m=1, n=n, k=k, d=d,
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(1, n, k // 64), correction_data=H.to_dev(W["corr"])))
+        many.append(mk(torch_empty(n, H.BF16)))
+        single.append(mk(torch_empty(n, H.BF16)))
+    kern.encode_many(many)
+    for a in single:
+        kern.encode(a)
+    torch.cuda.synchronize()
+    for a, b in zip(many, single):
+        assert torch.equal(a.d, b.d)
