@@ -83,7 +83,7 @@ def cpu_baseline(torch, layer, xs, budget_s=12.0):
     for mat, x in zip(layer, xs):
         host.append(dict(n=mat["n"], k=mat["k"], codes=mat["codes"].cpu().numpy(),
                          s=mat["scales"].cpu().numpy().view(np.uint16), b=mat["biases"].cpu().numpy().view(np.uint16),
-                         x=x.cpu().numpy().view(np.uint16)))
+                         x=x.view(torch.int16).cpu().numpy().view(np.uint16)))
     passes, bytes_done, t0 = 0, 0, time.perf_counter()
     while True:
         for h in host:

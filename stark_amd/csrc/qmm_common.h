@@ -58,8 +58,43 @@ QMM_DEVICE float wave_sum(float v) {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// 16-byte load of weight codes that are read exactly once per launch.
-QMM_DEVICE u32x4 load_stream(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+// 16-byte load of weight codes that are read exactly once per launch
+// (QMM_STREAM_NT=0 builds plain cached loads instead of nontemporal ones).
+#ifndef QMM_STREAM_NT
+#define QMM_STREAM_NT 1
+#endif
+QMM_DEVICE u32x4 load_stream(const void* p) {
+#if QMM_STREAM_NT
+    return __builtin_nontemporal_load((const u32x4*)p);
+#else
+    return *(const u32x4*)p;
+#endif
+}
+
+// (a & mask) | orv in one VALU op: gfx950 VOP3 takes no literal, so the mask
+// rides in an SGPR and the or-value in a VGPR.
+QMM_DEVICE uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(orv));
+    return r;
+}
+
+// Sum each of 8 per-lane values over the wave with a transposed butterfly
+// (10 shuffles instead of 48). Returns, in every lane, the total of value
+// r = 4*bit5 + 2*bit4 + bit3 of the lane id.
+QMM_DEVICE float wave_sum8(const float (&v)[8], int lane) {
+    const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8;
+    float a[4], b[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = (h32 ? v[4 + j] : v[j]) + __shfl_xor(h32 ? v[j] : v[4 + j], 32, 64);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b[j] = (h16 ? a[2 + j] : a[j]) + __shfl_xor(h16 ? a[j] : a[2 + j], 16, 64);
+    float c = (h8 ? b[1] : b[0]) + __shfl_xor(h8 ? b[0] : b[1], 8, 64);
+    c += __shfl_xor(c, 4, 64);
+    c += __shfl_xor(c, 2, 64);
+    c += __shfl_xor(c, 1, 64);
+    return c;
+}
 
 // D = a.lo*b.lo + a.hi*b.hi + c (products exact for bf16, f32 accumulate).
 QMM_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -112,6 +147,7 @@ constexpr int kMaxBatchOps = 8;
 struct AffineBatch {
     AffineOp op[kMaxBatchOps];
     uint32_t count;
+    uint32_t total;  // work tiles over all ops
 };
 
 // Launch helpers implemented in qmv_affine.hip.

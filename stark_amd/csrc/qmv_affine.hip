@@ -9,12 +9,13 @@
 //   acc += s * sum_{k in g} x*q + bias_term * sum_{k in g} x
 //
 // Design (HBM-bound streaming):
-// * one workgroup = 4 wave64s = a tile of 32 weight rows; the K axis is walked in
-//   passes of 4096 values; within a pass lane L of a wave owns 16-byte code
-//   chunks L, L+64, ... so every load instruction reads 1 KiB contiguous;
-// * the activation slice of the pass and the tile's per-group (scale, bias)
-//   are staged once per workgroup in LDS, then each lane keeps its activation
-//   chunks in registers for all 8 rows of its wave;
+// * one workgroup of 4 wave64s = a tile of 32 weight rows (8 per wave) over the
+//   whole K axis, walked in passes of 4096 values; within a pass lane L owns
+//   16-byte code chunks L, L+64, ... so every load instruction reads 1 KiB
+//   contiguous of a row;
+// * each wave issues its code loads first; activations and per-group
+//   (scale, bias) are then staged in LDS with 16-byte loads, so the one barrier
+//   per pass delays compute but never the HBM stream;
 // * 4-bit x bf16: nibbles become bf16 (1 + q/16) with one shift and one
 //   and-or per pair and feed v_dot2_f32_bf16 (products exact, f32 sums);
 //   the offset is folded into the group's (scale, bias):
@@ -28,8 +29,6 @@ namespace qmm {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerBlock = 32;
-constexpr int kRowsPerWave = kRowsPerBlock / (kThreads / 64);
 constexpr int kPassValues = 4096;
 
 // Byte B of a dword as f32 (selects v_cvt_f32_ubyteB).
@@ -143,135 +142,240 @@ __global__ __launch_bounds__(256) void qmv_affine_materialized(AffineOp op) {
     store_from_f32(op.d, op.d_dt, n, v);
 }
 
-// Per-lane activation registers for one pass.
-template <int BITS, int MT, bool DOT2>
-struct XRegs {
+// ------------------------------------------------------------------ fast path
+// A workgroup (4 wave64s) owns a tile of 32 consecutive weight rows of one op
+// (8 rows per wave) for MT activation rows, over the whole K axis walked in
+// passes of 4096 values. Per pass:
+//   1. every wave issues its code loads (8 rows x CPL 16-byte chunks per lane;
+//      lane L owns chunks L, L+64, ... so each instruction reads 1 KiB of a row)
+//   2. the workgroup stages the pass's activations and the tile's
+//      (scale, bias) pairs in LDS with 16-byte coalesced loads
+//   3. one barrier, then lanes read activations/metadata from LDS and consume
+//      the codes already in flight.
+// The barrier never delays the HBM stream: the code loads are issued before it.
+constexpr int kTileRows = 32;
+constexpr int kWaveRows = 8;
+
+template <int BITS>
+struct Geo {
     static constexpr int VPC = 128 / BITS;                // values per 16-byte chunk
     static constexpr int CPL = kPassValues / (64 * VPC);  // chunks per lane per pass
-    // DOT2: 16 bf16 pairs per 32-value chunk; else VPC floats per chunk.
-    static constexpr int WORDS = DOT2 ? 16 : VPC;
-    uint32_t v[MT][CPL][WORDS];
-    float sum[MT][CPL];
 };
 
-template <int BITS, int MT, bool DOT2>
-__global__ __launch_bounds__(kThreads) void qmv_affine_fast(AffineBatch batch) {
-    using X = XRegs<BITS, MT, DOT2>;
-    constexpr int VPC = X::VPC;
-    constexpr int CPL = X::CPL;
-    constexpr int RBATCH = BITS == 4 ? 8 : 4;  // rows whose codes are in flight together
+// (scale, bias_term) of weight row `w`, group `g`; DOT2 folds the +1 offset of
+// the (1 + q/16) encoding: (16 s, b - 16 s).
+template <int BITS, bool DOT2>
+__device__ __forceinline__ float2 fold_meta(float s, float bt) {
+    if (DOT2) {
+        const float s16 = 16.0f * s;
+        return make_float2(s16, bt - s16);
+    }
+    return make_float2(s, bt);
+}
+
+template <int BITS, bool DOT2>
+__device__ __forceinline__ float2 load_meta(const AffineOp& op, uint32_t w, uint32_t g) {
+    const size_t md = (size_t)w * op.os + (size_t)g * op.gs;
+    const float s = load_as_f32(op.scales, op.w_dt, md);
+    float bt;
+    if (op.corr_kind == STARK_QMM_CORRECTION_BIASES) {
+        bt = load_as_f32(op.corr, op.w_dt, md);
+    } else if (op.corr_kind == STARK_QMM_CORRECTION_ZERO_POINTS) {
+        const size_t zi = (size_t)w * op.zos + (size_t)g * op.zgs;
+        uint32_t zb;
+        if (BITS == 4) {
+            const uint32_t byte = ((const uint8_t*)op.corr)[zi >> 1];
+            zb = (zi & 1) ? (byte >> 4) & 15u : byte & 15u;
+        } else {
+            zb = ((const uint8_t*)op.corr)[zi];
+        }
+        bt = -s * (float)zb;
+    } else {
+        bt = -s * (float)(1u << (BITS - 1));
+    }
+    return fold_meta<BITS, DOT2>(s, bt);
+}
+
+__device__ __forceinline__ float half_to_f32(uint32_t h, uint32_t dt) {
+    return dt == STARK_QMM_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+// Stage the tile's metadata for groups [g0, g0+gcnt) as float2 [row][gpp].
+template <int BITS, bool DOT2>
+__device__ __forceinline__ void stage_meta(const AffineOp& op, const uint32_t* s_wrow, float2* s_meta, uint32_t n0,
+                                           uint32_t g0, uint32_t gcnt, uint32_t gpp, bool vec_go, bool vec_og) {
+    const int tid = threadIdx.x;
+    const bool biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
+    const float mid = (float)(1u << (BITS - 1));
+    if (vec_go) {
+        // group-output planes [G][N4]: 32 tile rows of one group are 64 contiguous bytes
+        const uint32_t nvec = gcnt * (kTileRows / 8);
+        for (uint32_t v = tid; v < nvec; v += kThreads) {
+            const uint32_t g = v >> 2, r8 = (v & 3) * 8;
+            const size_t off = (size_t)(g0 + g) * op.gs + n0 + r8;
+            const u32x4 sv = *(const u32x4*)((const uint16_t*)op.scales + off);
+            u32x4 bv = u32x4{0, 0, 0, 0};
+            if (biased) bv = *(const u32x4*)((const uint16_t*)op.corr + off);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float s = half_to_f32((sv[j >> 1] >> (16 * (j & 1))) & 0xffffu, op.w_dt);
+                const float b = biased ? half_to_f32((bv[j >> 1] >> (16 * (j & 1))) & 0xffffu, op.w_dt) : -s * mid;
+                s_meta[(r8 + j) * gpp + g] = fold_meta<BITS, DOT2>(s, b);
+            }
+        }
+    } else if (vec_og) {
+        // output-group planes [N][G]: 8 consecutive groups of one row are 16 bytes
+        const uint32_t per_row = gcnt / 8;
+        const uint32_t nvec = kTileRows * per_row;
+        for (uint32_t v = tid; v < nvec; v += kThreads) {
+            const uint32_t r = v / per_row, g8 = (v - r * per_row) * 8;
+            const size_t off = (size_t)s_wrow[r] * op.os + g0 + g8;
+            const u32x4 sv = *(const u32x4*)((const uint16_t*)op.scales + off);
+            u32x4 bv = u32x4{0, 0, 0, 0};
+            if (biased) bv = *(const u32x4*)((const uint16_t*)op.corr + off);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float s = half_to_f32((sv[j >> 1] >> (16 * (j & 1))) & 0xffffu, op.w_dt);
+                const float b = biased ? half_to_f32((bv[j >> 1] >> (16 * (j & 1))) & 0xffffu, op.w_dt) : -s * mid;
+                s_meta[r * gpp + g8 + j] = fold_meta<BITS, DOT2>(s, b);
+            }
+        }
+    } else {
+        // any dtype / correction / alignment: one element per thread step, ordered
+        // so that consecutive threads touch consecutive plane addresses
+        const bool go = op.os == 1;
+        for (uint32_t i = tid; i < kTileRows * gcnt; i += kThreads) {
+            uint32_t r, g;
+            if (go) {
+                g = i / kTileRows;
+                r = i - g * kTileRows;
+            } else {
+                r = i / gcnt;
+                g = i - r * gcnt;
+            }
+            s_meta[r * gpp + g] = load_meta<BITS, DOT2>(op, s_wrow[r], g0 + g);
+        }
+    }
+    (void)n0;
+}
+
+template <int BITS, int MT, bool DOT2, bool SIGNED>
+__global__ __launch_bounds__(kThreads) void qmv_affine_tile(AffineBatch batch) {
+    constexpr int VPC = Geo<BITS>::VPC;
+    constexpr int CPL = Geo<BITS>::CPL;
+    constexpr int RW = kWaveRows;
+    constexpr int XW = DOT2 ? 16 : VPC;  // activation words per chunk
 
     extern __shared__ __align__(16) uint8_t smem[];
 
-    // ---- locate this block's op (uniform scalar select; no dynamic kernarg indexing)
     const uint32_t bid = blockIdx.x;
-    int oi = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxBatchOps; ++i)
-        if (i < (int)batch.count && bid >= batch.op[i].block_begin) oi = i;
-    AffineOp op = batch.op[0];
-#pragma unroll
-    for (int i = 1; i < kMaxBatchOps; ++i)
-        if (oi == i) op = batch.op[i];
+    // The batch is the kernel's only argument, so it starts the kernarg
+    // segment: index the op table there with scalar loads.
+    (void)batch;
+    const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t oi = 0;
+    for (uint32_t i = 1; i < kb->count; ++i)
+        if (bid >= kb->op[i].block_begin) oi = i;
+    const AffineOp op = kb->op[oi];
 
     const uint32_t N = op.n, K = op.k;
-    const uint32_t nrb = (N + kRowsPerBlock - 1) / kRowsPerBlock;
+    const uint32_t nrb = (N + kTileRows - 1) / kTileRows;
     const uint32_t lb = bid - op.block_begin;
     const uint32_t mtile = lb / nrb;
-    const uint32_t n0 = (lb - mtile * nrb) * kRowsPerBlock;
+    const uint32_t n0 = (lb - mtile * nrb) * kTileRows;
     const uint32_t m0 = mtile * MT;
     const int mcount = min((int)MT, (int)(op.m - m0));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t row_bytes = (size_t)K * BITS / 8;
     const uint32_t gsz = op.group_size;
     const uint32_t G = K / gsz;
-    const uint32_t gpp = kPassValues / gsz;  // groups per pass
+    const uint32_t gpp = kPassValues / gsz;
 
-    uint32_t* s_wrow = (uint32_t*)smem;                                   // [32]
-    float2* s_meta = (float2*)(smem + 128);                               // [32 * gpp]
-    uint8_t* s_x = smem + 128 + (size_t)kRowsPerBlock * gpp * sizeof(float2);  // [MT][4096] bf16 or f32
+    uint32_t* s_wrow = (uint32_t*)smem;                                         // [32]
+    float2* s_meta = (float2*)(smem + 128);                                     // [32][gpp]
+    uint8_t* s_x = smem + 128 + (size_t)kTileRows * gpp * sizeof(float2);       // [MT][4096] bf16 / f32
 
-    if (tid < kRowsPerBlock) {
-        uint32_t n = n0 + tid;
-        uint32_t w = 0xffffffffu;
-        if (n < N) {
-            w = op.gather ? op.gather[(size_t)m0 * N + n] : n;
-            if (w >= op.bank_rows) w = 0xffffffffu;  // out-of-bank gathered row: NaN output below
-        }
-        s_wrow[tid] = w;
-    }
-
-    float acc[kRowsPerWave][MT];
+    // weight rows of this wave (tail rows are clamped, computed and discarded)
+    uint32_t wrow[RW];
+    uint32_t badmask = 0;  // bit r: gathered row r lies outside the bank
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r)
+    for (int r = 0; r < RW; ++r) {
+        const uint32_t n = min(n0 + wave * RW + r, N - 1);
+        const uint32_t w = op.gather ? op.gather[(size_t)m0 * N + n] : n;
+        const bool bad = w >= op.bank_rows;
+        badmask |= bad ? 1u << r : 0u;
+        wrow[r] = bad ? 0u : w;
+    }
+    if (lane < RW) s_wrow[wave * RW + lane] = wrow[lane];
+
+    // vectorized metadata staging applies to 16-bit planes with biases (or no
+    // correction) when the 16-byte loads stay aligned
+    const bool planes16 = op.w_dt != STARK_QMM_F32 &&
+                          (op.corr_kind == STARK_QMM_CORRECTION_BIASES || op.corr_kind == STARK_QMM_CORRECTION_SYMMETRIC) &&
+                          (((uintptr_t)op.scales | (uintptr_t)op.corr) & 15) == 0;
+    const bool vec_go = planes16 && op.os == 1 && !op.gather && (op.gs % 8) == 0 && n0 + kTileRows <= N;
+    const bool vec_og = planes16 && op.gs == 1 && (op.os % 8) == 0 && (gpp % 8) == 0 && (G % 8) == 0;
+    const bool x_vec = op.x_dt != STARK_QMM_F32 && (((uintptr_t)op.x) & 15) == 0 && (K % 8) == 0;
+
+    float acc[RW][MT];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 
     const uint32_t npass = (K + kPassValues - 1) / kPassValues;
-    const float midpoint = (float)(1u << (BITS - 1));
-    const bool go_layout = op.os == 1;  // group-output planes: consecutive rows are contiguous
-
     for (uint32_t p = 0; p < npass; ++p) {
         const uint32_t kbase = p * kPassValues;
         const uint32_t kvals = min((uint32_t)kPassValues, K - kbase);
         const uint32_t g0 = kbase / gsz;
         const uint32_t gcnt = min(gpp, G - g0);
-        __syncthreads();
+        const uint8_t* pass_codes = op.codes + (size_t)kbase * BITS / 8;
 
-        // ---- stage activations (as bf16 bits for DOT2, else as f32)
-        for (uint32_t i = tid; i < (uint32_t)mcount * kvals; i += kThreads) {
-            uint32_t m = i / kvals, kk = i - m * kvals;
-            size_t src = (size_t)(m0 + m) * K + kbase + kk;
-            if (DOT2) {
-                ((uint16_t*)s_x)[m * kPassValues + kk] = ((const uint16_t*)op.x)[src];
-            } else {
-                ((float*)s_x)[m * kPassValues + kk] = load_as_f32(op.x, op.x_dt, src);
-            }
+        // ---- 1. the HBM stream: this wave's codes for the pass
+        u32x4 w[RW][CPL];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const uint32_t c = lane + 64 * i;
+            const bool ok = c * VPC < kvals;
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                w[r][i] = ok ? load_stream(pass_codes + (size_t)wrow[r] * row_bytes + (size_t)c * 16)
+                             : u32x4{0, 0, 0, 0};
         }
-        // ---- stage (scale, bias_term) of the tile's rows for this pass
-        for (uint32_t i = tid; i < (uint32_t)kRowsPerBlock * gcnt; i += kThreads) {
-            uint32_t r, g;
-            if (go_layout) {
-                g = i / kRowsPerBlock;
-                r = i - g * kRowsPerBlock;
-            } else {
-                r = i / gcnt;
-                g = i - r * gcnt;
-            }
-            uint32_t w = s_wrow[r];
-            float2 e = make_float2(0.0f, 0.0f);
-            if (w != 0xffffffffu) {
-                size_t md = (size_t)w * op.os + (size_t)(g0 + g) * op.gs;
-                float s = load_as_f32(op.scales, op.w_dt, md);
-                float bt;
-                if (op.corr_kind == STARK_QMM_CORRECTION_BIASES) {
-                    bt = load_as_f32(op.corr, op.w_dt, md);
-                } else if (op.corr_kind == STARK_QMM_CORRECTION_ZERO_POINTS) {
-                    size_t zi = (size_t)w * op.zos + (size_t)(g0 + g) * op.zgs;
-                    uint32_t zb;
-                    if (BITS == 4) {
-                        uint32_t byte = ((const uint8_t*)op.corr)[zi >> 1];
-                        zb = (zi & 1) ? (byte >> 4) & 15u : byte & 15u;
-                    } else {
-                        zb = ((const uint8_t*)op.corr)[zi];
-                    }
-                    bt = -s * (float)zb;
-                } else {
-                    bt = -s * midpoint;
-                }
+
+        // ---- 2. stage activations and metadata
+        if (p > 0) __syncthreads();  // previous pass finished reading LDS
+        if (x_vec) {
+            const uint32_t vpr = kvals / 8;  // 16-byte vectors per activation row
+            for (uint32_t v = tid; v < (uint32_t)mcount * vpr; v += kThreads) {
+                const uint32_t m = v / vpr, kk = (v - m * vpr) * 8;
+                const u32x4 t = *(const u32x4*)((const uint16_t*)op.x + (size_t)(m0 + m) * K + kbase + kk);
                 if (DOT2) {
-                    float s16 = 16.0f * s;
-                    e = make_float2(s16, bt - s16);
+                    *(u32x4*)((uint16_t*)s_x + m * kPassValues + kk) = t;
                 } else {
-                    e = make_float2(s, bt);
+                    float* dst = (float*)s_x + m * kPassValues + kk;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dst[2 * e] = half_to_f32(t[e] & 0xffffu, op.x_dt);
+                        dst[2 * e + 1] = half_to_f32(t[e] >> 16, op.x_dt);
+                    }
                 }
             }
-            s_meta[r * gpp + g] = e;
+        } else {
+            for (uint32_t i = tid; i < (uint32_t)mcount * kvals; i += kThreads) {
+                const uint32_t m = i / kvals, kk = i - m * kvals;
+                const size_t src = (size_t)(m0 + m) * K + kbase + kk;
+                if (DOT2) ((uint16_t*)s_x)[m * kPassValues + kk] = ((const uint16_t*)op.x)[src];
+                else ((float*)s_x)[m * kPassValues + kk] = load_as_f32(op.x, op.x_dt, src);
+            }
         }
+        if (p == 0) __syncthreads();  // s_wrow visible to the metadata staging
+        stage_meta<BITS, DOT2>(op, s_wrow, s_meta, n0, g0, gcnt, gpp, vec_go, vec_og);
         __syncthreads();
 
-        // ---- activation registers for this lane's chunks
-        X xr;
+        // ---- 3. activations for this lane's chunks (from LDS)
+        uint32_t xr[MT][CPL][XW];
+        float xs[MT][CPL];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
 #pragma unroll
@@ -281,151 +385,137 @@ __global__ __launch_bounds__(kThreads) void qmv_affine_fast(AffineBatch batch) {
                 if (DOT2) {
                     uint32_t v[16];
                     if (ok) {
-                        const uint4* src = (const uint4*)((const uint16_t*)s_x + m * kPassValues + c * 32);
+                        const u32x4* src = (const u32x4*)((const uint16_t*)s_x + m * kPassValues + c * 32);
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
-                            uint4 t = src[q];
-                            v[4 * q + 0] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+                            const u32x4 t = src[q];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
                         }
                     } else {
 #pragma unroll
                         for (int q = 0; q < 16; ++q) v[q] = 0;
                     }
-                    float s = 0.0f;
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
-                        xr.v[m][i][4 * d + 0] = perm(v[4 * d + 2], v[4 * d + 0], 0x05040100u);
-                        xr.v[m][i][4 * d + 1] = perm(v[4 * d + 2], v[4 * d + 0], 0x07060302u);
-                        xr.v[m][i][4 * d + 2] = perm(v[4 * d + 3], v[4 * d + 1], 0x05040100u);
-                        xr.v[m][i][4 * d + 3] = perm(v[4 * d + 3], v[4 * d + 1], 0x07060302u);
+                        xr[m][i][4 * d + 0] = perm(v[4 * d + 2], v[4 * d + 0], 0x05040100u);
+                        xr[m][i][4 * d + 1] = perm(v[4 * d + 2], v[4 * d + 0], 0x07060302u);
+                        xr[m][i][4 * d + 2] = perm(v[4 * d + 3], v[4 * d + 1], 0x05040100u);
+                        xr[m][i][4 * d + 3] = perm(v[4 * d + 3], v[4 * d + 1], 0x07060302u);
                     }
+                    float s = 0.0f;
 #pragma unroll
                     for (int q = 0; q < 16; ++q) s = dot2_bf16(v[q], 0x3F803F80u, s);
-                    xr.sum[m][i] = s;
+                    xs[m][i] = s;
                 } else {
                     const float* src = (const float*)s_x + m * kPassValues + c * VPC;
                     float s = 0.0f;
 #pragma unroll
                     for (int q = 0; q < VPC; ++q) {
-                        // 4-bit: per dword the unpack yields values in order 0,2,4,6,1,3,5,7
-                        int srcq = q;
+                        int sq = q;
                         if (BITS == 4) {
-                            int d = q / 8, e = q % 8;
-                            srcq = 8 * d + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
+                            const int d = q / 8, e = q % 8;
+                            sq = 8 * d + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
                         }
-                        float xv = ok ? src[srcq] : 0.0f;
-                        xr.v[m][i][q] = __float_as_uint(xv);
+                        const float xv = ok ? src[sq] : 0.0f;
+                        xr[m][i][q] = __float_as_uint(xv);
                         s += xv;
                     }
-                    xr.sum[m][i] = s;
+                    xs[m][i] = s;
                 }
             }
         }
 
-        // ---- stream the wave's rows
-        const uint8_t* pass_codes = op.codes + (size_t)kbase * BITS / 8;
+        // ---- 4. dot products
+        const uint32_t magic = 0x3F803F80u;  // bf16 1.0 in both halves
 #pragma unroll
-        for (int rb = 0; rb < kRowsPerWave; rb += RBATCH) {
-            u32x4 w[RBATCH][CPL];
+        for (int r = 0; r < RW; ++r) {
 #pragma unroll
-            for (int r = 0; r < RBATCH; ++r) {
-                const uint32_t wrow = s_wrow[wave * kRowsPerWave + rb + r];
+            for (int i = 0; i < CPL; ++i) {
+                const uint32_t c = lane + 64 * i;
+                const uint32_t g = min((c * VPC) / gsz, gpp - 1);
+                const float2 e = s_meta[(wave * RW + r) * gpp + g];
+                uint32_t wd[4] = {w[r][i][0], w[r][i][1], w[r][i][2], w[r][i][3]};
+                if (SIGNED) {
 #pragma unroll
-                for (int i = 0; i < CPL; ++i) {
-                    const uint32_t c = lane + 64 * i;
-                    if (wrow != 0xffffffffu && c * VPC < kvals) {
-                        w[r][i] = load_stream(pass_codes + (size_t)wrow * row_bytes + (size_t)c * 16);
-                    } else {
-                        w[r][i] = u32x4{0, 0, 0, 0};
+                    for (int d = 0; d < 4; ++d) wd[d] ^= BITS == 4 ? 0x88888888u : 0x80808080u;
+                }
+                // 4-bit pairs (n0,n4),(n1,n5),(n2,n6),(n3,n7) of a dword as bf16 (1 + q/16)
+                uint32_t pr[4][4];
+                if (DOT2) {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const uint32_t u = wd[d];
+                        pr[d][0] = and_or(u << 3, 0x00780078u, magic);
+                        pr[d][1] = and_or(u >> 1, 0x00780078u, magic);
+                        pr[d][2] = and_or(u >> 5, 0x00780078u, magic);
+                        pr[d][3] = and_or(u >> 9, 0x00780078u, magic);
                     }
                 }
-            }
 #pragma unroll
-            for (int r = 0; r < RBATCH; ++r) {
-                const int row = wave * kRowsPerWave + rb + r;
+                for (int m = 0; m < MT; ++m) {
+                    float dsum = 0.0f;
+                    if (DOT2) {
 #pragma unroll
-                for (int i = 0; i < CPL; ++i) {
-                    const uint32_t c = lane + 64 * i;
-                    const uint32_t g = min((c * VPC) / gsz, gpp - 1);
-                    const float2 e = s_meta[row * gpp + g];
-                    uint32_t wd[4] = {w[r][i][0], w[r][i][1], w[r][i][2], w[r][i][3]};
-                    if (op.flags & FLAG_SIGNED) {
-#pragma unroll
-                        for (int d = 0; d < 4; ++d) wd[d] ^= BITS == 4 ? 0x88888888u : 0x80808080u;
-                    }
-#pragma unroll
-                    for (int m = 0; m < MT; ++m) {
-                        float dsum = 0.0f;
-                        if (DOT2) {
-#pragma unroll
-                            for (int d = 0; d < 4; ++d) {
-                                const uint32_t u = wd[d];
-                                const uint32_t p0 = ((u << 3) & 0x00780078u) | 0x3F803F80u;
-                                const uint32_t p1 = ((u >> 1) & 0x00780078u) | 0x3F803F80u;
-                                const uint32_t p2 = ((u >> 5) & 0x00780078u) | 0x3F803F80u;
-                                const uint32_t p3 = ((u >> 9) & 0x00780078u) | 0x3F803F80u;
-                                dsum = dot2_bf16(p0, xr.v[m][i][4 * d + 0], dsum);
-                                dsum = dot2_bf16(p1, xr.v[m][i][4 * d + 1], dsum);
-                                dsum = dot2_bf16(p2, xr.v[m][i][4 * d + 2], dsum);
-                                dsum = dot2_bf16(p3, xr.v[m][i][4 * d + 3], dsum);
-                            }
-                        } else if (BITS == 4) {
-#pragma unroll
-                            for (int d = 0; d < 4; ++d) {
-                                const uint32_t lo = wd[d] & 0x0F0F0F0Fu;
-                                const uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;
-                                const float* xv = (const float*)&xr.v[m][i][8 * d];
-                                dsum = fmaf(ubyte<0>(lo), xv[0], dsum);
-                                dsum = fmaf(ubyte<1>(lo), xv[1], dsum);
-                                dsum = fmaf(ubyte<2>(lo), xv[2], dsum);
-                                dsum = fmaf(ubyte<3>(lo), xv[3], dsum);
-                                dsum = fmaf(ubyte<0>(hi), xv[4], dsum);
-                                dsum = fmaf(ubyte<1>(hi), xv[5], dsum);
-                                dsum = fmaf(ubyte<2>(hi), xv[6], dsum);
-                                dsum = fmaf(ubyte<3>(hi), xv[7], dsum);
-                            }
-                        } else {
-#pragma unroll
-                            for (int d = 0; d < 4; ++d) {
-                                const float* xv = (const float*)&xr.v[m][i][4 * d];
-                                dsum = fmaf(ubyte<0>(wd[d]), xv[0], dsum);
-                                dsum = fmaf(ubyte<1>(wd[d]), xv[1], dsum);
-                                dsum = fmaf(ubyte<2>(wd[d]), xv[2], dsum);
-                                dsum = fmaf(ubyte<3>(wd[d]), xv[3], dsum);
-                            }
+                        for (int d = 0; d < 4; ++d) {
+                            dsum = dot2_bf16(pr[d][0], xr[m][i][4 * d + 0], dsum);
+                            dsum = dot2_bf16(pr[d][1], xr[m][i][4 * d + 1], dsum);
+                            dsum = dot2_bf16(pr[d][2], xr[m][i][4 * d + 2], dsum);
+                            dsum = dot2_bf16(pr[d][3], xr[m][i][4 * d + 3], dsum);
                         }
-                        acc[rb + r][m] = fmaf(e.x, dsum, fmaf(e.y, xr.sum[m][i], acc[rb + r][m]));
+                    } else if (BITS == 4) {
+                        const float* xv = (const float*)xr[m][i];
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            const uint32_t lo = wd[d] & 0x0F0F0F0Fu;
+                            const uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;
+                            dsum = fmaf(ubyte<0>(lo), xv[8 * d + 0], dsum);
+                            dsum = fmaf(ubyte<1>(lo), xv[8 * d + 1], dsum);
+                            dsum = fmaf(ubyte<2>(lo), xv[8 * d + 2], dsum);
+                            dsum = fmaf(ubyte<3>(lo), xv[8 * d + 3], dsum);
+                            dsum = fmaf(ubyte<0>(hi), xv[8 * d + 4], dsum);
+                            dsum = fmaf(ubyte<1>(hi), xv[8 * d + 5], dsum);
+                            dsum = fmaf(ubyte<2>(hi), xv[8 * d + 6], dsum);
+                            dsum = fmaf(ubyte<3>(hi), xv[8 * d + 7], dsum);
+                        }
+                    } else {
+                        const float* xv = (const float*)xr[m][i];
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            dsum = fmaf(ubyte<0>(wd[d]), xv[4 * d + 0], dsum);
+                            dsum = fmaf(ubyte<1>(wd[d]), xv[4 * d + 1], dsum);
+                            dsum = fmaf(ubyte<2>(wd[d]), xv[4 * d + 2], dsum);
+                            dsum = fmaf(ubyte<3>(wd[d]), xv[4 * d + 3], dsum);
+                        }
                     }
+                    acc[r][m] = fmaf(e.x, dsum, fmaf(e.y, xs[m][i], acc[r][m]));
                 }
             }
         }
     }
 
     // ---- reduce across the wave and apply the D-ops (kernel.rs:270-281)
+    const int rrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+    const uint32_t n = n0 + wave * RW + rrow;
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) {
-        const int row = wave * kRowsPerWave + r;
-        const uint32_t n = n0 + row;
+    for (int m = 0; m < MT; ++m) {
+        float v8[RW];
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            float v = wave_sum(acc[r][m]);
-            if (lane == 0 && n < N && m < mcount) {
-                const size_t o = (size_t)(m0 + m) * N + n;
-                if (s_wrow[row] == 0xffffffffu) {
-                    store_from_f32(op.d, op.d_dt, o, __builtin_nanf(""));
-                    continue;
-                }
-                v = op.ab_scale * v;
-                if (op.flags & FLAG_ACCUMULATE) v += load_as_f32(op.d, op.d_dt, o);
-                if (op.bias) v += load_as_f32(op.bias, op.w_dt, n);
-                if (op.flags & FLAG_SOFT_CAP) v = op.soft_cap * tanhf(v / op.soft_cap);
-                store_from_f32(op.d, op.d_dt, o, v);
-            }
+        for (int r = 0; r < RW; ++r) v8[r] = acc[r][m];
+        const float v0 = wave_sum8(v8, lane);
+        if ((lane & 7) == 0 && n < N && m < mcount) {
+            const size_t o = (size_t)(m0 + m) * N + n;
+            float v = op.ab_scale * v0;
+            if (op.flags & FLAG_ACCUMULATE) v += load_as_f32(op.d, op.d_dt, o);
+            if (op.bias) v += load_as_f32(op.bias, op.w_dt, n);
+            if (op.flags & FLAG_SOFT_CAP) v = op.soft_cap * tanhf(v / op.soft_cap);
+            if ((badmask >> rrow) & 1u) v = __builtin_nanf("");
+            store_from_f32(op.d, op.d_dt, o, v);
         }
     }
 }
 
-template <int BITS, int MT, bool DOT2>
+template <int BITS, int MT, bool DOT2, bool SIGNED>
 stark_qmm_status launch_fast(const AffineOp* ops, uint32_t count, hipStream_t stream) {
     AffineBatch batch{};
     uint32_t blocks = 0;
@@ -433,17 +523,17 @@ stark_qmm_status launch_fast(const AffineOp* ops, uint32_t count, hipStream_t st
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = ops[i];
         batch.op[i].block_begin = blocks;
-        const uint32_t nrb = (ops[i].n + kRowsPerBlock - 1) / kRowsPerBlock;
+        const uint32_t nrb = (ops[i].n + kTileRows - 1) / kTileRows;
         const uint32_t mt = ops[i].gather ? ops[i].m : (ops[i].m + MT - 1) / MT;
         blocks += nrb * mt;
         const size_t gpp = kPassValues / ops[i].group_size;
-        const size_t need = 128 + kRowsPerBlock * gpp * sizeof(float2) +
-                            (size_t)MT * kPassValues * (DOT2 ? 2 : 4);
-        if (need > lds) lds = need;
+        const size_t need = 128 + kTileRows * gpp * sizeof(float2) + (size_t)MT * kPassValues * (DOT2 ? 2 : 4);
+        lds = need > lds ? need : lds;
     }
     batch.count = count;
+    batch.total = blocks;
     if (blocks == 0) return STARK_QMM_OK;
-    hipLaunchKernelGGL((qmv_affine_fast<BITS, MT, DOT2>), dim3(blocks), dim3(kThreads), lds, stream, batch);
+    hipLaunchKernelGGL((qmv_affine_tile<BITS, MT, DOT2, SIGNED>), dim3(blocks), dim3(kThreads), lds, stream, batch);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
 }
@@ -488,16 +578,25 @@ stark_qmm_status launch_affine_gemv(const AffineOp* ops, uint32_t count, int bit
     bool gathered = false;
     for (uint32_t i = 0; i < count; ++i) gathered |= ops[i].gather != nullptr;
     const bool mt2 = max_m >= 2 && !gathered;
-    for (uint32_t start = 0; start < count; start += kMaxBatchOps) {
-        uint32_t c = count - start < (uint32_t)kMaxBatchOps ? count - start : (uint32_t)kMaxBatchOps;
-        stark_qmm_status st;
-        if (bits == 4) {
-            if (dot2) st = mt2 ? launch_fast<4, 2, true>(ops + start, c, stream) : launch_fast<4, 1, true>(ops + start, c, stream);
-            else st = mt2 ? launch_fast<4, 2, false>(ops + start, c, stream) : launch_fast<4, 1, false>(ops + start, c, stream);
-        } else {
-            st = mt2 ? launch_fast<8, 2, false>(ops + start, c, stream) : launch_fast<8, 1, false>(ops + start, c, stream);
+    // one launch per signedness class
+    for (int sg = 0; sg < 2; ++sg) {
+        std::vector<AffineOp> cls;
+        for (uint32_t i = 0; i < count; ++i)
+            if (((ops[i].flags & FLAG_SIGNED) != 0) == (sg == 1)) cls.push_back(ops[i]);
+        for (size_t start = 0; start < cls.size(); start += kMaxBatchOps) {
+            const uint32_t c = (uint32_t)std::min<size_t>(kMaxBatchOps, cls.size() - start);
+            const AffineOp* o = cls.data() + start;
+            stark_qmm_status st;
+#define QMM_LAUNCH(B, M, D) (sg ? launch_fast<B, M, D, true>(o, c, stream) : launch_fast<B, M, D, false>(o, c, stream))
+            if (bits == 4) {
+                if (dot2) st = mt2 ? QMM_LAUNCH(4, 2, true) : QMM_LAUNCH(4, 1, true);
+                else st = mt2 ? QMM_LAUNCH(4, 2, false) : QMM_LAUNCH(4, 1, false);
+            } else {
+                st = mt2 ? QMM_LAUNCH(8, 2, false) : QMM_LAUNCH(8, 1, false);
+            }
+#undef QMM_LAUNCH
+            if (st != STARK_QMM_OK) return st;
         }
-        if (st != STARK_QMM_OK) return st;
     }
     return STARK_QMM_OK;
 }
