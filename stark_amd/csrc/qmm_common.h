@@ -147,13 +147,18 @@ constexpr int kMaxBatchOps = 8;
 struct AffineBatch {
     AffineOp op[kMaxBatchOps];
     uint32_t count;
-    uint32_t total;  // work tiles over all ops
+    uint32_t total;     // work tiles over all ops
+    uint32_t nib_mask;  // 0x00780078: nibble-pair mask, passed in so it stays in an SGPR
+    uint32_t nib_one;   // 0x3F803F80: bf16 1.0 pair, likewise
 };
 
 // Launch helpers implemented in qmv_affine.hip.
 stark_qmm_status launch_affine_gemv(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream);
 stark_qmm_status launch_affine_generic(const AffineOp& op, int bits, hipStream_t stream);
 bool affine_fast_eligible(const AffineOp& op, int bits);
+// Wave-independent kernel for decode-shaped 4-bit products (qmv_decode.hip).
+bool decode_eligible(const AffineOp& op, int bits);
+stark_qmm_status launch_affine_decode(const AffineOp* ops, uint32_t count, hipStream_t stream);
 stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stream);
 // Full-precision B operand (MatmulB::FullPrecision).
 struct DenseOp {

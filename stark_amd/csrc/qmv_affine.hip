@@ -566,7 +566,20 @@ stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stre
 
 // ops: same bits; each op must be affine_fast_eligible. M per op arbitrary
 // (weights are re-streamed once per pair of M rows).
-stark_qmm_status launch_affine_gemv(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream) {
+stark_qmm_status launch_affine_gemv(const AffineOp* ops_in, uint32_t count_in, int bits, hipStream_t stream) {
+    if (count_in == 0) return STARK_QMM_OK;
+    // decode-shaped 4-bit products go to the wave-independent decode kernel
+    std::vector<AffineOp> decode, others;
+    for (uint32_t i = 0; i < count_in; ++i) {
+        const AffineOp& o = ops_in[i];
+        (decode_eligible(o, bits) ? decode : others).push_back(o);
+    }
+    if (!decode.empty()) {
+        stark_qmm_status st = launch_affine_decode(decode.data(), (uint32_t)decode.size(), stream);
+        if (st != STARK_QMM_OK) return st;
+    }
+    const AffineOp* ops = others.data();
+    const uint32_t count = (uint32_t)others.size();
     if (count == 0) return STARK_QMM_OK;
     uint32_t max_m = 0;
     bool dot2 = true;

@@ -25,7 +25,7 @@ from typing import Optional, Sequence
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libstark_qmm.so")
+LIB_PATH = os.environ.get("QMM_LIB_OVERRIDE") or os.path.join(HERE, "libstark_qmm.so")
 
 # ---------------------------------------------------------------- constants
 

@@ -240,3 +240,26 @@ def test_encode_many_matches_single(qmm, oracle):
     torch.cuda.synchronize()
     for a, b in zip(many, single):
         assert torch.equal(a.d, b.d)
+
+
+@pytest.mark.parametrize("n,k,gs", [(40, 4160, 32), (64, 8192 + 512, 64), (1000, 12288, 128), (3072, 1024, 64)])
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_streaming_kernel_shapes(qmm, oracle, n, k, gs, m, layout):
+    """Shapes the persistent streaming kernel takes (4-bit, bf16 activations,
+    N % 8 == 0): partial passes, a shifted last tile (N % 32 != 0), both plane
+    layouts."""
+    run_case(qmm, oracle, m=m, n=n, k=k, gs=gs, layout=layout, seed=n + k + m)
+
+
+@pytest.mark.parametrize("correction,signed", [(0, False), (1, True), (0, True)])
+def test_streaming_kernel_corrections(qmm, oracle, correction, signed):
+    run_case(qmm, oracle, m=1, n=72, k=4096, correction=correction, signed=signed, quantizer=False, seed=5)
+    run_case(qmm, oracle, m=2, n=72, k=4096, correction=correction, signed=signed, quantizer=False, w_dt=H.F16,
+             seed=6)
+
+
+def test_streaming_kernel_d_ops_on_shifted_tile(qmm, oracle):
+    """N=40: the last 32-row tile overlaps the first; accumulate must add once."""
+    run_case(qmm, oracle, m=1, n=40, k=2048, ab_scale=0.5, accumulate=True, with_bias=True, d_dt=H.F32, seed=8)
+    run_case(qmm, oracle, m=2, n=40, k=2048, accumulate=True, soft_cap=2.0, d_dt=H.BF16, seed=9)
