@@ -434,7 +434,8 @@ __global__ __launch_bounds__(kThreads) void qmv_affine_tile(AffineBatch batch) {
             for (int i = 0; i < CPL; ++i) {
                 const uint32_t c = lane + 64 * i;
                 const uint32_t g = min((c * VPC) / gsz, gpp - 1);
-                const float2 e = s_meta[(wave * RW + r) * gpp + g];
+                // chunks past K have no staged metadata: their LDS holds stale bits
+                const float2 e = c * VPC < kvals ? s_meta[(wave * RW + r) * gpp + g] : float2{0.0f, 0.0f};
                 uint32_t wd[4] = {w[r][i][0], w[r][i][1], w[r][i][2], w[r][i][3]};
                 if (SIGNED) {
 #pragma unroll
@@ -569,10 +570,20 @@ stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stre
 stark_qmm_status launch_affine_gemv(const AffineOp* ops_in, uint32_t count_in, int bits, hipStream_t stream) {
     if (count_in == 0) return STARK_QMM_OK;
     // decode-shaped 4-bit products go to the wave-independent decode kernel
-    std::vector<AffineOp> decode, others;
+    std::vector<AffineOp> mfma, decode, others;
     for (uint32_t i = 0; i < count_in; ++i) {
         const AffineOp& o = ops_in[i];
+#ifndef QMM_DISABLE_MFMA
+        if (mfma_eligible(o, bits)) {
+            mfma.push_back(o);
+            continue;
+        }
+#endif
         (decode_eligible(o, bits) ? decode : others).push_back(o);
+    }
+    if (!mfma.empty()) {
+        stark_qmm_status st = launch_affine_mfma(mfma.data(), (uint32_t)mfma.size(), stream);
+        if (st != STARK_QMM_OK) return st;
     }
     if (!decode.empty()) {
         stark_qmm_status st = launch_affine_decode(decode.data(), (uint32_t)decode.size(), stream);

@@ -263,3 +263,29 @@ def test_streaming_kernel_d_ops_on_shifted_tile(qmm, oracle):
     """N=40: the last 32-row tile overlaps the first; accumulate must add once."""
     run_case(qmm, oracle, m=1, n=40, k=2048, ab_scale=0.5, accumulate=True, with_bias=True, d_dt=H.F32, seed=8)
     run_case(qmm, oracle, m=2, n=40, k=2048, accumulate=True, soft_cap=2.0, d_dt=H.BF16, seed=9)
+
+
+@pytest.mark.parametrize("n,k,gs", [(80, 4160, 32), (64, 8192 + 512, 64), (1040, 12288, 128), (3072, 1024, 64),
+                                    (96, 96, 32)])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_matrix_core_kernel_shapes(qmm, oracle, n, k, gs, m, layout):
+    """Shapes the 4-bit matrix-core kernel takes (bf16 activations, N % 16 == 0,
+    N >= 64, M <= 16): every activation-row class (1, 2, 4, 8 and two blocks of
+    8), partial steps and passes, a shifted last 64-row tile."""
+    run_case(qmm, oracle, m=m, n=n, k=k, gs=gs, layout=layout, seed=n + k + m + 7 * layout)
+
+
+@pytest.mark.parametrize("correction,signed", [(0, False), (1, True), (0, True)])
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_matrix_core_kernel_corrections(qmm, oracle, correction, signed, m):
+    run_case(qmm, oracle, m=m, n=144, k=4096, correction=correction, signed=signed, quantizer=False, seed=5 + m)
+    run_case(qmm, oracle, m=m, n=144, k=4096, correction=correction, signed=signed, quantizer=False, w_dt=H.F16,
+             seed=6 + m)
+
+
+@pytest.mark.parametrize("m", [1, 2, 6, 12])
+def test_matrix_core_kernel_d_ops_on_shifted_tile(qmm, oracle, m):
+    """N=80: the last 64-row tile overlaps the first; accumulate must add once."""
+    run_case(qmm, oracle, m=m, n=80, k=2048, ab_scale=0.5, accumulate=True, with_bias=True, d_dt=H.F32, seed=8)
+    run_case(qmm, oracle, m=m, n=80, k=2048, accumulate=True, soft_cap=2.0, d_dt=H.BF16, seed=9)
