@@ -273,6 +273,12 @@ def _args(a: MatmulArguments) -> _Args:
     return s
 
 
+@dataclass
+class PreparedBatch:
+    array: object  # ctypes array of stark_qmm_args
+    keep: list     # the MatmulArguments whose tensors the array points into
+
+
 class MatmulKernel:
     """trait MatmulKernel (kernel.rs:15-79) over stark_qmm_create/encode."""
 
@@ -295,6 +301,15 @@ class MatmulKernel:
     def encode_many(self, arguments: Sequence[MatmulArguments], stream=None) -> None:
         arr = (_Args * len(arguments))(*[_args(a) for a in arguments])
         _check(lib().stark_qmm_encode_many(self._h, arr, len(arguments), _stream(stream)), "encode_many")
+
+    def prepare_many(self, arguments: Sequence[MatmulArguments]) -> "PreparedBatch":
+        """Marshal a batch of arguments once (the C structs and the tensors they
+        point into are kept alive) so that encode_prepared() issues it with no
+        per-call Python conversion, as a compiled caller would."""
+        return PreparedBatch((_Args * len(arguments))(*[_args(a) for a in arguments]), list(arguments))
+
+    def encode_prepared(self, batch: "PreparedBatch", stream=None) -> None:
+        _check(lib().stark_qmm_encode_many(self._h, batch.array, len(batch.keep), _stream(stream)), "encode_many")
 
     def close(self) -> None:
         if getattr(self, "_h", None):
