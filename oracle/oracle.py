@@ -79,6 +79,8 @@ def _declare(l):
         "so_moe_accumulate": (None, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]),
         "so_moe_adjust_routes": (None, [vp, vp, vp, u32, u32, u32, u32]),
         "so_gated_silu_bf16": (None, [vp, vp, u32, u32]),
+        "so_routed_experts": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, u32, i32, u32, u32, u32, u32,
+                                    u32, i32, i32, i32, i32, i32, vp]),
         "so_quantize_affine": (None, [vp, sz, sz, i32, sz, i32, vp, vp, vp]),
         "so_quantize_q8_0": (None, [vp, sz, sz, vp]),
         "so_quantize_q4_k": (None, [vp, sz, sz, vp]),
@@ -317,6 +319,25 @@ def gated_silu_bf16(projected_bits, hidden, batch):
     p = np.ascontiguousarray(projected_bits, np.uint16)
     out = np.zeros(batch * hidden, np.uint16)
     lib().so_gated_silu_bf16(_p(p), _p(out), hidden, batch)
+    return out
+
+
+def routed_experts(input_bits, logits, up, down, rows, model, hidden, experts, active, expert_scales=None,
+                   layout=GROUP_OUTPUT, bits=4, group=64, plane_dt=BF16, round_logits=False, round_weights=False,
+                   round_products=False, round_accumulator=False, sort_ids=False) -> np.ndarray:
+    """RoutedExperts::encode_scaled restated (routed.rs:154-257). up/down are
+    dicts with codes, scales, biases (None = symmetric). Returns bf16 bits."""
+    out = np.zeros(rows * model, np.uint16)
+    keep = [np.ascontiguousarray(input_bits, np.uint16), np.ascontiguousarray(logits, np.float32)]
+    gains = None if expert_scales is None else np.ascontiguousarray(expert_scales, np.float32)
+    st = lib().so_routed_experts(_p(keep[0]), _p(keep[1]), _p(gains) if gains is not None else None,
+                                 _p(up["codes"]), _p(up["scales"]), _p(up["biases"]) if up["biases"] is not None else None,
+                                 _p(down["codes"]), _p(down["scales"]),
+                                 _p(down["biases"]) if down["biases"] is not None else None, layout, bits, group,
+                                 plane_dt, rows, model, hidden, experts, active, int(round_logits), int(round_weights),
+                                 int(round_products), int(round_accumulator), int(sort_ids), _p(out))
+    if st:
+        raise ValueError(f"so_routed_experts status {st}")
     return out
 
 

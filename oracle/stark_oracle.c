@@ -547,6 +547,85 @@ void so_gated_silu_bf16(const uint16_t* projected, uint16_t* out, uint32_t hidde
     }
 }
 
+/* encodable_block/mlp/routed.rs:154-257 */
+int so_routed_experts(const uint16_t* input, const float* logits, const float* expert_scales,
+                      const uint8_t* up_codes, const void* up_scales, const void* up_biases,
+                      const uint8_t* down_codes, const void* down_scales, const void* down_biases, int layout,
+                      int bits, uint32_t group_size, int plane_dt, uint32_t rows, uint32_t model, uint32_t hidden,
+                      uint32_t experts, uint32_t active, int round_logits, int round_weights, int round_products,
+                      int round_accumulator, int sort_ids, uint16_t* output) {
+    const size_t routes = (size_t)rows * active;
+    uint32_t* ids = (uint32_t*)malloc(routes * sizeof(uint32_t));
+    float* weights = (float*)malloc(routes * sizeof(float));
+    float* accumulator = (float*)calloc((size_t)rows * model, sizeof(float));
+    uint32_t* up_ids = (uint32_t*)malloc((size_t)2 * hidden * sizeof(uint32_t));
+    uint32_t* down_ids = (uint32_t*)malloc((size_t)model * sizeof(uint32_t));
+    uint16_t* projected = (uint16_t*)malloc((size_t)2 * hidden * sizeof(uint16_t));
+    uint16_t* activated = (uint16_t*)malloc((size_t)hidden * sizeof(uint16_t));
+    uint16_t* down_out = (uint16_t*)malloc((size_t)model * sizeof(uint16_t));
+    float* unit = (float*)malloc((size_t)experts * sizeof(float));
+    int status = 0;
+    so_moe_route(logits, ids, weights, rows, experts, active, round_weights, round_logits);
+    if (expert_scales) {
+        so_moe_adjust_routes(ids, weights, expert_scales, rows, experts, active, sort_ids);
+    } else if (sort_ids) {
+        for (uint32_t e = 0; e < experts; ++e) unit[e] = 1.0f;
+        so_moe_adjust_routes(ids, weights, unit, rows, experts, active, 1);
+    }
+    so_matmul_args up = {0}, down = {0};
+    up.codes = up_codes;
+    up.codes_size = (size_t)experts * 2 * hidden * model * (size_t)bits / 8;
+    up.scales = up_scales;
+    up.correction = up_biases ? SO_CORR_BIASES : SO_CORR_SYMMETRIC;
+    up.correction_data = up_biases;
+    up.layout = layout;
+    up.row_count = experts * 2 * hidden;
+    up.group_count = model / group_size;
+    up.bits = bits;
+    up.group_size = group_size;
+    up.b_transpose = 1;
+    up.ab_scale = 1.0f;
+    up.m = 1;
+    up.n = 2 * hidden;
+    up.k = model;
+    up.weights_dt = plane_dt;
+    up.input_dt = SO_BF16;
+    up.output_dt = SO_BF16;
+    up.gather_indices = up_ids;
+    up.d = projected;
+    down = up;
+    down.codes = down_codes;
+    down.codes_size = (size_t)experts * model * hidden * (size_t)bits / 8;
+    down.scales = down_scales;
+    down.correction = down_biases ? SO_CORR_BIASES : SO_CORR_SYMMETRIC;
+    down.correction_data = down_biases;
+    down.row_count = experts * model;
+    down.group_count = hidden / group_size;
+    down.n = model;
+    down.k = hidden;
+    down.gather_indices = down_ids;
+    down.a = activated;
+    down.d = down_out;
+    for (uint32_t row = 0; row < rows && status == 0; ++row) {
+        for (uint32_t rank = 0; rank < active && status == 0; ++rank) {
+            const uint32_t route = row * active + rank;
+            so_moe_gather_rows(ids, up_ids, route, 2 * hidden, experts, 2 * hidden);
+            up.a = input + (size_t)row * model;
+            status = so_matmul(&up);
+            if (status) break;
+            so_gated_silu_bf16(projected, activated, hidden, 1);
+            so_moe_gather_rows(ids, down_ids, route, model, experts, model);
+            status = so_matmul(&down);
+            if (status) break;
+            so_moe_accumulate(down_out, weights, accumulator, output, model, route, row * model, rank == 0,
+                              rank + 1 == active, round_products, round_accumulator);
+        }
+    }
+    free(ids); free(weights); free(accumulator); free(up_ids); free(down_ids);
+    free(projected); free(activated); free(down_out); free(unit);
+    return status;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Test-input generators. Parity is defined on decode of the packed bytes, so */
 /* these only need to produce valid encodings.                                */

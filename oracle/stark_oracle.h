@@ -81,6 +81,20 @@ int so_matmul(const so_matmul_args* args);
 /* Row-parallel variant (OpenMP over output columns); identical arithmetic per output. */
 int so_matmul_parallel(const so_matmul_args* args, int threads);
 
+/* encodable_block/mlp/routed.rs:154-257 (RoutedExperts::encode_scaled): route
+ * (moe.rs:24-85), optional adjust (moe.rs:147-184; unit gains when only
+ * sort_ids is set, routed.rs:205-208), then per (row, rank) in order: gathered
+ * up product [2*hidden] (bf16 out), gated SiLU, gathered down product [model]
+ * (bf16 out), accumulate (moe.rs:109-145). Banks are MLX affine with planes in
+ * `plane_dt`; biases NULL selects the symmetric correction. Returns so_matmul's
+ * status (0 ok). */
+int so_routed_experts(const uint16_t* input, const float* logits, const float* expert_scales,
+                      const uint8_t* up_codes, const void* up_scales, const void* up_biases,
+                      const uint8_t* down_codes, const void* down_scales, const void* down_biases, int layout,
+                      int bits, uint32_t group_size, int plane_dt, uint32_t rows, uint32_t model, uint32_t hidden,
+                      uint32_t experts, uint32_t active, int round_logits, int round_weights, int round_products,
+                      int round_accumulator, int sort_ids, uint16_t* output);
+
 /* backends/cpu/kernel/matmul/vision.rs:249-336 (BF16-effective reference dot). */
 void so_reference_affine_linear_bf16(const uint16_t* input, const uint8_t* weights, const uint16_t* scales,
                                      const uint16_t* biases, const uint32_t* indices, uint16_t* bf16_output,

@@ -11,7 +11,8 @@ QMM_DEVICE float round_bf16(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(
 // MoeRoute (moe.rs:23-85): one wave per token row, experts striped over lanes.
 // Top-k is a repeated argmax where a strictly greater value wins and ties go to
 // the lowest expert id (moe.rs:61-66). The softmax denominator is a wave
-// reduction (the reference sums sequentially; weights agree to rounding).
+// reduction and exp is the device expf (the reference sums sequentially with
+// the platform's libm exp): ids are exact, weights agree to a few ulp.
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, uint32_t* ids, float* weights,
                                                         uint32_t rows, uint32_t experts, uint32_t active,
                                                         uint32_t round_weights, uint32_t round_logits) {
@@ -92,7 +93,7 @@ __global__ void moe_adjust_kernel(uint32_t* ids, float* weights, const float* sc
     const size_t base = (size_t)row * active;
     for (uint32_t r = 0; r < active; ++r) {
         const uint32_t id = ids[base + r];
-        weights[base + r] = id < experts ? weights[base + r] * scales[id] : __builtin_nanf("");
+        weights[base + r] = id < experts ? weights[base + r] * (scales ? scales[id] : 1.0f) : __builtin_nanf("");
     }
     if (sort_ids) {
         for (uint32_t r = 1; r < active; ++r) {
@@ -138,6 +139,17 @@ __global__ void moe_accumulate_kernel(const uint16_t* input, const float* weight
 }
 
 }  // namespace
+
+// Adjust with optional gains: NULL scales stand for the unit gains the
+// reference allocates when only the id sort is requested (routed.rs:205-208).
+stark_qmm_status launch_moe_adjust(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
+                                   uint32_t experts, uint32_t active, uint32_t sort_ids, hipStream_t stream) {
+    if (rows == 0) return STARK_QMM_OK;
+    hipLaunchKernelGGL(moe_adjust_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream, ids, weights, scales, rows,
+                       experts, active, sort_ids);
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
 
 }  // namespace qmm
 
@@ -189,21 +201,6 @@ stark_qmm_status stark_qmm_moe_accumulate(const void* input, const float* weight
                        output_offset, initialize, finalize, round_product, round_accumulator);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
-}
-
-}  // extern "C"
-
-extern "C" {
-
-uint64_t stark_qmm_routed_experts_workspace_size(uint32_t rows, uint32_t model, uint32_t hidden, uint32_t experts,
-                                                 uint32_t active) {
-    (void)rows; (void)model; (void)hidden; (void)experts; (void)active;
-    return 0;
-}
-
-stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* args, void* stream) {
-    (void)args; (void)stream;
-    return STARK_QMM_UNSUPPORTED;
 }
 
 }  // extern "C"

@@ -1,0 +1,394 @@
+// Routed experts (RoutedExperts::encode_scaled,
+// crates/stark-engine/src/encodable_block/mlp/routed.rs:154-257) as one device
+// pipeline with expert compaction:
+//
+//   1. route (moe.hip) and, when asked, adjust the routes;
+//   2. compaction (one workgroup): a counting sort of the routes by expert,
+//      cut into slots of at most 16 routes of one expert, each slot filed in a
+//      list by its route count class (1, 2, 3-4, 5-8, 9-16). The counting-sort
+//      idea follows vendor/lily-core/src/kernels/metal/moe.metal:905-1036;
+//   3. grouped up product per class: every slot streams its expert's
+//      [value | gate] rows once for all its routes (matrix-core tile with the
+//      8 value rows and the matching 8 gate rows of the expert), rounds both to
+//      bf16 and applies the gated SiLU in the epilogue (gated_act_mul semantics);
+//   4. grouped down product per class: bf16 result per route;
+//   5. weighted accumulation over the ranks of each token in rank order, with
+//      the reference's rounding switches (moe.rs:109-145).
+//
+// The numerics per (token, rank) are those of the reference's loop: products
+// rounded to bf16 where LinearMatmul writes bf16, the gate on bf16 inputs, and
+// accumulation in rank order. Compaction changes only which workgroup computes
+// a route; each output value of the matrix-core tile depends on its own
+// activation row alone.
+#include <cmath>
+
+#include "mfma_tile.h"
+
+namespace qmm {
+
+namespace {
+
+using namespace mfma;
+
+constexpr uint32_t kSlotRoutes = 16;
+constexpr int kClasses = 5;
+
+__device__ __host__ inline uint32_t count_class(uint32_t c) {
+    return c <= 1 ? 0 : c <= 2 ? 1 : c <= 4 ? 2 : c <= 8 ? 3 : 4;
+}
+
+// Workspace carve-up (byte offsets, 256-aligned).
+struct RoutedLayout {
+    uint64_t ids, weights, sorted, slots, lists, header, act, proj, total;
+    uint32_t routes, max_slots;
+};
+
+RoutedLayout routed_layout(uint32_t rows, uint32_t model, uint32_t hidden, uint32_t experts, uint32_t active) {
+    RoutedLayout L{};
+    const uint64_t routes = (uint64_t)rows * active;
+    L.routes = (uint32_t)routes;
+    L.max_slots = (uint32_t)(std::min<uint64_t>(experts, routes) + (routes + kSlotRoutes - 1) / kSlotRoutes);
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const uint64_t at = off;
+        off += (bytes + 255) / 256 * 256;
+        return at;
+    };
+    L.ids = take(4 * routes);
+    L.weights = take(4 * routes);
+    L.sorted = take(4 * routes);
+    L.slots = take(16ull * L.max_slots);
+    L.lists = take(4ull * kClasses * L.max_slots);
+    L.header = take(4 * 8);
+    L.act = take(2 * routes * hidden);
+    L.proj = take(2 * routes * model);
+    L.total = off;
+    return L;
+}
+
+// ---- 2. compaction: one workgroup of 1024 threads, one thread per expert id.
+__global__ __launch_bounds__(1024) void moe_compact(const uint32_t* ids, uint32_t routes, uint32_t experts,
+                                                    uint32_t max_slots, uint32_t* sorted, uint32_t* slots,
+                                                    uint32_t* lists, uint32_t* header) {
+    __shared__ uint32_t cnt[1024], fill[1024], off[1024], soff[1024], wsum[2][16], ccount[kClasses];
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    cnt[t] = 0;
+    fill[t] = 0;
+    if (t < kClasses) ccount[t] = 0;
+    __syncthreads();
+    for (uint32_t r = t; r < routes; r += 1024) {
+        uint32_t e = ids[r];
+        e = e < experts ? e : 0;  // out-of-range ids read expert 0's rows (MoeGatherRows, moe.rs:87-107)
+        atomicAdd(&cnt[e], 1u);
+    }
+    __syncthreads();
+    // exclusive scans of the route counts and of the slot counts over experts
+    const uint32_t c = cnt[t], ns = (c + kSlotRoutes - 1) / kSlotRoutes;
+    uint32_t ic = c, is = ns;
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+        const uint32_t uc = __shfl_up(ic, d, 64), us = __shfl_up(is, d, 64);
+        if (lane >= d) {
+            ic += uc;
+            is += us;
+        }
+    }
+    if (lane == 63) {
+        wsum[0][wave] = ic;
+        wsum[1][wave] = is;
+    }
+    __syncthreads();
+    uint32_t pc = 0, ps = 0;
+    for (uint32_t w = 0; w < wave; ++w) {
+        pc += wsum[0][w];
+        ps += wsum[1][w];
+    }
+    off[t] = pc + ic - c;
+    soff[t] = ps + is - ns;
+    __syncthreads();
+    for (uint32_t r = t; r < routes; r += 1024) {
+        uint32_t e = ids[r];
+        e = e < experts ? e : 0;
+        sorted[off[e] + atomicAdd(&fill[e], 1u)] = r;
+    }
+    for (uint32_t s = 0; s < ns; ++s) {
+        const uint32_t slot = soff[t] + s, n = min(kSlotRoutes, c - s * kSlotRoutes);
+        slots[4 * slot + 0] = t;
+        slots[4 * slot + 1] = off[t] + s * kSlotRoutes;
+        slots[4 * slot + 2] = n;
+        slots[4 * slot + 3] = 0;
+        const uint32_t cl = count_class(n);
+        lists[cl * max_slots + atomicAdd(&ccount[cl], 1u)] = slot;
+    }
+    __syncthreads();
+    if (t < kClasses) header[t] = ccount[t];
+}
+
+// Launch record of a grouped product, read through the kernarg segment.
+struct GroupedLaunch {
+    AffineOp op;             // the bank: codes, planes, activation base, k, group, strides
+    const uint32_t* slots;   // [max_slots][4] expert, first sorted position, routes
+    const uint32_t* list;    // slot ids of this class
+    const uint32_t* header;  // per-class slot counts
+    const uint32_t* sorted;  // route ids in expert order
+    uint16_t* out;           // up: act [routes][hidden]; down: proj [routes][model]
+    uint32_t cls, tiles, active, hidden, model;
+    uint32_t nib_mask, nib_one;
+};
+
+// silu(gate) * value in bf16 steps (gated_act_mul; SiLU as
+// src/backends/common/gpu_types/activation_type.rs:35-46)
+__device__ __forceinline__ uint16_t gated_silu(float value_f, float gate_f) {
+    const float v = bf16_bits_to_f32(f32_to_bf16_bits(value_f));
+    const float x = bf16_bits_to_f32(f32_to_bf16_bits(gate_f));
+    const float y = x / (1.0f + expf(-1.0f * x));
+    const float a = bf16_bits_to_f32(f32_to_bf16_bits(y));
+    return f32_to_bf16_bits(v * a);
+}
+
+// ---- 3. grouped up product + gated SiLU. Work item = (slot, tile of 8 value rows).
+template <int MP, int MB, bool SIGNED, bool BIASED, bool BF>
+__global__ __launch_bounds__(kWg) void moe_up_mfma(GroupedLaunch launch) {
+    (void)launch;
+    __shared__ MfmaLds<MP, MB> lds;
+    const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
+    const uint32_t items = L->header[L->cls] * L->tiles;
+    const uint32_t H = L->hidden, A = L->active, model = L->model;
+    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+        const uint32_t slot = L->list[item / L->tiles], t = item % L->tiles;
+        const uint32_t e = L->slots[4 * slot], begin = L->slots[4 * slot + 1], cnt = L->slots[4 * slot + 2];
+        const uint32_t nA = e * 2 * H + 8 * t, nB = nA + H;
+        const uint32_t* routes = L->sorted + begin;
+        mfma_tile<MP, MB, SIGNED, BIASED, BF>(
+            L->op, nA, nB, cnt, [&](uint32_t m) { return (size_t)(routes[m] / A) * model; }, lds, L->nib_mask,
+            L->nib_one);
+        for (uint32_t q = threadIdx.x; q < (uint32_t)MP * MB * 8; q += kWg) {
+            const uint32_t m = q / 8, i = q % 8;
+            if (m >= cnt) continue;
+            const float v = (lds.red[0][m][i] + lds.red[1][m][i]) + (lds.red[2][m][i] + lds.red[3][m][i]);
+            const float g = (lds.red[0][m][8 + i] + lds.red[1][m][8 + i]) +
+                            (lds.red[2][m][8 + i] + lds.red[3][m][8 + i]);
+            L->out[(size_t)routes[m] * H + 8 * t + i] = gated_silu(v, g);
+        }
+        __syncthreads();  // lds.red is rewritten by the next item
+    }
+}
+
+// ---- 4. grouped down product. Work item = (slot, tile of 16 output rows).
+template <int MP, int MB, bool SIGNED, bool BIASED, bool BF>
+__global__ __launch_bounds__(kWg) void moe_down_mfma(GroupedLaunch launch) {
+    (void)launch;
+    __shared__ MfmaLds<MP, MB> lds;
+    const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
+    const uint32_t items = L->header[L->cls] * L->tiles;
+    const uint32_t H = L->hidden, model = L->model;
+    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+        const uint32_t slot = L->list[item / L->tiles], t = item % L->tiles;
+        const uint32_t e = L->slots[4 * slot], begin = L->slots[4 * slot + 1], cnt = L->slots[4 * slot + 2];
+        const uint32_t nA = e * model + 16 * t;
+        const uint32_t* routes = L->sorted + begin;
+        mfma_tile<MP, MB, SIGNED, BIASED, BF>(
+            L->op, nA, nA + 8, cnt, [&](uint32_t m) { return (size_t)routes[m] * H; }, lds, L->nib_mask,
+            L->nib_one);
+        for (uint32_t q = threadIdx.x; q < (uint32_t)MP * MB * kRows; q += kWg) {
+            const uint32_t m = q / kRows, r = q % kRows;
+            if (m >= cnt) continue;
+            const float v = (lds.red[0][m][r] + lds.red[1][m][r]) + (lds.red[2][m][r] + lds.red[3][m][r]);
+            L->out[(size_t)routes[m] * model + 16 * t + r] = f32_to_bf16_bits(v);
+        }
+        __syncthreads();
+    }
+}
+
+// ---- 5. accumulation over ranks in order (moe.rs:109-145 applied rank 0..k-1).
+__global__ void moe_accumulate_ranks(const uint16_t* proj, const float* weights, uint16_t* output, uint32_t model,
+                                     uint32_t active, uint32_t round_product, uint32_t round_accumulator) {
+    const uint32_t row = blockIdx.y, p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= model) return;
+    float acc = 0.0f;
+    for (uint32_t rank = 0; rank < active; ++rank) {
+        const uint32_t route = row * active + rank;
+        float product = bf16_bits_to_f32(proj[(size_t)route * model + p]) * weights[route];
+        if (round_product) product = bf16_bits_to_f32(f32_to_bf16_bits(product));
+        float value = (rank == 0 ? 0.0f : acc) + product;
+        if (round_accumulator) value = bf16_bits_to_f32(f32_to_bf16_bits(value));
+        acc = value;
+    }
+    output[(size_t)row * model + p] = f32_to_bf16_bits(acc);
+}
+
+#define QMM_GROUPED_KERNEL(NAME)                                                                  \
+    template <int MP, int MB, bool SG, bool BI, bool BF>                                          \
+    struct NAME##_k {                                                                             \
+        static void* fn() { return (void*)&NAME<MP, MB, SG, BI, BF>; }                            \
+    };
+QMM_GROUPED_KERNEL(moe_up_mfma)
+QMM_GROUPED_KERNEL(moe_down_mfma)
+#undef QMM_GROUPED_KERNEL
+
+template <template <int, int, bool, bool, bool> class K, int MP, int MB>
+void* pick(bool sg, bool bi, bool bf) {
+    if (sg) {
+        if (bi) return bf ? K<MP, MB, true, true, true>::fn() : K<MP, MB, true, true, false>::fn();
+        return bf ? K<MP, MB, true, false, true>::fn() : K<MP, MB, true, false, false>::fn();
+    }
+    if (bi) return bf ? K<MP, MB, false, true, true>::fn() : K<MP, MB, false, true, false>::fn();
+    return bf ? K<MP, MB, false, false, true>::fn() : K<MP, MB, false, false, false>::fn();
+}
+
+template <template <int, int, bool, bool, bool> class K>
+void* pick_class(int cls, bool sg, bool bi, bool bf) {
+    switch (cls) {
+    case 0: return pick<K, 1, 1>(sg, bi, bf);
+    case 1: return pick<K, 2, 1>(sg, bi, bf);
+    case 2: return pick<K, 4, 1>(sg, bi, bf);
+    case 3: return pick<K, 8, 1>(sg, bi, bf);
+    default: return pick<K, 8, 2>(sg, bi, bf);
+    }
+}
+
+// Largest number of slots a class can hold: an expert receives at most one
+// route per token, and a slot of class c holds at least lo(c) routes.
+uint32_t class_slot_bound(int cls, uint32_t routes, uint32_t experts, uint32_t max_slots) {
+    static const uint32_t lo[kClasses] = {1, 2, 3, 5, 9};
+    return std::min<uint32_t>(std::min<uint32_t>(max_slots, routes / lo[cls]), cls == 4 ? max_slots : experts);
+}
+
+AffineOp bank_op(const stark_qmm_b& b, uint32_t rows, uint32_t k, const void* x) {
+    AffineOp o{};
+    o.codes = (const uint8_t*)b.codes;
+    o.scales = b.scales;
+    o.corr = b.correction_data;
+    o.x = x;
+    o.n = rows;
+    o.k = k;
+    o.m = 1;
+    if (b.params.layout == STARK_QMM_LAYOUT_OUTPUT_GROUP) {
+        o.os = b.params.group_count;
+        o.gs = 1;
+    } else {
+        o.os = 1;
+        o.gs = (b.params.row_count + 3u) / 4u * 4u;
+    }
+    o.group_size = b.group_size;
+    o.corr_kind = b.correction;
+    o.w_dt = STARK_QMM_BF16;
+    o.x_dt = STARK_QMM_BF16;
+    o.d_dt = STARK_QMM_BF16;
+    o.flags = b.signed_codes ? FLAG_SIGNED : 0u;
+    o.ab_scale = 1.0f;
+    return o;
+}
+
+// Bank accepted by the grouped matrix-core kernels.
+stark_qmm_status check_bank(const stark_qmm_b& b, uint64_t rows, uint32_t k, uint32_t max_count) {
+    if (!b.codes || !b.scales) return STARK_QMM_INVALID_ARGUMENT;
+    if (b.mode != STARK_QMM_MODE_U4) return STARK_QMM_UNSUPPORTED;
+    if (b.group_size != 32 && b.group_size != 64 && b.group_size != 128) return STARK_QMM_UNSUPPORTED_GROUP_SIZE;
+    if (b.correction == STARK_QMM_CORRECTION_ZERO_POINTS) return STARK_QMM_UNSUPPORTED;
+    if (b.correction == STARK_QMM_CORRECTION_BIASES && !b.correction_data) return STARK_QMM_INVALID_ARGUMENT;
+    if (b.params.materialize_affine_input_sum) return STARK_QMM_UNSUPPORTED;
+    if (b.params.row_count != rows || (uint64_t)b.params.group_count * b.group_size != k)
+        return STARK_QMM_UNSUPPORTED_LAYOUT;
+    if (rows * k / 2 > b.codes_size) return STARK_QMM_UNSUPPORTED_LAYOUT;
+    // the widest class in use must fit a step's groups into its slots (S = 16 / MP)
+    const uint32_t mp = max_count <= 1 ? 1 : max_count <= 2 ? 2 : max_count <= 4 ? 4 : 8;
+    if (16 / mp < 128 / b.group_size) return STARK_QMM_UNSUPPORTED_GROUP_SIZE;
+    if (((uintptr_t)b.codes | (uintptr_t)b.scales | (uintptr_t)b.correction_data) & 15) return STARK_QMM_UNSUPPORTED;
+    // group-output planes: the 16-byte metadata loads need 8-row aligned plane rows
+    if (b.params.layout == STARK_QMM_LAYOUT_GROUP_OUTPUT && ((rows + 3) / 4 * 4) % 8)
+        return STARK_QMM_UNSUPPORTED_LAYOUT;
+    return STARK_QMM_OK;
+}
+
+}  // namespace
+
+}  // namespace qmm
+
+using namespace qmm;
+
+extern "C" {
+
+uint64_t stark_qmm_routed_experts_workspace_size(uint32_t rows, uint32_t model, uint32_t hidden, uint32_t experts,
+                                                 uint32_t active) {
+    return routed_layout(rows, model, hidden, experts, active).total;
+}
+
+stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* stream_ptr) {
+    if (!a || a->struct_size != sizeof(stark_qmm_routed_args)) return STARK_QMM_ABI_MISMATCH;
+    const uint32_t R = a->rows, model = a->model, H = a->hidden, E = a->experts, A = a->active;
+    // geometry accepted by RoutedExperts::new / encode_scaled (routed.rs:62-73, 162-170)
+    if (R == 0 || R > 1024 || E == 0 || E > 1024 || A == 0 || A > 32 || A > E || model == 0 || model > 16384 ||
+        H == 0 || H > 131072)
+        return STARK_QMM_INVALID_ARGUMENT;
+    if (!a->input || !a->router_logits || !a->output || !a->workspace) return STARK_QMM_INVALID_ARGUMENT;
+    if (model % 64 || H % 64) return STARK_QMM_UNSUPPORTED_LAYOUT;  // K of both products, 16-row tiles
+    if (((uintptr_t)a->input | (uintptr_t)a->workspace) & 15) return STARK_QMM_UNSUPPORTED;
+    const RoutedLayout Lw = routed_layout(R, model, H, E, A);
+    if (a->workspace_size < Lw.total) return STARK_QMM_WORKSPACE_TOO_SMALL;
+    const uint32_t max_count = std::min<uint32_t>(R, kSlotRoutes);
+    stark_qmm_status st = check_bank(a->up, (uint64_t)E * 2 * H, model, max_count);
+    if (st != STARK_QMM_OK) return st;
+    st = check_bank(a->down, (uint64_t)E * model, H, max_count);
+    if (st != STARK_QMM_OK) return st;
+    if (a->up.signed_codes != a->down.signed_codes || a->up.correction != a->down.correction)
+        return STARK_QMM_UNSUPPORTED;
+
+    hipStream_t stream = (hipStream_t)stream_ptr;
+    uint8_t* ws = (uint8_t*)a->workspace;
+    uint32_t* ids = (uint32_t*)(ws + Lw.ids);
+    float* weights = (float*)(ws + Lw.weights);
+    uint32_t* sorted = (uint32_t*)(ws + Lw.sorted);
+    uint32_t* slots = (uint32_t*)(ws + Lw.slots);
+    uint32_t* lists = (uint32_t*)(ws + Lw.lists);
+    uint32_t* header = (uint32_t*)(ws + Lw.header);
+    uint16_t* act = (uint16_t*)(ws + Lw.act);
+    uint16_t* proj = (uint16_t*)(ws + Lw.proj);
+
+    // 1. route (+ adjust), as routed.rs:188-209
+    st = stark_qmm_moe_route(a->router_logits, ids, weights, R, E, A, a->round_weights_bf16, a->round_logits_bf16,
+                             stream);
+    if (st != STARK_QMM_OK) return st;
+    if (a->expert_scales || a->sort_expert_ids)
+        st = launch_moe_adjust(ids, weights, a->expert_scales, R, E, A, a->expert_scales ? a->sort_expert_ids : 1,
+                               stream);
+    if (st != STARK_QMM_OK) return st;
+    // 2. compaction
+    hipLaunchKernelGGL(moe_compact, dim3(1), dim3(1024), 0, stream, ids, Lw.routes, E, Lw.max_slots, sorted, slots,
+                       lists, header);
+    QMM_HIP_CHECK(hipGetLastError());
+    // 3./4. grouped products, one launch per route-count class in use
+    const bool sg = a->up.signed_codes != 0, bi = a->up.correction == STARK_QMM_CORRECTION_BIASES, bf = true;
+    const int top = (int)count_class(max_count);
+    for (int pass = 0; pass < 2; ++pass) {
+        GroupedLaunch g{};
+        const bool up = pass == 0;
+        g.op = up ? bank_op(a->up, E * 2 * H, model, a->input) : bank_op(a->down, E * model, H, act);
+        g.slots = slots;
+        g.header = header;
+        g.sorted = sorted;
+        g.out = up ? act : proj;
+        g.tiles = up ? H / 8 : model / 16;
+        g.active = A;
+        g.hidden = H;
+        g.model = model;
+        g.nib_mask = 0x000F000Fu;
+        g.nib_one = 0x3F803F80u;
+        for (int c = 0; c <= top; ++c) {
+            g.cls = (uint32_t)c;
+            g.list = lists + (size_t)c * Lw.max_slots;
+            const uint64_t items = (uint64_t)class_slot_bound(c, Lw.routes, E, Lw.max_slots) * g.tiles;
+            if (items == 0) continue;
+            const uint32_t grid = (uint32_t)std::min<uint64_t>(items, 4096);
+            void* fn = up ? pick_class<moe_up_mfma_k>(c, sg, bi, bf) : pick_class<moe_down_mfma_k>(c, sg, bi, bf);
+            void* argv[] = {&g};
+            QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(grid), dim3(kWg), argv, 0, stream));
+        }
+    }
+    // 5. accumulate ranks in order
+    hipLaunchKernelGGL(moe_accumulate_ranks, dim3((model + 255) / 256, R), dim3(256), 0, stream, proj, weights,
+                       (uint16_t*)a->output, model, A, a->round_products_bf16, a->round_accumulator_bf16);
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
+
+}  // extern "C"

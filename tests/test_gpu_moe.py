@@ -1,0 +1,145 @@
+"""GPU parity of the MoE kernels (moe.rs:24-184 restated in the oracle) and of
+the fused routed-experts pipeline (routed.rs:154-257) through the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+from tests import helpers as H
+from tests import moe_cases as MC
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,experts,active,rw,rl", [(1, 128, 8, False, False), (16, 128, 8, True, False),
+                                                      (7, 64, 4, False, True), (33, 1024, 32, True, True),
+                                                      (4, 8, 8, False, False)])
+def test_route(qmm, oracle, rows, experts, active, rw, rl):
+    rng = np.random.default_rng(rows * experts + active)
+    logits = rng.normal(0, 2, rows * experts).astype(np.float32)
+    logits[: experts // 2] = logits[experts // 2: experts]  # exact ties: the lower id wins
+    want_ids, want_w = oracle.moe_route(logits, rows, experts, active, rw, rl)
+    ids, w = qmm.moe_route(H.to_dev(logits), rows, experts, active, rw, rl)
+    torch.cuda.synchronize()
+    # ids depend only on comparisons of the (optionally bf16-rounded) logits: exact
+    assert np.array_equal(H.from_dev(ids, np.uint32), want_ids)
+    # weights go through expf and the softmax denominator, whose last bits are
+    # libm's (the reference's own f32::exp is the platform's): a few f32 ulp, or
+    # one bf16 ulp once rounded to bf16
+    got_w = H.from_dev(w, np.float32)
+    rtol = 2.0 ** -7 if rw else 4e-7 * 8
+    assert np.allclose(got_w, want_w, rtol=rtol, atol=0)
+
+
+@pytest.mark.parametrize("sort_ids", [False, True])
+def test_adjust_exact(qmm, oracle, sort_ids):
+    rng = np.random.default_rng(5)
+    rows, E, A = 9, 16, 5
+    ids = np.stack([rng.permutation(E)[:A] for _ in range(rows)]).astype(np.uint32).ravel()
+    ids[3] = E + 2  # out of range: weight becomes NaN
+    w = rng.uniform(0, 1, rows * A).astype(np.float32)
+    g = rng.uniform(0.5, 2, E).astype(np.float32)
+    di, dw = H.to_dev(ids), H.to_dev(w.copy())
+    qmm.moe_adjust_routes(di, dw, H.to_dev(g), rows, E, A, sort_ids)
+    oracle.moe_adjust_routes(ids, w, g, rows, E, A, sort_ids)
+    torch.cuda.synchronize()
+    assert np.array_equal(H.from_dev(di, np.uint32), ids)
+    assert np.array_equal(H.from_dev(dw, np.float32).view(np.uint32), w.view(np.uint32))
+
+
+def test_gather_and_accumulate_exact(qmm, oracle):
+    rng = np.random.default_rng(11)
+    ids = np.array([3, 1, 7, 99], np.uint32)
+    for route in range(4):
+        want = oracle.moe_gather_rows(ids, route, 24, 8, 24)
+        got = qmm.moe_gather_rows(H.to_dev(ids), route, 24, 8, 24)
+        assert np.array_equal(H.from_dev(got, np.uint32), want)
+    L = 300
+    inp = oracle.f32_to_bf16(rng.normal(0, 1, L).astype(np.float32))
+    wts = rng.uniform(0, 1, 4).astype(np.float32)
+    for flags in [(1, 0, 0, 0), (0, 1, 1, 0), (0, 1, 0, 1), (1, 1, 1, 1)]:
+        init, fin, rp, ra = flags
+        acc = rng.normal(0, 1, L + 10).astype(np.float32)
+        out = np.zeros(L + 10, np.uint16)
+        da, do = H.to_dev(acc.copy()), H.to_dev(out.copy())
+        qmm.moe_accumulate(H.to_dev(inp), H.to_dev(wts), da, do, L, 2, 10, init, fin, rp, ra)
+        oracle.moe_accumulate(inp, wts, acc, out, L, 2, 10, init, fin, rp, ra)
+        torch.cuda.synchronize()
+        assert np.array_equal(H.from_dev(da, np.float32).view(np.uint32), acc.view(np.uint32))
+        assert np.array_equal(H.from_dev(do, np.uint16), out)
+
+
+def routed_check(qmm, O, c, **flags):
+    R, M, Hd, E, A = c["rows"], c["model"], c["hidden"], c["experts"], c["active"]
+    want = O.bf16_to_f32(O.routed_experts(c["x"], c["logits"], c["up"], c["down"], R, M, Hd, E, A,
+                                          expert_scales=c["scales"], layout=c["layout"], group=c["group"],
+                                          round_logits=flags.get("rl", False), round_weights=flags.get("rw", False),
+                                          round_products=flags.get("rp", False),
+                                          round_accumulator=flags.get("ra", False),
+                                          sort_ids=flags.get("si", False)))
+    corr = qmm.BIASES if c["up"]["biases"] is not None else qmm.SYMMETRIC
+
+    def qb(b, rows, cols):
+        return qmm.QuantizedB(codes=H.to_dev(b["codes"]), scales=H.to_dev(b["scales"]), correction=corr,
+                              correction_data=None if b["biases"] is None else H.to_dev(b["biases"]),
+                              params=qmm.QuantParams(c["layout"], rows, cols // c["group"]),
+                              group_size=c["group"])
+
+    out = qmm.routed_experts(H.to_dev(c["x"]), H.to_dev(c["logits"]), qb(c["up"], E * 2 * Hd, M),
+                             qb(c["down"], E * M, Hd), R, M, Hd, E, A,
+                             expert_scales=None if c["scales"] is None else H.to_dev(c["scales"]),
+                             round_logits=flags.get("rl", False), round_weights=flags.get("rw", False),
+                             round_products=flags.get("rp", False), round_accumulator=flags.get("ra", False),
+                             sort_expert_ids=flags.get("si", False))
+    torch.cuda.synchronize()
+    got = O.bf16_to_f32(H.from_dev(out.view(torch.int16), np.uint16))
+    # Each (token, rank) passes through bf16 roundings of the up product, the
+    # gate and the down product; a sum that lands on the other side of a bf16
+    # rounding boundary moves one ulp and propagates. Bound: 2 bf16 ulp of the
+    # value + 1e-2 relative + 5e-3 of the row's largest output.
+    want2, got2 = want.reshape(R, M), got.reshape(R, M)
+    scale = np.abs(want2).max(axis=1, keepdims=True)
+    tol = 2 * np.abs(want2) * 2.0 ** -8 + 1e-2 * np.abs(want2) + 5e-3 * scale + 1e-6
+    bad = np.abs(got2 - want2) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance; worst {np.abs(got2 - want2).max()}"
+    # and the bulk is exact or one ulp off
+    close = np.abs(got2 - want2) <= np.abs(want2) * 2.0 ** -7 + 1e-30
+    assert close.mean() > 0.9
+    return got, want
+
+
+@pytest.mark.parametrize("rows", [1, 3, 16, 40])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_routed_experts_pipeline(qmm, oracle, rows, layout):
+    """Qwen3-MoE-like geometry at reduced size: every route-count class, GO and
+    OG planes, rows > 16 (experts split into several slots)."""
+    c = MC.case(oracle, 100 + rows + 7 * layout, rows, model=256, hidden=128, experts=16, active=4, layout=layout)
+    routed_check(qmm, oracle, c)
+
+
+@pytest.mark.parametrize("biased,gains,flags", [(False, False, dict(rp=True, ra=True)),
+                                                (True, True, dict(si=True, rw=True)),
+                                                (True, False, dict(si=True, rl=True))])
+def test_routed_experts_options(qmm, oracle, biased, gains, flags):
+    c = MC.case(oracle, 55, 6, model=256, hidden=128, experts=8, active=3, biased=biased, gains=gains)
+    routed_check(qmm, oracle, c, **flags)
+
+
+def test_routed_experts_qwen3_moe_geometry(qmm, oracle):
+    """Config-3 widths (H=2048, I=768, E=128, top-8) at one token."""
+    c = MC.case(oracle, 9, 1, model=2048, hidden=768, experts=128, active=8)
+    routed_check(qmm, oracle, c)
+
+
+def test_routed_experts_rejections(qmm, oracle):
+    c = MC.case(oracle, 1, 2, model=256, hidden=128, experts=8, active=2)
+    b = qmm.QuantizedB(codes=H.to_dev(c["up"]["codes"]), scales=H.to_dev(c["up"]["scales"]),
+                       correction_data=H.to_dev(c["up"]["biases"]), params=qmm.QuantParams(1, 8 * 256, 256 // 64))
+    d = qmm.QuantizedB(codes=H.to_dev(c["down"]["codes"]), scales=H.to_dev(c["down"]["scales"]),
+                       correction_data=H.to_dev(c["down"]["biases"]), params=qmm.QuantParams(1, 8 * 256, 128 // 64))
+    x, lg = H.to_dev(c["x"]), H.to_dev(c["logits"])
+    with pytest.raises(qmm.MatmulError) as e:
+        qmm.routed_experts(x, lg, b, d, 2, 256, 128, 8, 2, workspace=torch.empty(16, dtype=torch.uint8,
+                                                                                  device="cuda"))
+    assert e.value.status == qmm.WORKSPACE_TOO_SMALL
+    with pytest.raises(qmm.MatmulError):
+        qmm.routed_experts(x, lg, b, d, 2, 256, 128, 8, 9)  # active > experts
