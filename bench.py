@@ -55,6 +55,69 @@ def quantize_gpu(w, group=GROUP):
     return codes, s.t().contiguous().view(torch.int16), b.t().contiguous().view(torch.int16)
 
 
+def quantize_gpu_bits(torch, w, bits, group=GROUP):
+    """MLX affine at `bits` (4 or 8) by the BASELINE rule: scale=(max-min)/(2^bits-1),
+    bias=min as bf16; codes little-endian (low nibble first for 4-bit)."""
+    if bits == 4:
+        return quantize_gpu(w, group)
+    n, k = w.shape
+    g = w.view(n, k // group, group)
+    mn, mx = g.amin(dim=2), g.amax(dim=2)
+    s = ((mx - mn) / 255.0).to(torch.bfloat16)
+    b = mn.to(torch.bfloat16)
+    sf, bf = s.float().unsqueeze(2), b.float().unsqueeze(2)
+    q = torch.where(sf > 0, torch.round((g - bf) / torch.where(sf > 0, sf, torch.ones_like(sf))),
+                    torch.zeros_like(g)).clamp(0, 255).to(torch.uint8).view(n, k).contiguous()
+    return q, s.t().contiguous().view(torch.int16), b.t().contiguous().view(torch.int16)
+
+
+def quantize_gguf_gpu(torch, w, kind):
+    """GGUF blocks for row-major w [N, K] (data generation on the GPU):
+    Q8_0: d = amax/127 (f16), q = round(x/d) int8, 34-byte blocks;
+    Q4_K: per 32-value sub-block scale (max-min)/15 and min, quantised to 6 bits
+    against the super-block's d/dmin (f16), 144-byte super-blocks laid out as
+    ggml's block_q4_K (d, dmin, 12 packed scale/min bytes, 128 nibble bytes)."""
+    n, k = w.shape
+    if kind == 8:
+        g = w.view(n, k // 32, 32)
+        d = (g.abs().amax(dim=2) / 127.0).to(torch.float16)
+        df = d.float().unsqueeze(2)
+        q = torch.where(df > 0, torch.round(g / torch.where(df > 0, df, torch.ones_like(df))),
+                        torch.zeros_like(g)).clamp(-127, 127).to(torch.int8)
+        out = torch.empty(n, k // 32, 34, dtype=torch.uint8, device=w.device)
+        out[:, :, 0:2] = d.view(torch.uint8).view(n, k // 32, 2)
+        out[:, :, 2:] = q.view(torch.uint8)
+        return out.view(-1)
+    g = w.view(n, k // 256, 8, 32)
+    mn = torch.clamp(g.amin(dim=3), max=0.0)
+    sc = (g.amax(dim=3) - mn) / 15.0
+    m = -mn
+    d = (sc.amax(dim=2) / 63.0).to(torch.float16)
+    dmin = (m.amax(dim=2) / 63.0).to(torch.float16)
+    dfl, dmf = d.float().unsqueeze(2), dmin.float().unsqueeze(2)
+    scq = torch.where(dfl > 0, torch.round(sc / torch.where(dfl > 0, dfl, torch.ones_like(dfl))),
+                      torch.zeros_like(sc)).clamp(0, 63)
+    mq = torch.where(dmf > 0, torch.round(m / torch.where(dmf > 0, dmf, torch.ones_like(dmf))),
+                     torch.zeros_like(m)).clamp(0, 63)
+    step = (dfl * scq).unsqueeze(3)
+    q = torch.where(step > 0, torch.round((g + (dmf * mq).unsqueeze(3)) / torch.where(step > 0, step, torch.ones_like(step))),
+                    torch.zeros_like(g)).clamp(0, 15).to(torch.int32)
+    sci, mi = scq.to(torch.int32), mq.to(torch.int32)
+    scales = torch.empty(n, k // 256, 12, dtype=torch.int32, device=w.device)
+    scales[..., 0:4] = (sci[..., 0:4] & 63) | ((sci[..., 4:8] >> 4) << 6)
+    scales[..., 4:8] = (mi[..., 0:4] & 63) | ((mi[..., 4:8] >> 4) << 6)
+    scales[..., 8:12] = (sci[..., 4:8] & 15) | ((mi[..., 4:8] & 15) << 4)
+    # element part*64 + half*32 + l sits in qs[part*32 + l] at shift 4*half (sub-block 2*part + half)
+    qv = q.view(n, k // 256, 4, 2, 32)
+    qs = (qv[:, :, :, 0, :] | (qv[:, :, :, 1, :] << 4)).reshape(n, k // 256, 128)
+    out = torch.empty(n, k // 256, 144, dtype=torch.uint8, device=w.device)
+    out[:, :, 0:2] = d.view(torch.uint8).view(n, k // 256, 2)
+    out[:, :, 2:4] = dmin.view(torch.uint8).view(n, k // 256, 2)
+    out[:, :, 4:16] = scales.to(torch.uint8)
+    out[:, :, 16:] = qs.to(torch.uint8)
+    return out.view(-1)
+
+
 def algorithmic_bytes(m=1):
     total = 0
     for _, n, k in SHAPES:
@@ -113,25 +176,8 @@ def copy_calibration(torch, mib=256):
     torch.cuda.synchronize()
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=360)
-    ap.add_argument("--warmup", type=int, default=72)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="also run a 256 MiB bitwise_not pass (byte-counter calibration under rocprofv3)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1).",
-              file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-    from stark_amd import qmm as Q
-    Q.lib()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
+def config1(args, torch, Q):
+    """Config 1: the Qwen3-8B W4 layer matvec set at M=1 (the headline line)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(SEED)
 
@@ -237,6 +283,169 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+def timed(torch, step, steps, warmup, stream):
+    """Warm up, then time `steps` calls of step(i) between two events on the
+    launch stream; also the mean of per-call event pairs. Returns ms per step."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(steps):
+        step(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def config2(args, torch, Q):
+    """Config 2: N=12288, K=4096 at M=1 and M=8 in MLX-affine 8-bit g64,
+    GGUF Q8_0 and GGUF Q4_K (one line each). Weights N(0,0.02) quantized by
+    each format's rule on the GPU; 8 rotating copies (> the 256 MB MALL)."""
+    N, K, copies = 12288, 4096, 8
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 2)
+    stream = torch.cuda.current_stream()
+    w = torch.randn(N, K, generator=gen, device="cuda") * 0.02
+    lines = []
+    for m in (1, 8):
+        x = torch.randn(m, K, generator=gen, device="cuda").to(torch.bfloat16)
+        # -- MLX affine 8-bit through MatmulKernel::encode
+        codes, sc, bi = quantize_gpu_bits(torch, w, 8)
+        mats = [(codes.clone(), sc.clone(), bi.clone()) for _ in range(copies)]
+        y = torch.empty(m * N, dtype=torch.int16, device="cuda")
+        kern = Q.MatmulKernel(Q.BF16, Q.BF16, Q.BF16)
+        batches = [kern.prepare_many([Q.MatmulArguments(
+            a=x.view(torch.int16), m=m, n=N, k=K, d=y,
+            b=Q.QuantizedB(codes=c, scales=s_, correction_data=b_, mode=Q.MODE_U8,
+                           params=Q.QuantParams(Q.GROUP_OUTPUT, N, K // GROUP)))]) for c, s_, b_ in mats]
+        ms = timed(torch, lambda i: kern.encode_prepared(batches[i % copies], stream), args.steps, args.warmup, stream)
+        nbytes = N * K + 2 * 2 * (K // GROUP) * N + m * 2 * K + m * 2 * N
+        lines.append(("mlx_affine_u8_g64", m, ms, nbytes))
+        del mats, batches
+        # -- GGUF Q8_0 / Q4_K through the hybrid operator (stream-ordered form)
+        xf = x.float().contiguous()
+        status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        for kind, name, block, bsize in ((Q.KIND_Q8_0, "gguf_q8_0", 32, 34), (Q.KIND_Q4_K, "gguf_q4_k", 256, 144)):
+            blocks = quantize_gguf_gpu(torch, w, kind)
+            views = [blocks.clone() for _ in range(copies)]
+            preps = []
+            for v in views:
+                op = Q.MappedOperation(matrices=[Q.MappedMatrix(codes=v)] * m, inputs=xf.view(-1), rows=N, columns=K,
+                                       format=("packed", kind))
+                preps.append(Q.mapped_prepare([op])[0])
+            ms = timed(torch, lambda i: Q.mapped_many_async(preps[i % copies], status, stream), args.steps,
+                       args.warmup, stream)
+            nbytes = N * (K // block) * bsize + m * 4 * K + m * 4 * N
+            lines.append((name, m, ms, nbytes))
+            del views, preps
+    for name, m, ms, nbytes in lines:
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": f"{name} matvec HBM GB/s", "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                          "dtype": "u8" if "u8" in name else "f32",
+                          "data": "synthetic: N(0,0.02) weights quantized by the format's rule, N(0,1) activations",
+                          "config": {"workload": f"config 2: {name} N={N} K={K} M={m}, {copies} rotating copies",
+                                     "bytes_per_step": nbytes, "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)},
+                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+
+
+def config3(args, torch, Q):
+    """Config 3: Qwen3-30B-A3B MoE layer decode: router 2048->128 bf16 matvec
+    (f32 logits), then stark_qmm_routed_experts (top-8 renormalised, expert
+    compaction, grouped W4 g64 gate/up + SiLU and down products, accumulate).
+    Tokens 1, 4, 16; 4 rotating layer copies (1.3 GB > the MALL)."""
+    Hm, E, I, A, copies = 2048, 128, 768, 8, 4
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 3)
+    stream = torch.cuda.current_stream()
+    layers = []
+    for _ in range(copies):
+        wr = (torch.randn(E, Hm, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        up = [quantize_gpu(torch.randn(2 * I, Hm, generator=gen, device="cuda") * 0.02) for _ in range(E)]
+        dn = [quantize_gpu(torch.randn(Hm, I, generator=gen, device="cuda") * 0.02) for _ in range(E)]
+        # banks: rows of every expert stacked; planes [G, rows] in group-output layout
+        ub = (torch.cat([u[0] for u in up]), torch.cat([u[1] for u in up], 1).contiguous(),
+              torch.cat([u[2] for u in up], 1).contiguous())
+        db = (torch.cat([d[0] for d in dn]), torch.cat([d[1] for d in dn], 1).contiguous(),
+              torch.cat([d[2] for d in dn], 1).contiguous())
+        del up, dn
+        layers.append((wr, ub, db))
+    per_expert = 2 * I * Hm // 2 + Hm * I // 2 + 2 * 2 * (Hm // GROUP) * 2 * I + 2 * 2 * (I // GROUP) * Hm
+    for T in (1, 4, 16):
+        x = torch.randn(T, Hm, generator=gen, device="cuda").to(torch.bfloat16)
+        logits = torch.empty(T * E, dtype=torch.float32, device="cuda")
+        out = torch.empty(T * Hm, dtype=torch.bfloat16, device="cuda")
+        rk = Q.MatmulKernel(Q.BF16, Q.BF16, Q.F32)
+        ws = torch.empty(Q.routed_experts_workspace_size(T, Hm, I, E, A), dtype=torch.uint8, device="cuda")
+        steps = []
+        uniq = []
+        for wr, ub, db in layers:
+            rb = rk.prepare_many([Q.MatmulArguments(a=x.view(torch.int16), m=T, n=E, k=Hm, d=logits,
+                                                    b=Q.FullPrecisionB(values=wr.view(torch.int16)))])
+            upb = Q.QuantizedB(codes=ub[0], scales=ub[1].view(-1), correction_data=ub[2].view(-1),
+                               params=Q.QuantParams(Q.GROUP_OUTPUT, E * 2 * I, Hm // GROUP))
+            dnb = Q.QuantizedB(codes=db[0], scales=db[1].view(-1), correction_data=db[2].view(-1),
+                               params=Q.QuantParams(Q.GROUP_OUTPUT, E * Hm, I // GROUP))
+            prep = Q.routed_experts(x.view(torch.int16), logits, upb, dnb, T, Hm, I, E, A, workspace=ws,
+                                    output=out, prepare_only=True)
+            steps.append((rb, prep))
+            rk.encode_prepared(rb, stream)
+            ids, _ = Q.moe_route(logits, T, E, A)
+            torch.cuda.synchronize()
+            uniq.append(len(set(ids.cpu().tolist())))
+
+        def step(i):
+            rb, prep = steps[i % copies]
+            rk.encode_prepared(rb, stream)
+            Q.routed_experts_prepared(prep, stream)
+
+        ms = timed(torch, step, args.steps, args.warmup, stream)
+        u = sum(uniq) / len(uniq)
+        nbytes = u * per_expert + E * Hm * 2 + T * Hm * 2 * 2 + T * E * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": "Qwen3-30B-A3B MoE layer decode HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic: N(0,0.02) weights W4 g64 (BASELINE rule), N(0,1) hidden states",
+                          "config": {"workload": f"config 3: router + routed experts, tokens={T}, E={E}, top-{A}, "
+                                                 f"H={Hm}, I={I}, {copies} rotating layer copies",
+                                     "unique_experts": u, "bytes_per_step": int(nbytes),
+                                     "tokens_per_s": round(T * 1000.0 / ms, 1),
+                                     "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)},
+                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 360 for config 1, else 200)")
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
+                    help="1: Qwen3-8B W4 layer set (headline); 2: 8-bit / Q8_0 / Q4_K; 3: Qwen3-30B-A3B MoE layer")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 256 MiB bitwise_not pass (byte-counter calibration under rocprofv3)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1).",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.steps is None:
+        args.steps = 360 if args.config == 1 else 200
+    if args.warmup is None:
+        args.warmup = 72 if args.config == 1 else 40
+
+    import torch
+    from stark_amd import qmm as Q
+    Q.lib()
+    torch.cuda.set_device(torch.device("cuda:0"))
+    {1: config1, 2: config2, 3: config3}[args.config](args, torch, Q)
 
 
 if __name__ == "__main__":

@@ -418,10 +418,27 @@ def routed_experts_workspace_size(rows, model, hidden, experts, active) -> int:
     return int(lib().stark_qmm_routed_experts_workspace_size(rows, model, hidden, experts, active))
 
 
+def mapped_prepare(operations: Sequence[MappedOperation]):
+    """Marshal a mapped batch once; returns (prepared, outputs) for mapped_many_async."""
+    ops, keep = _mapped_structs(operations)
+    outs = [torch.empty(len(op.matrices) * op.rows, dtype=torch.float32, device=op.inputs.device)
+            for op in operations]
+    ptrs = (C.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    return (ops, len(operations), ptrs, keep, list(operations)), outs
+
+
+def mapped_many_async(prepared, status_word: torch.Tensor, stream=None) -> None:
+    """stark_qmm_mapped_many_async: stream-ordered; ORs 1 into status_word
+    (device int32, caller-zeroed) when an input is not finite."""
+    ops, n, ptrs = prepared[0], prepared[1], prepared[2]
+    _check(lib().stark_qmm_mapped_many_async(ops, n, ptrs, _ptr(status_word), _stream(stream)), "mapped_many_async")
+
+
 def routed_experts(input: torch.Tensor, router_logits: torch.Tensor, up: QuantizedB, down: QuantizedB, rows: int,
                    model: int, hidden: int, experts: int, active: int, expert_scales=None, round_logits=False,
                    round_weights=False, round_products=False, round_accumulator=False, sort_expert_ids=False,
-                   workspace: Optional[torch.Tensor] = None, output: Optional[torch.Tensor] = None, stream=None):
+                   workspace: Optional[torch.Tensor] = None, output: Optional[torch.Tensor] = None, stream=None,
+                   prepare_only: bool = False):
     """RoutedExperts::encode_scaled (routed.rs:154-257) as one device pipeline."""
     need = routed_experts_workspace_size(rows, model, hidden, experts, active)
     if workspace is None:
@@ -442,5 +459,13 @@ def routed_experts(input: torch.Tensor, router_logits: torch.Tensor, up: Quantiz
     s.sort_expert_ids = int(sort_expert_ids)
     s.workspace = _ptr(workspace)
     s.workspace_size = _nbytes(workspace)
+    if prepare_only:
+        return s, (input, router_logits, expert_scales, up, down, workspace, output)
     _check(lib().stark_qmm_routed_experts(C.byref(s), _stream(stream)), "routed_experts")
     return output
+
+
+def routed_experts_prepared(prepared, stream=None) -> None:
+    """Issue a routed_experts call whose arguments were marshalled with
+    routed_experts(..., prepare_only=True)."""
+    _check(lib().stark_qmm_routed_experts(C.byref(prepared[0]), _stream(stream)), "routed_experts")
