@@ -376,7 +376,7 @@ def config3(args, torch, Q):
         del up, dn
         layers.append((wr, ub, db))
     per_expert = 2 * I * Hm // 2 + Hm * I // 2 + 2 * 2 * (Hm // GROUP) * 2 * I + 2 * 2 * (I // GROUP) * Hm
-    for T in (1, 4, 16):
+    for T in args.tokens:
         x = torch.randn(T, Hm, generator=gen, device="cuda").to(torch.bfloat16)
         logits = torch.empty(T * E, dtype=torch.float32, device="cuda")
         out = torch.empty(T * Hm, dtype=torch.bfloat16, device="cuda")
@@ -428,6 +428,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
                     help="1: Qwen3-8B W4 layer set (headline); 2: 8-bit / Q8_0 / Q4_K; 3: Qwen3-30B-A3B MoE layer")
+    ap.add_argument("--tokens", type=int, nargs="+", default=[1, 4, 16], help="config 3 tokens per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB bitwise_not pass (byte-counter calibration under rocprofv3)")

@@ -54,20 +54,22 @@ __device__ __forceinline__ uint32_t and_or_vs(uint32_t a, uint32_t vmask, uint32
     return r;
 }
 
-template <int MP, int MB>
+// P1: pass length (k values) when MP*MB <= 2; wider activation tiles use
+// shorter passes so the staged activations fit LDS.
+template <int MP, int MB, int P1 = QMM_MFMA_PASS_SMALL_M>
 struct Cfg {
     static constexpr int S = 16 / MP;  // group slots per activation row
     static constexpr int MR = MP * MB;
-    static constexpr int PASS = MR <= 2 ? QMM_MFMA_PASS_SMALL_M : (MR <= 8 ? 2048 : 1024);
+    static constexpr int PASS = MR <= 2 ? P1 : (MR <= 8 ? 2048 : 1024);
     static constexpr int Q = PASS / 4;      // k values per wave per pass
     static constexpr int SEGB = Q / 2;      // bytes of a row per wave per pass
     static constexpr int NI = SEGB / 64;    // 16-byte loads per lane per pass == steps per pass
     static constexpr int ROWB = SEGB + 16;  // padded LDS row: the 16 operand rows hit distinct banks
 };
 
-template <int MP, int MB>
+template <int MP, int MB, int P1 = QMM_MFMA_PASS_SMALL_M>
 struct MfmaLds {
-    using C = Cfg<MP, MB>;
+    using C = Cfg<MP, MB, P1>;
     u32x4 stage[4][kRows * C::ROWB / 16];    // per-wave code block [16][ROWB bytes]
     uint32_t meta[kRows][C::PASS / 32 + 4];  // raw 16-bit (scale | bias << 16) per (row, group)
     u32x4 xp[C::MR][C::PASS / 8];            // activation pairs (x0,x4)(x1,x5)(x2,x6)(x3,x7) per 8 values
@@ -92,10 +94,10 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 //   nA, nB : bank rows of tile rows 0..7 and 8..15 (multiples of 8, nB >= nA)
 //   M      : activation rows (<= MP*MB); xrow(m) = element offset of row m in op.x
 //   nib_s  : 0x000F000F, one2 : 0x3F803F80 (kernel arguments, scalar)
-template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, class XRow>
+template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, int P1 = QMM_MFMA_PASS_SMALL_M, class XRow>
 __device__ __forceinline__ void mfma_tile(const AffineOp& op, uint32_t nA, uint32_t nB, uint32_t M, XRow xrow,
-                                          MfmaLds<MP, MB>& lds, uint32_t nib_s, uint32_t one2) {
-    using Cf = Cfg<MP, MB>;
+                                          MfmaLds<MP, MB, P1>& lds, uint32_t nib_s, uint32_t one2) {
+    using Cf = Cfg<MP, MB, P1>;
     constexpr int S = Cf::S, MR = Cf::MR, PASS = Cf::PASS, Q = Cf::Q, SEGB = Cf::SEGB, NI = Cf::NI;
     constexpr int ROWB = Cf::ROWB;
 
@@ -145,7 +147,8 @@ __device__ __forceinline__ void mfma_tile(const AffineOp& op, uint32_t nA, uint3
     // Activation and metadata loads of one pass, all issued at once so that a
     // pass costs one memory round trip: activation vector v = tid + i*256 of
     // the [MR][PASS/8] table; one scale and one bias vector per thread.
-    constexpr int XI = MR * (PASS / 8) / kWg;
+    constexpr int XV = MR * (PASS / 8);             // activation vectors per pass
+    constexpr int XI = (XV + kWg - 1) / kWg;        // per thread
     u32x4 xv[XI], msv, mbv;
     auto load_aux = [&](uint32_t kbase) {
         const uint32_t kvals = min((uint32_t)PASS, K - kbase);
@@ -153,7 +156,7 @@ __device__ __forceinline__ void mfma_tile(const AffineOp& op, uint32_t nA, uint3
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
             const uint32_t v = tid + i * kWg, m = v / (PASS / 8), vi = v % (PASS / 8);
-            const bool ok = m < M && vi * 8 < kvals;
+            const bool ok = v < (uint32_t)XV && m < M && vi * 8 < kvals;
             const u32x4 t = *(const u32x4*)((const uint16_t*)op.x + (ok ? xrow(m) + kbase + vi * 8 : 0));
             xv[i] = ok ? t : u32x4{0, 0, 0, 0};
         }
@@ -200,13 +203,14 @@ __device__ __forceinline__ void mfma_tile(const AffineOp& op, uint32_t nA, uint3
             pq[1] = perm(t[2], t[0], 0x07060302u);
             pq[2] = perm(t[3], t[1], 0x05040100u);
             pq[3] = perm(t[3], t[1], 0x07060302u);
-            lds.xp[m][vi] = pq;
+            if (v < (uint32_t)XV) lds.xp[m][vi] = pq;
             float sm = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) sm = dot2_bf16(t[e], 0x3F803F80u, sm);
-            // the gs/8 vectors of a group sit in consecutive lanes
+            // the gs/8 vectors of a group sit in consecutive lanes (whole waves
+            // take part in the shuffles; lanes past the table add zeros)
             for (uint32_t off = 1; off < (op.group_size >> 3); off <<= 1) sm += __shfl_xor(sm, off, 64);
-            if ((vi & ((op.group_size >> 3) - 1)) == 0) lds.xs[m][(vi * 8) >> gshift] = sm;
+            if (v < (uint32_t)XV && (vi & ((op.group_size >> 3) - 1)) == 0) lds.xs[m][(vi * 8) >> gshift] = sm;
         }
         // ---- stage raw (scale, bias) pairs of the 16 tile rows
         if (op.os == 1) {

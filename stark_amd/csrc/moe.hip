@@ -8,80 +8,80 @@ namespace {
 
 QMM_DEVICE float round_bf16(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
 
-// MoeRoute (moe.rs:23-85): one wave per token row, experts striped over lanes.
-// Top-k is a repeated argmax where a strictly greater value wins and ties go to
-// the lowest expert id (moe.rs:61-66). The softmax denominator is a wave
-// reduction and exp is the device expf (the reference sums sequentially with
-// the platform's libm exp): ids are exact, weights agree to a few ulp.
-__global__ __launch_bounds__(64) void moe_route_kernel(const float* logits, uint32_t* ids, float* weights,
-                                                        uint32_t rows, uint32_t experts, uint32_t active,
-                                                        uint32_t round_weights, uint32_t round_logits) {
-    const uint32_t row = blockIdx.x;
-    const int lane = threadIdx.x;
+// MoeRoute (moe.rs:23-85): one 256-thread workgroup per token row. The
+// reference's top-k is a repeated argmax where a strictly greater value wins
+// and ties go to the lowest expert id (moe.rs:61-66), i.e. expert e lands at
+// rank #{e' : x[e'] > x[e] or (x[e'] == x[e] and e' < e)}. Each thread counts
+// that for its experts against the row staged in LDS: one pass, no
+// cross-lane argmax rounds. The softmax denominator is a tree sum and exp is
+// the device expf (the reference sums sequentially with the platform's libm
+// exp): ids are exact, weights agree to a few ulp.
+constexpr int kRouteThreads = 256;
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* logits, uint32_t* ids, float* weights,
+                                                                  uint32_t rows, uint32_t experts, uint32_t active,
+                                                                  uint32_t round_weights, uint32_t round_logits) {
+    __shared__ float xs[1024];
+    __shared__ float wred[kRouteThreads / 64];
+    __shared__ uint32_t sel[32];
+    __shared__ int all_finite;
+    const uint32_t row = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (row >= rows) return;
-    constexpr int kMaxPerLane = 1024 / 64;
-    float x[kMaxPerLane];
-    uint32_t used = 0;  // bit j: expert lane + 64*j already selected
-    bool valid = experts >= 1 && experts <= 1024 && active >= 1 && active <= 32 && active <= experts;
+    const bool shape_ok = experts >= 1 && experts <= 1024 && active >= 1 && active <= 32 && active <= experts;
     const uint32_t E = experts > 1024 ? 1024 : experts;
+    if (t == 0) all_finite = 1;
+    if (t < 32) sel[t] = 0;
+    __syncthreads();
     float mx = -INFINITY;
     bool finite = true;
-#pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-        const uint32_t e = lane + 64 * j;
-        float v = -INFINITY;
-        if (e < E) {
-            v = logits[(size_t)row * experts + e];
-            if (round_logits) v = round_bf16(v);
-            finite = finite && isfinite(v);
-            mx = fmaxf(mx, v);
-        } else {
-            used |= 1u << j;
-        }
-        x[j] = v;
+    for (uint32_t e = t; e < E; e += kRouteThreads) {
+        float v = logits[(size_t)row * experts + e];
+        if (round_logits) v = round_bf16(v);
+        xs[e] = v;
+        finite = finite && isfinite(v);
+        mx = fmaxf(mx, v);
     }
-    valid = valid && __all(finite) && experts <= 1024;
+    if (!finite) all_finite = 0;  // benign race: every writer stores 0
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) wred[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+    const bool valid = shape_ok && all_finite;
     float den = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j)
-        if (lane + 64 * j < E) den += expf(x[j] - mx);
+    for (uint32_t e = t; e < E; e += kRouteThreads) den += expf(xs[e] - mx);
     den = wave_sum(den);
-    float selected_sum = 0.0f;
-    float w_rank = 0.0f;  // lane r keeps the weight of rank r
-    for (uint32_t rank = 0; rank < active && rank < 32; ++rank) {
-        float best = -INFINITY;
-        uint32_t sel = 0xffffffffu;
-#pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j) {
-            if (!(used & (1u << j)) && x[j] > best) {
-                best = x[j];
-                sel = lane + 64 * j;
-            }
+    __syncthreads();  // every thread has read wred (max) before it is reused
+    if (lane == 0) wred[wave] = den;
+    // ranks by counting
+    for (uint32_t e = t; e < E; e += kRouteThreads) {
+        const float v = xs[e];
+        uint32_t rank = 0;
+        for (uint32_t f = 0; f < E; ++f) {
+            const float u = xs[f];
+            rank += (u > v || (u == v && f < e)) ? 1u : 0u;
         }
-        // wave argmax: larger value wins; equal values -> lower id
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            float ob = __shfl_xor(best, off, 64);
-            uint32_t os = __shfl_xor(sel, off, 64);
-            if (ob > best || (ob == best && os < sel)) {
-                best = ob;
-                sel = os;
-            }
-        }
-        // nothing left that is > -inf: the reference keeps expert 0
-        const uint32_t chosen = sel == 0xffffffffu ? 0u : sel;
-        if (sel != 0xffffffffu && (sel & 63u) == (uint32_t)lane) used |= 1u << (sel >> 6);
-        const float score = expf(best - mx) / den;
-        selected_sum += score;
-        if ((uint32_t)lane == rank) w_rank = score;
-        if (lane == 0) ids[(size_t)row * active + rank] = valid ? chosen : 0u;
+        if (rank < active) sel[rank] = e;
     }
-    if ((uint32_t)lane < active) {
-        float s = w_rank / selected_sum;
+    __syncthreads();
+    den = (wred[0] + wred[1]) + (wred[2] + wred[3]);
+    // scores of the selected experts, then their sum in rank order (as the
+    // reference accumulates), then the renormalised weights
+    __shared__ float score[32];
+    __shared__ float selected_sum;
+    if (t < active && t < 32) score[t] = expf(xs[sel[t]] - mx) / den;
+    __syncthreads();
+    if (t == 0) {
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < active && r < 32; ++r) sum += score[r];
+        selected_sum = sum;
+    }
+    __syncthreads();
+    if (t < active && t < 32) {
+        float s = score[t] / selected_sum;
         if (round_weights) s = round_bf16(s);
-        weights[(size_t)row * active + lane] = valid ? s : __builtin_nanf("");
+        ids[(size_t)row * active + t] = valid ? sel[t] : 0u;
+        weights[(size_t)row * active + t] = valid ? s : __builtin_nanf("");
     }
 }
 
@@ -163,7 +163,7 @@ stark_qmm_status stark_qmm_moe_route(const float* logits, uint32_t* ids, float* 
     if (rows == 0) return STARK_QMM_OK;
     if (!logits || !ids || !weights || active == 0 || active > 32 || experts == 0 || experts > 1024)
         return STARK_QMM_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(moe_route_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, logits, ids, weights, rows,
+    hipLaunchKernelGGL(moe_route_kernel, dim3(rows), dim3(kRouteThreads), 0, (hipStream_t)stream, logits, ids, weights, rows,
                        experts, active, round_weights, round_logits);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;

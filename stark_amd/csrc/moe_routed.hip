@@ -39,9 +39,12 @@ __device__ __host__ inline uint32_t count_class(uint32_t c) {
 
 // Workspace carve-up (byte offsets, 256-aligned).
 struct RoutedLayout {
-    uint64_t ids, weights, sorted, slots, lists, header, act, proj, total;
+    uint64_t ids, weights, sorted, table, header, act, proj, total;
     uint32_t routes, max_slots;
 };
+
+// Slot record: expert, route count, then up to 16 route ids (128 bytes).
+constexpr uint32_t kRecWords = 32;
 
 RoutedLayout routed_layout(uint32_t rows, uint32_t model, uint32_t hidden, uint32_t experts, uint32_t active) {
     RoutedLayout L{};
@@ -57,8 +60,7 @@ RoutedLayout routed_layout(uint32_t rows, uint32_t model, uint32_t hidden, uint3
     L.ids = take(4 * routes);
     L.weights = take(4 * routes);
     L.sorted = take(4 * routes);
-    L.slots = take(16ull * L.max_slots);
-    L.lists = take(4ull * kClasses * L.max_slots);
+    L.table = take(4ull * kRecWords * kClasses * L.max_slots);
     L.header = take(4 * 8);
     L.act = take(2 * routes * hidden);
     L.proj = take(2 * routes * model);
@@ -67,10 +69,13 @@ RoutedLayout routed_layout(uint32_t rows, uint32_t model, uint32_t hidden, uint3
 }
 
 // ---- 2. compaction: one workgroup of 1024 threads, one thread per expert id.
+// Routes are counting-sorted by expert, then every expert's routes are cut
+// into slots of at most 16 and each slot is written as a self-contained record
+// into the table of its route-count class.
 __global__ __launch_bounds__(1024) void moe_compact(const uint32_t* ids, uint32_t routes, uint32_t experts,
-                                                    uint32_t max_slots, uint32_t* sorted, uint32_t* slots,
-                                                    uint32_t* lists, uint32_t* header) {
-    __shared__ uint32_t cnt[1024], fill[1024], off[1024], soff[1024], wsum[2][16], ccount[kClasses];
+                                                    uint32_t max_slots, uint32_t* sorted, uint32_t* table,
+                                                    uint32_t* header) {
+    __shared__ uint32_t cnt[1024], fill[1024], off[1024], wsum[16], ccount[kClasses];
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     cnt[t] = 0;
     fill[t] = 0;
@@ -82,42 +87,31 @@ __global__ __launch_bounds__(1024) void moe_compact(const uint32_t* ids, uint32_
         atomicAdd(&cnt[e], 1u);
     }
     __syncthreads();
-    // exclusive scans of the route counts and of the slot counts over experts
-    const uint32_t c = cnt[t], ns = (c + kSlotRoutes - 1) / kSlotRoutes;
-    uint32_t ic = c, is = ns;
+    // exclusive scan of the route counts over experts
+    const uint32_t c = cnt[t];
+    uint32_t ic = c;
     for (uint32_t d = 1; d < 64; d <<= 1) {
-        const uint32_t uc = __shfl_up(ic, d, 64), us = __shfl_up(is, d, 64);
-        if (lane >= d) {
-            ic += uc;
-            is += us;
-        }
+        const uint32_t u = __shfl_up(ic, d, 64);
+        if (lane >= d) ic += u;
     }
-    if (lane == 63) {
-        wsum[0][wave] = ic;
-        wsum[1][wave] = is;
-    }
+    if (lane == 63) wsum[wave] = ic;
     __syncthreads();
-    uint32_t pc = 0, ps = 0;
-    for (uint32_t w = 0; w < wave; ++w) {
-        pc += wsum[0][w];
-        ps += wsum[1][w];
-    }
+    uint32_t pc = 0;
+    for (uint32_t w = 0; w < wave; ++w) pc += wsum[w];
     off[t] = pc + ic - c;
-    soff[t] = ps + is - ns;
     __syncthreads();
     for (uint32_t r = t; r < routes; r += 1024) {
         uint32_t e = ids[r];
         e = e < experts ? e : 0;
         sorted[off[e] + atomicAdd(&fill[e], 1u)] = r;
     }
-    for (uint32_t s = 0; s < ns; ++s) {
-        const uint32_t slot = soff[t] + s, n = min(kSlotRoutes, c - s * kSlotRoutes);
-        slots[4 * slot + 0] = t;
-        slots[4 * slot + 1] = off[t] + s * kSlotRoutes;
-        slots[4 * slot + 2] = n;
-        slots[4 * slot + 3] = 0;
-        const uint32_t cl = count_class(n);
-        lists[cl * max_slots + atomicAdd(&ccount[cl], 1u)] = slot;
+    __syncthreads();  // sorted[] complete and visible to the workgroup
+    for (uint32_t s0 = 0; s0 < c; s0 += kSlotRoutes) {
+        const uint32_t n = min(kSlotRoutes, c - s0), cl = count_class(n);
+        uint32_t* rec = table + ((size_t)cl * max_slots + atomicAdd(&ccount[cl], 1u)) * kRecWords;
+        rec[0] = t;
+        rec[1] = n;
+        for (uint32_t i = 0; i < n; ++i) rec[2 + i] = sorted[off[t] + s0 + i];
     }
     __syncthreads();
     if (t < kClasses) header[t] = ccount[t];
@@ -126,10 +120,8 @@ __global__ __launch_bounds__(1024) void moe_compact(const uint32_t* ids, uint32_
 // Launch record of a grouped product, read through the kernarg segment.
 struct GroupedLaunch {
     AffineOp op;             // the bank: codes, planes, activation base, k, group, strides
-    const uint32_t* slots;   // [max_slots][4] expert, first sorted position, routes
-    const uint32_t* list;    // slot ids of this class
+    const uint32_t* table;   // this class's slot records
     const uint32_t* header;  // per-class slot counts
-    const uint32_t* sorted;  // route ids in expert order
     uint16_t* out;           // up: act [routes][hidden]; down: proj [routes][model]
     uint32_t cls, tiles, active, hidden, model;
     uint32_t nib_mask, nib_one;
@@ -146,19 +138,19 @@ __device__ __forceinline__ uint16_t gated_silu(float value_f, float gate_f) {
 }
 
 // ---- 3. grouped up product + gated SiLU. Work item = (slot, tile of 8 value rows).
-template <int MP, int MB, bool SIGNED, bool BIASED, bool BF>
+template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, int P1>
 __global__ __launch_bounds__(kWg) void moe_up_mfma(GroupedLaunch launch) {
     (void)launch;
-    __shared__ MfmaLds<MP, MB> lds;
+    __shared__ MfmaLds<MP, MB, P1> lds;
     const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t items = L->header[L->cls] * L->tiles;
     const uint32_t H = L->hidden, A = L->active, model = L->model;
     for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-        const uint32_t slot = L->list[item / L->tiles], t = item % L->tiles;
-        const uint32_t e = L->slots[4 * slot], begin = L->slots[4 * slot + 1], cnt = L->slots[4 * slot + 2];
+        const uint32_t* rec = L->table + (size_t)(item / L->tiles) * kRecWords;
+        const uint32_t t = item % L->tiles, e = rec[0], cnt = rec[1];
         const uint32_t nA = e * 2 * H + 8 * t, nB = nA + H;
-        const uint32_t* routes = L->sorted + begin;
-        mfma_tile<MP, MB, SIGNED, BIASED, BF>(
+        const uint32_t* routes = rec + 2;
+        mfma_tile<MP, MB, SIGNED, BIASED, BF, P1>(
             L->op, nA, nB, cnt, [&](uint32_t m) { return (size_t)(routes[m] / A) * model; }, lds, L->nib_mask,
             L->nib_one);
         for (uint32_t q = threadIdx.x; q < (uint32_t)MP * MB * 8; q += kWg) {
@@ -174,19 +166,19 @@ __global__ __launch_bounds__(kWg) void moe_up_mfma(GroupedLaunch launch) {
 }
 
 // ---- 4. grouped down product. Work item = (slot, tile of 16 output rows).
-template <int MP, int MB, bool SIGNED, bool BIASED, bool BF>
+template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, int P1>
 __global__ __launch_bounds__(kWg) void moe_down_mfma(GroupedLaunch launch) {
     (void)launch;
-    __shared__ MfmaLds<MP, MB> lds;
+    __shared__ MfmaLds<MP, MB, P1> lds;
     const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t items = L->header[L->cls] * L->tiles;
     const uint32_t H = L->hidden, model = L->model;
     for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-        const uint32_t slot = L->list[item / L->tiles], t = item % L->tiles;
-        const uint32_t e = L->slots[4 * slot], begin = L->slots[4 * slot + 1], cnt = L->slots[4 * slot + 2];
+        const uint32_t* rec = L->table + (size_t)(item / L->tiles) * kRecWords;
+        const uint32_t t = item % L->tiles, e = rec[0], cnt = rec[1];
         const uint32_t nA = e * model + 16 * t;
-        const uint32_t* routes = L->sorted + begin;
-        mfma_tile<MP, MB, SIGNED, BIASED, BF>(
+        const uint32_t* routes = rec + 2;
+        mfma_tile<MP, MB, SIGNED, BIASED, BF, P1>(
             L->op, nA, nA + 8, cnt, [&](uint32_t m) { return (size_t)routes[m] * H; }, lds, L->nib_mask,
             L->nib_one);
         for (uint32_t q = threadIdx.x; q < (uint32_t)MP * MB * kRows; q += kWg) {
@@ -217,32 +209,31 @@ __global__ void moe_accumulate_ranks(const uint16_t* proj, const float* weights,
 }
 
 #define QMM_GROUPED_KERNEL(NAME)                                                                  \
-    template <int MP, int MB, bool SG, bool BI, bool BF>                                          \
+    template <int MP, int MB, bool SG, bool BI, bool BF, int P1>                                  \
     struct NAME##_k {                                                                             \
-        static void* fn() { return (void*)&NAME<MP, MB, SG, BI, BF>; }                            \
+        static void* fn() { return (void*)&NAME<MP, MB, SG, BI, BF, P1>; }                        \
     };
 QMM_GROUPED_KERNEL(moe_up_mfma)
 QMM_GROUPED_KERNEL(moe_down_mfma)
 #undef QMM_GROUPED_KERNEL
 
-template <template <int, int, bool, bool, bool> class K, int MP, int MB>
-void* pick(bool sg, bool bi, bool bf) {
-    if (sg) {
-        if (bi) return bf ? K<MP, MB, true, true, true>::fn() : K<MP, MB, true, true, false>::fn();
-        return bf ? K<MP, MB, true, false, true>::fn() : K<MP, MB, true, false, false>::fn();
-    }
-    if (bi) return bf ? K<MP, MB, false, true, true>::fn() : K<MP, MB, false, true, false>::fn();
-    return bf ? K<MP, MB, false, false, true>::fn() : K<MP, MB, false, false, false>::fn();
+template <template <int, int, bool, bool, bool, int> class K, int MP, int MB, int P1>
+void* pick(bool sg, bool bi) {
+    if (sg) return bi ? K<MP, MB, true, true, true, P1>::fn() : K<MP, MB, true, false, true, P1>::fn();
+    return bi ? K<MP, MB, false, true, true, P1>::fn() : K<MP, MB, false, false, true, P1>::fn();
 }
 
-template <template <int, int, bool, bool, bool> class K>
-void* pick_class(int cls, bool sg, bool bi, bool bf) {
+// Kernel for a route-count class; the one- and two-route classes take a pass
+// length matched to K so that all four waves of a tile get work.
+template <template <int, int, bool, bool, bool, int> class K>
+void* pick_class(int cls, bool sg, bool bi, uint32_t k) {
+    const bool short_k = k <= 1024;
     switch (cls) {
-    case 0: return pick<K, 1, 1>(sg, bi, bf);
-    case 1: return pick<K, 2, 1>(sg, bi, bf);
-    case 2: return pick<K, 4, 1>(sg, bi, bf);
-    case 3: return pick<K, 8, 1>(sg, bi, bf);
-    default: return pick<K, 8, 2>(sg, bi, bf);
+    case 0: return short_k ? pick<K, 1, 1, 1024>(sg, bi) : pick<K, 1, 1, 2048>(sg, bi);
+    case 1: return short_k ? pick<K, 2, 1, 1024>(sg, bi) : pick<K, 2, 1, 2048>(sg, bi);
+    case 2: return pick<K, 4, 1, 2048>(sg, bi);
+    case 3: return pick<K, 8, 1, 2048>(sg, bi);
+    default: return pick<K, 8, 2, 2048>(sg, bi);
     }
 }
 
@@ -338,8 +329,7 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
     uint32_t* ids = (uint32_t*)(ws + Lw.ids);
     float* weights = (float*)(ws + Lw.weights);
     uint32_t* sorted = (uint32_t*)(ws + Lw.sorted);
-    uint32_t* slots = (uint32_t*)(ws + Lw.slots);
-    uint32_t* lists = (uint32_t*)(ws + Lw.lists);
+    uint32_t* table = (uint32_t*)(ws + Lw.table);
     uint32_t* header = (uint32_t*)(ws + Lw.header);
     uint16_t* act = (uint16_t*)(ws + Lw.act);
     uint16_t* proj = (uint16_t*)(ws + Lw.proj);
@@ -353,19 +343,17 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
                                stream);
     if (st != STARK_QMM_OK) return st;
     // 2. compaction
-    hipLaunchKernelGGL(moe_compact, dim3(1), dim3(1024), 0, stream, ids, Lw.routes, E, Lw.max_slots, sorted, slots,
-                       lists, header);
+    hipLaunchKernelGGL(moe_compact, dim3(1), dim3(1024), 0, stream, ids, Lw.routes, E, Lw.max_slots, sorted, table,
+                       header);
     QMM_HIP_CHECK(hipGetLastError());
     // 3./4. grouped products, one launch per route-count class in use
-    const bool sg = a->up.signed_codes != 0, bi = a->up.correction == STARK_QMM_CORRECTION_BIASES, bf = true;
+    const bool sg = a->up.signed_codes != 0, bi = a->up.correction == STARK_QMM_CORRECTION_BIASES;
     const int top = (int)count_class(max_count);
     for (int pass = 0; pass < 2; ++pass) {
         GroupedLaunch g{};
         const bool up = pass == 0;
         g.op = up ? bank_op(a->up, E * 2 * H, model, a->input) : bank_op(a->down, E * model, H, act);
-        g.slots = slots;
         g.header = header;
-        g.sorted = sorted;
         g.out = up ? act : proj;
         g.tiles = up ? H / 8 : model / 16;
         g.active = A;
@@ -375,11 +363,11 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
         g.nib_one = 0x3F803F80u;
         for (int c = 0; c <= top; ++c) {
             g.cls = (uint32_t)c;
-            g.list = lists + (size_t)c * Lw.max_slots;
+            g.table = table + (size_t)c * Lw.max_slots * kRecWords;
             const uint64_t items = (uint64_t)class_slot_bound(c, Lw.routes, E, Lw.max_slots) * g.tiles;
             if (items == 0) continue;
             const uint32_t grid = (uint32_t)std::min<uint64_t>(items, 4096);
-            void* fn = up ? pick_class<moe_up_mfma_k>(c, sg, bi, bf) : pick_class<moe_down_mfma_k>(c, sg, bi, bf);
+            void* fn = up ? pick_class<moe_up_mfma_k>(c, sg, bi, model) : pick_class<moe_down_mfma_k>(c, sg, bi, H);
             void* argv[] = {&g};
             QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(grid), dim3(kWg), argv, 0, stream));
         }
