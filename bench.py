@@ -421,13 +421,50 @@ def config3(args, torch, Q):
                                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
 
 
+PEAK_MFMA_BF16_TFLOPS = 2500.0
+
+
+def config4(args, torch, Q):
+    """Config 4 (prefill part): M=2048 tokens through the Qwen3-8B W4 g64
+    projection set on the matrix-core dequant-GEMM; one step = the seven
+    products (q, k, v, o, gate, up, down) of one layer."""
+    Mtok = 2048
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 4)
+    stream = torch.cuda.current_stream()
+    layer = build_layer_set(torch, Q, gen)
+    kern = Q.MatmulKernel(Q.BF16, Q.BF16, Q.BF16)
+    xs = {k: torch.randn(Mtok, k, generator=gen, device="cuda").to(torch.bfloat16) for k in (4096, 12288)}
+    outs = [torch.empty(Mtok * mat["n"], dtype=torch.int16, device="cuda") for mat in layer]
+    args_list = [Q.MatmulArguments(a=xs[mat["k"]].view(torch.int16), m=Mtok, n=mat["n"], k=mat["k"], d=out,
+                                   b=Q.QuantizedB(codes=mat["codes"], scales=mat["scales"],
+                                                  params=Q.QuantParams(Q.GROUP_OUTPUT, mat["n"], mat["k"] // GROUP),
+                                                  correction_data=mat["biases"]))
+                 for mat, out in zip(layer, outs)]
+    batch = kern.prepare_many(args_list)
+    ms = timed(torch, lambda i: kern.encode_prepared(batch, stream), args.steps, args.warmup, stream)
+    flops = sum(2 * Mtok * n * k for _, n, k in SHAPES)
+    tf = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({"metric": "Qwen3-8B W4 prefill dequant-GEMM TFLOP/s", "value": round(tf, 1), "unit": "TFLOP/s",
+                      "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                      "data": "synthetic: N(0,0.02) weights W4 g64 (BASELINE rule), N(0,1) bf16 activations",
+                      "config": {"workload": f"config 4 prefill: M={Mtok} through q,k,v,o,gate,up,down (one layer)",
+                                 "flops_per_step": flops, "prefill_tokens_per_s_36_layers":
+                                     round(Mtok * 1000.0 / (ms * LAYERS), 1)},
+                      "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_MFMA_BF16_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4),
+                                   "traffic": None}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 360 for config 1, else 200)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
-                    help="1: Qwen3-8B W4 layer set (headline); 2: 8-bit / Q8_0 / Q4_K; 3: Qwen3-30B-A3B MoE layer")
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3, 4),
+                    help="1: Qwen3-8B W4 layer set (headline); 2: 8-bit / Q8_0 / Q4_K; 3: Qwen3-30B-A3B MoE layer; "
+                         "4: prefill dequant-GEMM at M=2048")
     ap.add_argument("--tokens", type=int, nargs="+", default=[1, 4, 16], help="config 3 tokens per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -438,15 +475,15 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.steps is None:
-        args.steps = 360 if args.config == 1 else 200
+        args.steps = {1: 360, 4: 20}.get(args.config, 200)
     if args.warmup is None:
-        args.warmup = 72 if args.config == 1 else 40
+        args.warmup = {1: 72, 4: 3}.get(args.config, 40)
 
     import torch
     from stark_amd import qmm as Q
     Q.lib()
     torch.cuda.set_device(torch.device("cuda:0"))
-    {1: config1, 2: config2, 3: config3}[args.config](args, torch, Q)
+    {1: config1, 2: config2, 3: config3, 4: config4}[args.config](args, torch, Q)
 
 
 if __name__ == "__main__":

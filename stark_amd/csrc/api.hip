@@ -183,6 +183,11 @@ stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kr, const stark_qmm_args* ar
     if (m == 0 || n == 0) return STARK_QMM_OK;
     if (!args->d || (!x && k)) return STARK_QMM_INVALID_ARGUMENT;
     if (materialize && m == 1) return launch_affine_materialized(op, stream);
+    // Prefill-sized products run the dequant-GEMM (bf16-rounded weight tiles, as
+    // the reference's Metal GEMM); the reference-accumulation mode keeps the
+    // f32-dequant GEMV kernels for every M (kernel.rs:34-37, metal mod.rs:341-357).
+    if (!kr->reference_accumulation && !materialize && gemm_eligible(op, bits))
+        return launch_affine_gemm(op, bits, stream);
     if (affine_fast_eligible(op, bits)) return launch_affine_gemv(&op, 1, bits, stream);
     return launch_affine_generic(op, bits, stream);
 }
@@ -208,7 +213,7 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
         stark_qmm_status st = build_affine_op(kr, a->b, a->m, a->n, a->k, x, a->d, a->d_ops, a->gather_indices, &op, &bits);
         if (st != STARK_QMM_OK) return st;
         if (!a->d || (!x && a->k)) return STARK_QMM_INVALID_ARGUMENT;
-        if (!affine_fast_eligible(op, bits) || op.gather) {
+        if (!affine_fast_eligible(op, bits) || op.gather || (op.m > 16 && !kr->reference_accumulation)) {
             rest.push_back(i);
         } else if (bits == 4) {
             fast4.push_back(op);

@@ -1,0 +1,216 @@
+// Prefill dequant-GEMM (M > 16) for MLX-affine 4/8-bit weights on the gfx950
+// matrix cores: D[M,N] = X[M,K] * W[N,K]^T with W dequantised per tile.
+//
+// Reference: the Metal GEMM with its dequantising B loader
+// (crates/stark-engine/src/backends/metal/kernel/matmul/gemm/gemm.metal:122-203,
+// gemm/common/quant_scale_bias.h:23-138) dequantises each B tile into
+// threadgroup memory in the activation type and multiplies there; the CPU
+// twin of that rounding is reference_affine_linear_bf16
+// (backends/cpu/kernel/matmul/vision.rs:249-336): w = bf16_rne(f32(q)*s + b).
+// Here: a workgroup (4 waves) owns a 128x128 output tile; per 64-wide K step
+// the X tile is staged in LDS as is and the W tile is dequantised into LDS as
+// bf16 (w = s*q + bias_term rounded to nearest even), double-buffered so the
+// next step's global loads overlap the current step's v_mfma_f32_16x16x32_bf16
+// work (each wave: a 64x64 block = 4x4 MFMA tiles, 32 MFMAs per K step). The
+// D-ops (ab_scale, accumulate, bias, soft-cap) and the output rounding follow
+// kernel.rs:270-281.
+#include "qmm_common.h"
+
+namespace qmm {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row: 16-byte pad spreads the MFMA reads over the banks
+
+struct GemmLds {
+    uint16_t a[2][kBM][kLdsRow];
+    uint16_t b[2][kBN][kLdsRow];
+};
+
+template <bool BF>
+__device__ __forceinline__ float plane_f32(const void* p, size_t i) {
+    const uint16_t h = ((const uint16_t*)p)[i];
+    return BF ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+// BITS: 4 or 8. CORR: 0 symmetric, 1 biases. BF: bf16 (else f16) planes.
+template <int BITS, int CORR, bool SIGNED, bool BF>
+__global__ __launch_bounds__(256) void qgemm_mfma(AffineOp op) {
+    __shared__ GemmLds lds;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t M = op.m, N = op.n, K = op.k;
+    const uint32_t m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const size_t row_bytes = (size_t)K * BITS / 8;
+    const uint16_t* X = (const uint16_t*)op.x;
+
+    // ---- per-thread load assignment
+    // X tile [128][64] bf16: 4 x 16 B per thread (row tid/2 + 64i... -> row (tid + 256 i) / 8, col 8*(tid % 8))
+    // W tile: 128 rows x (64*BITS/8) bytes. 4-bit: 2 threads per row (32 codes each);
+    // 8-bit: 4 threads per row (16 codes each), two passes of 64 rows.
+    constexpr int WPT = BITS == 4 ? 32 : 16;             // codes per thread per pass
+    constexpr int TPR = kBK / WPT;                       // threads per row
+    constexpr int WPASS = (kBN * TPR + 255) / 256;       // passes over the rows
+    u32x4 xa[4];
+    u32x4 wc[WPASS][BITS == 4 ? 1 : 1];
+    float ws[WPASS], wb[WPASS];
+
+    auto load_step = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
+            const uint32_t m = m0 + r;
+            xa[i] = m < M ? *(const u32x4*)(X + (size_t)m * K + k0 + c) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int p = 0; p < WPASS; ++p) {
+            const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
+            const uint32_t n = n0 + r;
+            const bool ok = r < (uint32_t)kBN && n < N;
+            const uint32_t kk = k0 + part * WPT;  // first k of this thread's codes
+            const uint8_t* src = op.codes + (size_t)(ok ? n : 0) * row_bytes + (size_t)kk * BITS / 8;
+            wc[p][0] = ok ? __builtin_nontemporal_load((const u32x4*)src) : u32x4{0, 0, 0, 0};
+            const size_t si = (size_t)(ok ? n : 0) * op.os + (size_t)(kk / op.group_size) * op.gs;
+            ws[p] = ok ? plane_f32<BF>(op.scales, si) : 0.0f;
+            wb[p] = ok && CORR == 1 ? plane_f32<BF>(op.corr, si) : 0.0f;
+        }
+    };
+    auto store_step = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
+            *(u32x4*)&lds.a[buf][r][c] = xa[i];
+        }
+#pragma unroll
+        for (int p = 0; p < WPASS; ++p) {
+            const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
+            if (r >= (uint32_t)kBN) continue;
+            const float s = ws[p];
+            // bias term: biases, or -s * 2^(bits-1) for the symmetric correction
+            const float b = CORR == 1 ? wb[p] : -s * (float)(1 << (BITS - 1));
+            uint32_t packed[WPT / 2];
+#pragma unroll
+            for (int e = 0; e < WPT; e += 2) {
+                uint32_t q0, q1;
+                if (BITS == 4) {
+                    const uint32_t word = wc[p][0][e / 8];
+                    q0 = (word >> (4 * (e % 8))) & 15u;
+                    q1 = (word >> (4 * (e % 8 + 1))) & 15u;
+                    if (SIGNED) {
+                        q0 ^= 8u;
+                        q1 ^= 8u;
+                    }
+                } else {
+                    const uint32_t word = wc[p][0][e / 4];
+                    q0 = (word >> (8 * (e % 4))) & 255u;
+                    q1 = (word >> (8 * (e % 4 + 1))) & 255u;
+                    if (SIGNED) {
+                        q0 ^= 128u;
+                        q1 ^= 128u;
+                    }
+                }
+                const float w0 = fmaf((float)q0, s, b), w1 = fmaf((float)q1, s, b);
+                packed[e / 2] = (uint32_t)f32_to_bf16_bits(w0) | ((uint32_t)f32_to_bf16_bits(w1) << 16);
+            }
+#pragma unroll
+            for (int q = 0; q < WPT / 8; ++q)
+                *(u32x4*)&lds.b[buf][r][part * WPT + 8 * q] =
+                    u32x4{packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]};
+        }
+    };
+
+    // wave (wm, wn) owns rows wm*64.., cols wn*64.. of the tile
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint32_t li = lane & 15, lk = (lane >> 4) * 8;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    load_step(0);
+    store_step(0);
+    __syncthreads();
+    const uint32_t steps = K / kBK;
+    for (uint32_t s = 0; s < steps; ++s) {
+        const int cur = s & 1;
+        if (s + 1 < steps) load_step((s + 1) * kBK);
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 32) {
+            u32x4 af[4], bfr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *(const u32x4*)&lds.a[cur][wm * 64 + 16 * i + li][kk + lk];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bfr[j] = *(const u32x4*)&lds.b[cur][wn * 64 + 16 * j + li][kk + lk];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, af[i]), __builtin_bit_cast(bf16x8, bfr[j]), acc[i][j], 0, 0, 0);
+        }
+        if (s + 1 < steps) store_step(cur ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: C[i][j] of a 16x16 block sits in lane j + 16*(i/4), element i%4
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
+                const uint32_t n = n0 + wn * 64 + 16 * j + (lane & 15);
+                if (m >= M || n >= N) continue;
+                const size_t o = (size_t)m * N + n;
+                float v = op.ab_scale * acc[i][j][e];
+                if (op.flags & FLAG_ACCUMULATE) v += load_as_f32(op.d, op.d_dt, o);
+                if (op.bias) v += load_as_f32(op.bias, op.w_dt, n);
+                if (op.flags & FLAG_SOFT_CAP) v = op.soft_cap * tanhf(v / op.soft_cap);
+                store_from_f32(op.d, op.d_dt, o, v);
+            }
+}
+
+}  // namespace
+
+bool gemm_eligible(const AffineOp& o, int bits) {
+    if (bits != 4 && bits != 8) return false;
+    if (o.x_dt != STARK_QMM_BF16 || o.gather || o.m <= 16) return false;
+    if (o.w_dt == STARK_QMM_F32) return false;
+    if (!(o.corr_kind == STARK_QMM_CORRECTION_BIASES || o.corr_kind == STARK_QMM_CORRECTION_SYMMETRIC)) return false;
+    if (o.group_size != 32 && o.group_size != 64 && o.group_size != 128) return false;
+    if (o.k == 0 || o.k % kBK) return false;
+    return (((uintptr_t)o.codes | (uintptr_t)o.x) & 15) == 0;
+}
+
+stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t stream) {
+    const dim3 grid((op.n + kBN - 1) / kBN, (op.m + kBM - 1) / kBM);
+    if (grid.x == 0 || grid.y == 0) return STARK_QMM_OK;
+    const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
+    const bool bf = op.w_dt == STARK_QMM_BF16;
+#define QMM_G(B, C, S, F) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F>), grid, dim3(256), 0, stream, op)
+#define QMM_G_BITS(B)                                                      \
+    if (bi) {                                                              \
+        if (sg) { if (bf) QMM_G(B, 1, true, true); else QMM_G(B, 1, true, false); } \
+        else { if (bf) QMM_G(B, 1, false, true); else QMM_G(B, 1, false, false); }  \
+    } else {                                                               \
+        if (sg) { if (bf) QMM_G(B, 0, true, true); else QMM_G(B, 0, true, false); } \
+        else { if (bf) QMM_G(B, 0, false, true); else QMM_G(B, 0, false, false); }  \
+    }
+    if (bits == 4) {
+        QMM_G_BITS(4)
+    } else {
+        QMM_G_BITS(8)
+    }
+#undef QMM_G_BITS
+#undef QMM_G
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
+
+}  // namespace qmm

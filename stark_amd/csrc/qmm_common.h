@@ -160,6 +160,9 @@ bool affine_fast_eligible(const AffineOp& op, int bits);
 bool decode_eligible(const AffineOp& op, int bits);
 stark_qmm_status launch_affine_decode(const AffineOp* ops, uint32_t count, hipStream_t stream);
 stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stream);
+// Prefill dequant-GEMM on the matrix cores for M > 16 (qgemm_mfma.hip).
+bool gemm_eligible(const AffineOp& op, int bits);
+stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t stream);
 // Route adjustment with optional gains (moe.hip).
 stark_qmm_status launch_moe_adjust(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
                                    uint32_t experts, uint32_t active, uint32_t sort_ids, hipStream_t stream);

@@ -289,3 +289,109 @@ def test_matrix_core_kernel_d_ops_on_shifted_tile(qmm, oracle, m):
     """N=80: the last 64-row tile overlaps the first; accumulate must add once."""
     run_case(qmm, oracle, m=m, n=80, k=2048, ab_scale=0.5, accumulate=True, with_bias=True, d_dt=H.F32, seed=8)
     run_case(qmm, oracle, m=m, n=80, k=2048, accumulate=True, soft_cap=2.0, d_dt=H.BF16, seed=9)
+
+
+# --------------------------------------------------------------- prefill GEMM
+
+def bf16_effective_reference(O, W, x, m, n, k, bits, gs, layout, correction, w_dt, signed):
+    """f64 product with the weights the GEMM multiplies: w = bf16_rne(f32(q)*s + bias_term)
+    (backends/cpu/kernel/matmul/vision.rs:249-336 for biases; the symmetric bias
+    term -s*2^(bits-1) and the signed-code XOR as kernel.rs:219-265)."""
+    codes = W["codes"][: n * k * bits // 8]
+    if bits == 4:
+        q = np.stack([codes & 15, codes >> 4], axis=-1).reshape(n, k).astype(np.int64)
+    else:
+        q = codes.reshape(n, k).astype(np.int64)
+    if signed:
+        q ^= 1 << (bits - 1)
+    G = k // gs
+    s = H.load(O, W["scales"], w_dt).astype(np.float32)
+    s = s.reshape(n, G) if layout == 0 else s.reshape(G, -1)[:, :n].T
+    if correction == 1:
+        b = H.load(O, W["corr"], w_dt).astype(np.float32)
+        b = b.reshape(n, G) if layout == 0 else b.reshape(G, -1)[:, :n].T
+    else:
+        b = -s * np.float32(1 << (bits - 1))
+    w = q.astype(np.float32) * np.repeat(s, gs, 1) + np.repeat(b, gs, 1)  # exact product, one rounding
+    w = O.bf16_to_f32(O.f32_to_bf16(w.astype(np.float32).ravel())).reshape(n, k).astype(np.float64)
+    xf = H.load(O, x, H.BF16).astype(np.float64).reshape(m, k)
+    return xf @ w.T, np.abs(xf) @ np.abs(w).T
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 96, 512), (64, 256, 1024), (200, 300, 4096), (2048, 128, 256),
+                                   (130, 1000, 192)])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prefill_gemm_shapes(qmm, oracle, m, n, k, bits):
+    """M > 16 runs the matrix-core dequant-GEMM: bf16-effective weights, f32
+    accumulation. Checked against the f64 product of the same bf16 weights, and
+    against the exact-f32 CPU kernel at the reference's own GPU/CPU bar
+    (quant_dispatch_test.rs:189: rel 0.05 / abs 0.4)."""
+    rng = np.random.default_rng(m * 7 + n + bits)
+    layout = 1 if (m + bits) % 2 else 0
+    W = H.affine_weights(oracle, rng, n, k, bits, 64, layout, 1, H.BF16)
+    x = H.activations(oracle, rng, m, k, H.BF16)
+    d = torch_empty(m * n, H.F32)
+    kern = qmm.MatmulKernel(H.BF16, H.BF16, H.F32)
+    mode = qmm.MODE_U4 if bits == 4 else qmm.MODE_U8
+    kern.encode(qmm.MatmulArguments(a=H.to_dev(x), m=m, n=n, k=k, d=d, b=qmm.QuantizedB(
+        codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]), params=qmm.QuantParams(layout, n, k // 64),
+        mode=mode, correction_data=H.to_dev(W["corr"]))))
+    torch.cuda.synchronize()
+    got = H.from_dev(d, np.float32).reshape(m, n)
+    want, mag = bf16_effective_reference(oracle, W, x, m, n, k, bits, 64, layout, 1, H.BF16, False)
+    check(got.ravel(), want.ravel(), mag=mag.ravel(), label=f"gemm m{m} n{n} k{k} b{bits}")
+    st, exact = oracle.matmul(a=x, m=m, n=n, k=k, codes=W["codes"], scales=W["scales"], correction_data=W["corr"],
+                              layout=layout, bits=bits, group_size=64, output_dt=H.F32, threads=8)
+    assert st == 0
+    assert np.all(np.abs(got.ravel() - exact) <= 0.05 * np.abs(exact) + 0.4)
+
+
+@pytest.mark.parametrize("correction,signed,w_dt,gs", [(0, False, H.BF16, 64), (1, True, H.F16, 32),
+                                                       (0, True, H.BF16, 128), (1, False, H.F16, 64)])
+def test_prefill_gemm_corrections(qmm, oracle, correction, signed, w_dt, gs):
+    m, n, k = 40, 160, 512
+    rng = np.random.default_rng(gs + correction)
+    for layout in (0, 1):
+        W = H.affine_weights(oracle, rng, n, k, 4, gs, layout, correction, w_dt, quantizer=False)
+        x = H.activations(oracle, rng, m, k, H.BF16)
+        d = torch_empty(m * n, H.BF16)
+        kern = qmm.MatmulKernel(w_dt, H.BF16, H.BF16)
+        kern.encode(qmm.MatmulArguments(a=H.to_dev(x), m=m, n=n, k=k, d=d, b=qmm.QuantizedB(
+            codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]), params=qmm.QuantParams(layout, n, k // gs),
+            group_size=gs, correction=correction, signed_codes=signed,
+            correction_data=None if W["corr"] is None else H.to_dev(W["corr"]))))
+        torch.cuda.synchronize()
+        got = H.load(oracle, H.from_dev(d, np.uint16), H.BF16)
+        want, mag = bf16_effective_reference(oracle, W, x, m, n, k, 4, gs, layout, correction, w_dt, signed)
+        check(got, want.ravel(), mag=mag.ravel(), label=f"gemm corr{correction} s{signed} l{layout}")
+
+
+def test_prefill_gemm_d_ops_and_reference_mode(qmm, oracle):
+    """D-ops in the GEMM epilogue; with set_reference_accumulation the same
+    product takes the f32-dequant path and meets the exact oracle's bar."""
+    m, n, k = 33, 130, 256
+    rng = np.random.default_rng(3)
+    W = H.affine_weights(oracle, rng, n, k, 4, 64, 1, 1, H.BF16)
+    x = H.activations(oracle, rng, m, k, H.BF16)
+    prior = rng.normal(0, 1, m * n).astype(np.float32)
+    bias = oracle.f32_to_bf16(rng.normal(0, 0.5, n).astype(np.float32))
+    for reference in (False, True):
+        d = H.to_dev(prior.copy())
+        kern = qmm.MatmulKernel(H.BF16, H.BF16, H.F32)
+        kern.set_reference_accumulation(reference)
+        kern.encode(qmm.MatmulArguments(a=H.to_dev(x), m=m, n=n, k=k, d=d, b=qmm.QuantizedB(
+            codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]), params=qmm.QuantParams(1, n, k // 64),
+            correction_data=H.to_dev(W["corr"])), d_transform=qmm.MatmulDOps(ab_scale=0.5, accumulate=True,
+                                                                              bias=H.to_dev(bias), soft_cap=3.0)))
+        torch.cuda.synchronize()
+        got = H.from_dev(d, np.float32)
+        st, want = oracle.matmul(a=x, m=m, n=n, k=k, codes=W["codes"], scales=W["scales"],
+                                 correction_data=W["corr"], layout=1, bits=4, group_size=64, output_dt=H.F32,
+                                 d=prior.copy(), ab_scale=0.5, accumulate=True, bias=bias, soft_cap=3.0)
+        assert st == 0
+        if reference:
+            mag = H.dequant_magnitude(oracle, W["codes"], W["scales"], W["corr"], n, k, 4, 64, 1, 1, H.BF16, x,
+                                      H.BF16, m, out_n=n)
+            check(got, want, mag=mag * 0.5 + 4.0, label="reference mode")
+        else:
+            assert np.all(np.abs(got - want) <= 0.05 * np.abs(want) + 0.4)
