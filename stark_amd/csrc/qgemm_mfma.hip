@@ -21,6 +21,7 @@ namespace qmm {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 64;
@@ -49,22 +50,24 @@ __global__ __launch_bounds__(256) void qgemm_mfma(AffineOp op) {
     const uint16_t* X = (const uint16_t*)op.x;
 
     // ---- per-thread load assignment
-    // X tile [128][64] bf16: 4 x 16 B per thread (row tid/2 + 64i... -> row (tid + 256 i) / 8, col 8*(tid % 8))
-    // W tile: 128 rows x (64*BITS/8) bytes. 4-bit: 2 threads per row (32 codes each);
-    // 8-bit: 4 threads per row (16 codes each), two passes of 64 rows.
-    constexpr int WPT = BITS == 4 ? 32 : 16;             // codes per thread per pass
-    constexpr int TPR = kBK / WPT;                       // threads per row
-    constexpr int WPASS = (kBN * TPR + 255) / 256;       // passes over the rows
-    u32x4 xa[4];
-    u32x4 wc[WPASS][BITS == 4 ? 1 : 1];
-    float ws[WPASS], wb[WPASS];
+    // X tile [128][64] bf16: 4 x 16 B per thread (row v / 8, column 8 * (v % 8)).
+    // W tile: 128 rows x (64*BITS/8) bytes. 4-bit: 2 threads per row (32 codes
+    // each); 8-bit: 4 threads per row (16 codes each), two passes of 64 rows.
+    constexpr int WPT = BITS == 4 ? 32 : 16;        // codes per thread per pass
+    constexpr int TPR = kBK / WPT;                  // threads per row
+    constexpr int WPASS = (kBN * TPR + 255) / 256;  // passes over the rows
+    struct Stage {
+        u32x4 xa[4];
+        u32x4 wc[WPASS];
+        float ws[WPASS], wb[WPASS];
+    };
 
-    auto load_step = [&](uint32_t k0) {
+    auto load_step = [&](Stage& st, uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
             const uint32_t m = m0 + r;
-            xa[i] = m < M ? *(const u32x4*)(X + (size_t)m * K + k0 + c) : u32x4{0, 0, 0, 0};
+            st.xa[i] = m < M ? *(const u32x4*)(X + (size_t)m * K + k0 + c) : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
@@ -73,48 +76,49 @@ __global__ __launch_bounds__(256) void qgemm_mfma(AffineOp op) {
             const bool ok = r < (uint32_t)kBN && n < N;
             const uint32_t kk = k0 + part * WPT;  // first k of this thread's codes
             const uint8_t* src = op.codes + (size_t)(ok ? n : 0) * row_bytes + (size_t)kk * BITS / 8;
-            wc[p][0] = ok ? __builtin_nontemporal_load((const u32x4*)src) : u32x4{0, 0, 0, 0};
+            st.wc[p] = ok ? __builtin_nontemporal_load((const u32x4*)src) : u32x4{0, 0, 0, 0};
             const size_t si = (size_t)(ok ? n : 0) * op.os + (size_t)(kk / op.group_size) * op.gs;
-            ws[p] = ok ? plane_f32<BF>(op.scales, si) : 0.0f;
-            wb[p] = ok && CORR == 1 ? plane_f32<BF>(op.corr, si) : 0.0f;
+            st.ws[p] = ok ? plane_f32<BF>(op.scales, si) : 0.0f;
+            st.wb[p] = ok && CORR == 1 ? plane_f32<BF>(op.corr, si) : 0.0f;
         }
     };
-    auto store_step = [&](int buf) {
+    // X to LDS as is; W dequantised: w = s*q + bias_term (exact in f32: bf16/f16
+    // s times a <= 8-bit q), rounded to bf16 by v_cvt_pk_bf16_f32 (nearest even).
+    auto store_step = [&](const Stage& st, int buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
-            *(u32x4*)&lds.a[buf][r][c] = xa[i];
+            *(u32x4*)&lds.a[buf][r][c] = st.xa[i];
         }
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
             const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
             if (r >= (uint32_t)kBN) continue;
-            const float s = ws[p];
+            const float s = st.ws[p];
             // bias term: biases, or -s * 2^(bits-1) for the symmetric correction
-            const float b = CORR == 1 ? wb[p] : -s * (float)(1 << (BITS - 1));
+            const float b = CORR == 1 ? st.wb[p] : -s * (float)(1 << (BITS - 1));
+            uint32_t bytes[WPT / 4];  // code e of this thread sits in byte e % 4 of bytes[e / 4]
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                uint32_t u = st.wc[p][d];
+                if (BITS == 4) {
+                    if (SIGNED) u ^= 0x88888888u;
+                    const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+                    // codes 8d..8d+7: low nibbles are the even codes, high nibbles the odd
+                    bytes[2 * d] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);      // codes 8d..8d+3
+                    bytes[2 * d + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // codes 8d+4..8d+7
+                } else {
+                    bytes[d] = SIGNED ? u ^ 0x80808080u : u;
+                }
+            }
             uint32_t packed[WPT / 2];
 #pragma unroll
             for (int e = 0; e < WPT; e += 2) {
-                uint32_t q0, q1;
-                if (BITS == 4) {
-                    const uint32_t word = wc[p][0][e / 8];
-                    q0 = (word >> (4 * (e % 8))) & 15u;
-                    q1 = (word >> (4 * (e % 8 + 1))) & 15u;
-                    if (SIGNED) {
-                        q0 ^= 8u;
-                        q1 ^= 8u;
-                    }
-                } else {
-                    const uint32_t word = wc[p][0][e / 4];
-                    q0 = (word >> (8 * (e % 4))) & 255u;
-                    q1 = (word >> (8 * (e % 4 + 1))) & 255u;
-                    if (SIGNED) {
-                        q0 ^= 128u;
-                        q1 ^= 128u;
-                    }
-                }
-                const float w0 = fmaf((float)q0, s, b), w1 = fmaf((float)q1, s, b);
-                packed[e / 2] = (uint32_t)f32_to_bf16_bits(w0) | ((uint32_t)f32_to_bf16_bits(w1) << 16);
+                const uint32_t word = bytes[e / 4];
+                const float q0 = (float)((word >> (8 * (e % 4))) & 255u);
+                const float q1 = (float)((word >> (8 * (e % 4 + 1))) & 255u);
+                const bf16x2 pr = {(__bf16)fmaf(q0, s, b), (__bf16)fmaf(q1, s, b)};
+                packed[e / 2] = __builtin_bit_cast(uint32_t, pr);
             }
 #pragma unroll
             for (int q = 0; q < WPT / 8; ++q)
@@ -131,21 +135,14 @@ __global__ __launch_bounds__(256) void qgemm_mfma(AffineOp op) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
-
-    load_step(0);
-    store_step(0);
-    __syncthreads();
-    const uint32_t steps = K / kBK;
-    for (uint32_t s = 0; s < steps; ++s) {
-        const int cur = s & 1;
-        if (s + 1 < steps) load_step((s + 1) * kBK);
+    auto compute = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 32) {
             u32x4 af[4], bfr[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *(const u32x4*)&lds.a[cur][wm * 64 + 16 * i + li][kk + lk];
+            for (int i = 0; i < 4; ++i) af[i] = *(const u32x4*)&lds.a[buf][wm * 64 + 16 * i + li][kk + lk];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bfr[j] = *(const u32x4*)&lds.b[cur][wn * 64 + 16 * j + li][kk + lk];
+            for (int j = 0; j < 4; ++j) bfr[j] = *(const u32x4*)&lds.b[buf][wn * 64 + 16 * j + li][kk + lk];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -153,7 +150,20 @@ __global__ __launch_bounds__(256) void qgemm_mfma(AffineOp op) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, af[i]), __builtin_bit_cast(bf16x8, bfr[j]), acc[i][j], 0, 0, 0);
         }
-        if (s + 1 < steps) store_step(cur ^ 1);
+    };
+
+    // One register stage: step s computes from LDS buffer s%2 while the loads
+    // of step s+1 are in flight; they then go to the other buffer.
+    const uint32_t steps = K / kBK;
+    Stage st;
+    load_step(st, 0);
+    store_step(st, 0);
+    __syncthreads();
+    for (uint32_t s = 0; s < steps; ++s) {
+        const int cur = s & 1;
+        if (s + 1 < steps) load_step(st, (s + 1) * kBK);
+        compute(cur);
+        if (s + 1 < steps) store_step(st, cur ^ 1);
         __syncthreads();
     }
 
