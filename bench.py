@@ -240,7 +240,7 @@ def config1(args, torch, Q):
     value = bytes_step / (ms_step * 1e-3) / 1e9
     achieved = bytes_step / (mean_launch_ms * 1e-3) / 1e9
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "qmv_w4_mfma_layerset_pmc.md")
+    tfile = os.path.join(ROOT, "profiles", "qmv_mfma_w4_layerset_pmc.md")
     if os.path.exists(tfile):
         import re
         hit = re.search(r"hbm_bytes_per_launch\s*=\s*(\d+)", open(tfile).read())
@@ -278,7 +278,7 @@ def config1(args, torch, Q):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": "qmv_w4_mfma<1,1,false,true,true> (one launch per step)",
+            "kernel": "qmv_mfma<1,1,false,true,true,4> (one launch per step)",
         },
         "cpu_baseline": cpu,
     }

@@ -166,9 +166,9 @@ stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t st
 // Route adjustment with optional gains (moe.hip).
 stark_qmm_status launch_moe_adjust(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
                                    uint32_t experts, uint32_t active, uint32_t sort_ids, hipStream_t stream);
-// Matrix-core kernel for 4-bit products with M <= 16 (qmv_mfma.hip).
+// Matrix-core kernel for 4/8-bit products with M <= 16 (qmv_mfma.hip).
 bool mfma_eligible(const AffineOp& op, int bits);
-stark_qmm_status launch_affine_mfma(const AffineOp* ops, uint32_t count, hipStream_t stream);
+stark_qmm_status launch_affine_mfma(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream);
 // Full-precision B operand (MatmulB::FullPrecision).
 struct DenseOp {
     const void* w;           // [N, ld] (transpose) or [K, ld]

@@ -582,7 +582,7 @@ stark_qmm_status launch_affine_gemv(const AffineOp* ops_in, uint32_t count_in, i
         (decode_eligible(o, bits) ? decode : others).push_back(o);
     }
     if (!mfma.empty()) {
-        stark_qmm_status st = launch_affine_mfma(mfma.data(), (uint32_t)mfma.size(), stream);
+        stark_qmm_status st = launch_affine_mfma(mfma.data(), (uint32_t)mfma.size(), bits, stream);
         if (st != STARK_QMM_OK) return st;
     }
     if (!decode.empty()) {
