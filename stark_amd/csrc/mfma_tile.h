@@ -1,4 +1,4 @@
-// mfma_tile.h -- one 16-row tile of a 4-bit affine product on the gfx950
+// mfma_tile.h -- one 16-row tile of a 4- or 8-bit affine product on the gfx950
 // matrix cores (activation rows M <= 16), shared by the plain product kernel
 // (qmv_mfma.hip) and the grouped MoE kernels (moe_routed.hip).
 //
@@ -13,23 +13,26 @@
 // x*q*2^-69 in f32's normal range; the flush multiplies by s * 2^69. Products
 // are exact and accumulate in f32.
 //
+// MFMA roles: B columns are the 16 weight rows of the tile; A rows are
+// (activation row, group slot) pairs -- A holds x where the k position's group
+// maps to the row's slot and 0 elsewhere -- so the accumulator keeps S = 16/MP
+// groups apart and each group's scale and bias are applied once, in f32, when
+// its period of steps ends (the "flush"). The group geometry (group size,
+// slots, flush points) is fixed at compile time.
+//
 // Schedule: a workgroup (4 waves) owns a 16-row tile (two 8-row halves that
-// may sit anywhere in the bank, e.g. an expert's value and gate rows). K is walked in passes; each wave takes a contiguous quarter of a pass.
-// A wave loads its quarter of the 16 rows with 16-byte lanes laid out row-major
-// (one load instruction covers whole 128-512 byte row segments, which HBM
-// streams far better than the 64-byte pieces of the MFMA operand layout),
-// writes it to a private padded LDS block and reads it back in operand layout.
-// Activations (as bf16 pairs in the MFMA's k order, with per-group sums) and
-// the raw (scale, bias) pairs of the tile are staged in LDS once per pass; the
-// next pass's code loads are in flight while the current pass computes. The
-// four waves' partial sums meet in LDS and are added in a fixed order before
-// the D-ops.
+// may sit anywhere in the bank, e.g. an expert's value and gate rows). K is
+// walked in passes; each wave takes a contiguous quarter of a pass. A wave
+// loads its quarter of the 16 rows with 16-byte lanes laid out row-major (one
+// load instruction covers whole 128-512 byte row segments), writes it to a
+// private padded LDS block and reads it back in operand layout. Activations
+// (as bf16 pairs in the MFMA's k order, with per-group sums) and the raw scale
+// and bias planes of the tile are staged in LDS once per pass; the next pass's
+// loads -- or the next tile's -- are issued into the same registers as soon as
+// the current pass sits in LDS. The four waves' partial sums meet in LDS and
+// are added in a fixed order before the D-ops.
 #pragma once
 #include "qmm_common.h"
-
-#ifndef QMM_MFMA_PASS_SMALL_M
-#define QMM_MFMA_PASS_SMALL_M 4096
-#endif
 
 namespace qmm {
 namespace mfma {
@@ -39,170 +42,167 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWg = 256;
 constexpr int kRows = 16;   // tile rows (MFMA B columns)
-constexpr int kStep = 128;  // k values per step (4 MFMAs, 64 bytes of a row)
+constexpr int kStep = 128;  // k values per step (4 MFMAs)
 constexpr int kBufNt = 2;   // buffer-load cache policy: nontemporal (streamed once)
 
-
-// P1: pass length (k values) when MP*MB <= 2; wider activation tiles use
-// shorter passes so the staged activations fit LDS.
-template <int MP, int MB, int P1 = QMM_MFMA_PASS_SMALL_M, int BITS = 4>
-struct Cfg {
-    static constexpr int S = 16 / MP;  // group slots per activation row
-    static constexpr int MR = MP * MB;
-    static constexpr int PASS = MR <= 2 ? P1 : (MR <= 8 ? 2048 : 1024);
-    static constexpr int Q = PASS / 4;             // k values per wave per pass
-    static constexpr int SEGB = Q * BITS / 8;      // bytes of a row per wave per pass
-    static constexpr int NI = SEGB / 64;           // 16-byte code loads per lane per pass
-    static constexpr int NSTEP = Q / kStep;        // MFMA steps per pass
-    static constexpr int ROWB = SEGB + 16;         // padded LDS row: the 16 operand rows hit distinct banks
+// Plane flags of a tile op (runtime: they only touch staging and the flush).
+enum : uint32_t {
+    PLANE_BF16 = 1u << 0,      // scale/bias planes are bf16 (else f16)
+    PLANE_BIASED = 1u << 1,    // bias plane present (else symmetric: -s * 2^(bits-1))
+    PLANE_GROUP_OUT = 1u << 2  // group-output planes [G][N4] (else output-group [N][G])
 };
 
-template <int MP, int MB, int P1 = QMM_MFMA_PASS_SMALL_M, int BITS = 4>
+__host__ __device__ inline uint32_t plane_flags(const AffineOp& op) {
+    return (op.w_dt == STARK_QMM_BF16 ? PLANE_BF16 : 0u) |
+           (op.corr_kind == STARK_QMM_CORRECTION_BIASES ? PLANE_BIASED : 0u) | (op.os == 1 ? PLANE_GROUP_OUT : 0u);
+}
+
+// Compile-time geometry. P1: pass length (k values of 4-bit codes) when
+// MP*MB <= 2; wider activation tiles use shorter passes so the staged
+// activations fit LDS. 8-bit codes take half the k per pass (same bytes).
+template <int MP, int MB, int GS, int BITS, int P1>
+struct Geo {
+    static constexpr int S = 16 / MP;        // group slots per activation row
+    static constexpr int MR = MP * MB;       // activation rows of the tile
+    static constexpr int GPS = kStep / GS;   // groups per step
+    static_assert(GS == 32 || GS == 64 || GS == 128, "group size");
+    static_assert(S >= GPS, "a step's groups must fit the slots");
+    static constexpr int PERIOD = S / GPS;   // steps between flushes
+    static constexpr int PASS = (MR <= 2 ? P1 : (MR <= 8 ? 2048 : 1024)) * 4 / BITS;
+    static constexpr int Q = PASS / 4;       // k values per wave per pass
+    static constexpr int SEGB = Q * BITS / 8;  // bytes of a row per wave per pass
+    static constexpr int NI = SEGB / 64;     // 16-byte code loads per lane per pass
+    static constexpr int NSTEP = Q / kStep;  // MFMA steps per wave per pass
+    static constexpr int ROWB = SEGB + 16;   // padded LDS row: the 16 operand rows hit distinct banks
+    static constexpr int GPP = PASS / GS;    // groups per pass
+    static constexpr int GPW = Q / GS;       // groups per wave per pass
+    static constexpr int LPR = SEGB / 16;    // lanes per row segment of a code load
+    static constexpr int RPI = 64 / LPR;     // rows per code load instruction
+    static constexpr int XV = MR * (PASS / 8);  // activation vectors per pass
+    static constexpr int XI = (XV + kWg - 1) / kWg;
+    static_assert(NI >= 1 && RPI <= 8 && 8 % RPI == 0, "pass too short for 16 rows");
+};
+
+template <int MP, int MB, int GS, int BITS, int P1>
 struct MfmaLds {
-    using C = Cfg<MP, MB, P1, BITS>;
-    u32x4 stage[4][kRows * C::ROWB / 16];    // per-wave code block [16][ROWB bytes]
-    uint32_t meta[kRows][C::PASS / 32 + 4];  // raw 16-bit (scale | bias << 16) per (row, group)
-    u32x4 xp[C::MR][C::PASS / 8];            // activation pairs (x0,x4)(x1,x5)(x2,x6)(x3,x7) per 8 values
-    float xs[C::MR][C::PASS / 32 + 4];       // activation sum per group
-    float red[4][C::MR][kRows];              // per-wave partial outputs
+    using G = Geo<MP, MB, GS, BITS, P1>;
+    u32x4 stage[4][kRows * G::ROWB / 16];     // per-wave code block [16][ROWB bytes]
+    // a flush reads S slots from the wave's first group on; slots past the
+    // wave's groups are read (and discarded), hence the S extra entries
+    uint16_t sc[G::GPP + G::S][kRows];        // raw scale plane of the tile [group][row]
+    uint16_t bi[G::GPP + G::S][kRows];        // raw bias plane
+    u32x4 xp[G::MR][G::PASS / 8];             // activation pairs per 8 values, in MFMA k order
+    float xs[G::MR][G::GPP + G::S];           // activation sum per group
+    float red[4][G::MR][kRows];               // per-wave partial outputs
     u32x4 zero[4];
 };
-
-template <bool BF>
-__device__ __forceinline__ float h2f(uint32_t h) {
-    return BF ? __uint_as_float(h << 16) : f16_bits_to_f32(h);
-}
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Tile engine: one 16-row tile of a 4-bit affine product on the matrix cores,
-// run pass by pass, with the loads of the next pass -- or of the next tile --
-// issued into the same registers as soon as the current pass sits in LDS.
-// A tile is described by
+__device__ __forceinline__ float plane_f32(uint32_t h, bool bf) {
+    return bf ? __uint_as_float(h << 16) : f16_bits_to_f32(h);
+}
+
+// Tile engine. A tile is described by
 //   op     : codes / planes / activation base, K, group size, plane strides
 //   nA, nB : bank rows of tile rows 0..7 and 8..15 (multiples of 8, nB >= nA)
 //   M      : activation rows (<= MP*MB); xrow(m) = element offset of row m in op.x
-// run() leaves the per-(activation row, tile row) sums in lds.red[wave][m][r]
-// (add the four waves in order (0+1)+(2+3)) behind a barrier.
-template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, int P1 = QMM_MFMA_PASS_SMALL_M, int BITS = 4>
+// load() issues one pass's global loads into registers; run() walks every pass
+// of the tile (calling next() once the last pass is in LDS, to issue the next
+// tile's loads) and leaves the per-(activation row, tile row) sums in
+// lds.red[wave][m][r] behind a barrier (add the four waves in order (0+1)+(2+3)).
+// keep_x: the activations staged for the previous tile are this tile's too
+// (same op, one pass): they are neither loaded nor staged.
+template <int MP, int MB, int GS, int BITS, bool SIGNED, int P1>
 struct TileEngine {
-    using Cf = Cfg<MP, MB, P1, BITS>;
-    static constexpr int S = Cf::S, MR = Cf::MR, PASS = Cf::PASS, Q = Cf::Q, SEGB = Cf::SEGB, NI = Cf::NI;
-    static constexpr int NSTEP = Cf::NSTEP;
-    static constexpr int ROWB = Cf::ROWB;
-    static constexpr int LPR = SEGB / 16;         // lanes per row segment of a code load
-    static constexpr int RPI = 64 / LPR;          // rows per code load instruction (divides 8)
-    static constexpr int XV = MR * (PASS / 8);    // activation vectors per pass
-    static constexpr int XI = (XV + kWg - 1) / kWg;
+    using G = Geo<MP, MB, GS, BITS, P1>;
+    static constexpr int S = G::S, MR = G::MR, PASS = G::PASS, Q = G::Q, SEGB = G::SEGB, NI = G::NI;
+    static constexpr int NSTEP = G::NSTEP, PERIOD = G::PERIOD, GPS = G::GPS, GPP = G::GPP, GPW = G::GPW;
+    static constexpr int ROWB = G::ROWB, LPR = G::LPR, RPI = G::RPI, XV = G::XV, XI = G::XI;
+    static constexpr int GSH = GS == 32 ? 5 : GS == 64 ? 6 : 7;
 
-    MfmaLds<MP, MB, P1, BITS>& lds;
-    int tid, lane;
-    uint32_t wave, j, kq, am, aslot, qbase, lcol, nib, one2;
+    MfmaLds<MP, MB, GS, BITS, P1>& lds;
+    uint32_t tid, lane, wave, j, kq, am, aslot, lcol;
     uint8_t* wstage;
-    u32x4 w[NI];       // codes of the loaded pass
-    u32x4 xv[XI];      // activations of the loaded pass
-    u32x4 msv, mbv;    // scale / bias vectors of the loaded pass
+    u32x4 w[NI];     // codes of the loaded pass
+    u32x4 xv[XI];    // activations of the loaded pass
+    u32x4 msv, mbv;  // scale / bias vectors of the loaded pass
 
-    __device__ __forceinline__ TileEngine(MfmaLds<MP, MB, P1, BITS>& l, uint32_t nib_s, uint32_t one2_s) : lds(l) {
+    __device__ __forceinline__ explicit TileEngine(MfmaLds<MP, MB, GS, BITS, P1>& l) : lds(l) {
         tid = threadIdx.x;
         lane = tid & 63;
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        j = lane & 15;  // B/C column (tile row)
-        kq = lane >> 4; // k quarter of a step
-        am = j / S;     // A row j -> (activation row, slot)
+        j = lane & 15;   // B/C column (tile row)
+        kq = lane >> 4;  // k quarter of a step
+        am = j / S;      // A row j -> (activation row, slot)
         aslot = j % S;
-        qbase = wave * Q;  // wave's first k within a pass
         lcol = (lane % LPR) * 16;
         wstage = (uint8_t*)lds.stage[wave];
-        nib = nib_s;
-        one2 = one2_s;
         if (tid < 4) lds.zero[tid] = u32x4{0, 0, 0, 0};
     }
 
-    static __device__ __forceinline__ uint32_t gshift_of(const AffineOp& op) {
-        return 31 - __builtin_clz(op.group_size);
-    }
-    // output-group rows start 16-byte aligned only when the group count is a
-    // multiple of 8 (passes start at multiples of 8 groups)
-    static __device__ __forceinline__ bool og_vec_of(const AffineOp& op) {
-        return op.os % 8 == 0 && (((uintptr_t)op.scales | (uintptr_t)op.corr) & 15) == 0;
+    // Output-group plane rows are read as 16-byte vectors when every row of a
+    // pass starts 16-byte aligned (8 groups at a time); otherwise the planes
+    // are staged element by element.
+    static __device__ __forceinline__ bool og_vec(const AffineOp& op, uint32_t gcnt) {
+        return op.os % 8 == 0 && gcnt % 8 == 0 && (((uintptr_t)op.scales | (uintptr_t)op.corr) & 15) == 0;
     }
 
     // Issue every global load of pass `kbase` of a tile: codes through a buffer
     // resource starting at row nA (16-byte piece i*64 + lane of the wave's
     // row-major [16][SEGB] block; pieces past K get an offset beyond the
     // resource and read as zero), activations (vector v = tid + i*256 of the
-    // [MR][PASS/8] table) and one scale and one bias vector per thread.
+    // [MR][PASS/8] table) and one scale and one bias vector per thread. No
+    // value is selected here (a select would wait for the load): loads whose
+    // slot is unused read from the array base and are never staged.
     template <class XRow>
-    __device__ __forceinline__ void load(const AffineOp& op, uint32_t nA, uint32_t nB, uint32_t M, XRow xrow,
-                                         uint32_t kbase) {
+    __device__ __forceinline__ void load(const AffineOp& op, uint32_t pf, uint32_t nA, uint32_t nB, uint32_t M,
+                                         XRow xrow, uint32_t kbase, bool keep_x = false) {
         const uint32_t K = op.k, kvals = min((uint32_t)PASS, K - kbase);
-        const uint32_t gshift = gshift_of(op), g0 = kbase >> gshift, gcnt = kvals >> gshift;
+        const uint32_t g0 = kbase >> GSH;
         const uint32_t row_bytes = K * BITS / 8;
+        if (!keep_x) {
 #pragma unroll
-        for (int i = 0; i < XI; ++i) {
-            const uint32_t v = tid + i * kWg, m = v / (PASS / 8), vi = v % (PASS / 8);
-            const bool ok = v < (uint32_t)XV && m < M && vi * 8 < kvals;
-            const u32x4 t = *(const u32x4*)((const uint16_t*)op.x + (ok ? xrow(m) + kbase + vi * 8 : 0));
-            xv[i] = ok ? t : u32x4{0, 0, 0, 0};
+            for (int i = 0; i < XI; ++i) {
+                const uint32_t v = tid + i * kWg, m = v / (PASS / 8), vi = v % (PASS / 8);
+                const bool ok = v < (uint32_t)XV && m < M && vi * 8 < kvals;
+                xv[i] = *(const u32x4*)((const uint16_t*)op.x + (ok ? xrow(m) + kbase + vi * 8 : 0));
+            }
         }
-        bool ok;
+        const uint32_t gcnt = kvals >> GSH;
         size_t off;
-        if (op.os == 1) {  // group-output planes [G][N4]: 8 rows of group tid/2 per vector
-            ok = (uint32_t)tid < gcnt * 2;
+        bool ok;
+        if (pf & PLANE_GROUP_OUT) {  // [G][N4]: 8 rows of group tid/2 per vector
+            ok = tid < gcnt * 2;
             off = (size_t)(g0 + (tid >> 1)) * op.gs + ((tid & 1) ? nB : nA);
-        } else {  // output-group planes [N][G]: 8 groups of a row per vector
-            const uint32_t per_row = og_vec_of(op) ? gcnt / 8 : 0;  // 0: staged element by element
-            ok = (uint32_t)tid < kRows * per_row;
+        } else {  // [N][G]: 8 groups of row tid/(gcnt/8) per vector
+            const uint32_t per_row = og_vec(op, gcnt) ? gcnt / 8 : 0;
+            ok = per_row && tid < kRows * per_row;
             const uint32_t r = per_row ? tid / per_row : 0, g8 = per_row ? (tid % per_row) * 8 : 0;
             off = (size_t)(r < 8 ? nA + r : nB + r - 8) * op.os + g0 + g8;
         }
         off = ok ? off : 0;
-        const u32x4 sv = *(const u32x4*)((const uint16_t*)op.scales + off);
-        msv = ok ? sv : u32x4{0, 0, 0, 0};
-        if (BIASED) {
-            const u32x4 bv = *(const u32x4*)((const uint16_t*)op.corr + off);
-            mbv = ok ? bv : u32x4{0, 0, 0, 0};
-        } else {
-            mbv = u32x4{0, 0, 0, 0};
-        }
+        msv = *(const u32x4*)((const uint16_t*)op.scales + off);
+        if (pf & PLANE_BIASED) mbv = *(const u32x4*)((const uint16_t*)op.corr + off);
         const uint32_t hi_skip = nB - nA - 8;  // extra rows between the two halves
         const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(op.codes + (size_t)nA * row_bytes), 0, (int)((nB - nA + 8) * row_bytes), 0x00020000);
         const uint32_t voff = (lane / LPR) * row_bytes + wave * SEGB + lcol;
-        const uint32_t vo = qbase + lcol * 8 / BITS < kvals ? voff : 0x80000000u;
+        const uint32_t vo = wave * Q + lcol * 8 / BITS < kvals ? voff : 0x80000000u;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
             w[i] = __builtin_bit_cast(
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           crs, vo, (i * RPI + (i * RPI >= 8 ? hi_skip : 0)) * row_bytes + kbase / 2, kBufNt));
+                           crs, vo, (i * RPI + (i * RPI >= 8 ? hi_skip : 0)) * row_bytes + kbase * BITS / 8, kBufNt));
     }
 
-    // Run every pass of a tile whose first pass has been load()ed. After the
-    // last pass is staged, next() is called to issue the next tile's loads.
-    template <class XRow, class Next>
-    __device__ __forceinline__ void run(const AffineOp& op, uint32_t nA, uint32_t nB, uint32_t M, XRow xrow,
-                                        Next next) {
-        const uint32_t K = op.k;
-        const uint32_t gshift = gshift_of(op);
-        const bool og_vec = og_vec_of(op);
-        const uint32_t gps_shift = 7 - gshift;             // log2(groups per step)
-        const uint32_t period = (uint32_t)S >> gps_shift;  // steps per accumulator period
-        const uint32_t gw = qbase >> gshift;                // wave's first group within a pass
-
-        f32x4 acc[MB], C[MB];
-#pragma unroll
-        for (int b = 0; b < MB; ++b) acc[b] = C[b] = f32x4{0, 0, 0, 0};
-
-        for (uint32_t kbase = 0; kbase < K; kbase += PASS) {
-            const uint32_t kvals = min((uint32_t)PASS, K - kbase);
-            const uint32_t gcnt = kvals >> gshift;  // K % group_size == 0
-
-            if (kbase) __syncthreads();  // every wave finished the previous pass's LDS
-            // ---- stage activations: bf16 x * 2^64 (4-bit odd codes: x * 2^60), in
-            // the operand order of the code masks, and per-group sums of x
+    // Stage the loaded pass into LDS (after a barrier when the previous pass's
+    // LDS may still be read).
+    __device__ __forceinline__ void stage(const AffineOp& op, uint32_t pf, uint32_t nA, uint32_t nB, uint32_t kbase,
+                                          uint32_t gcnt, bool keep_x) {
+        if (!keep_x) {
 #pragma unroll
             for (int i = 0; i < XI; ++i) {
                 const uint32_t v = tid + i * kWg, m = v / (PASS / 8), vi = v % (PASS / 8);
@@ -225,144 +225,174 @@ struct TileEngine {
                 float sm = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) sm = dot2_bf16(t[e], 0x3F803F80u, sm);
-                // the gs/8 vectors of a group sit in consecutive lanes (whole waves
-                // take part in the shuffles; lanes past the table add zeros)
-                for (uint32_t off = 1; off < (op.group_size >> 3); off <<= 1) sm += __shfl_xor(sm, off, 64);
-                if (v < (uint32_t)XV && (vi & ((op.group_size >> 3) - 1)) == 0) lds.xs[m][(vi * 8) >> gshift] = sm;
+                // the GS/8 vectors of a group sit in consecutive lanes
+#pragma unroll
+                for (int o = 1; o < GS / 8; o <<= 1) sm += __shfl_xor(sm, o, 64);
+                if (v < (uint32_t)XV && (vi & (GS / 8 - 1)) == 0) lds.xs[m][(vi * 8) >> GSH] = sm;
             }
-            // ---- stage raw (scale, bias) pairs of the 16 tile rows
-            if (op.os == 1) {
-                if ((uint32_t)tid < gcnt * 2) {
-                    const uint32_t g = tid >> 1, r8 = (tid & 1) * 8;
+        }
+        if (pf & PLANE_GROUP_OUT) {
+            if (tid < gcnt * 2) {
+                const uint32_t g = tid >> 1, h = (tid & 1) * 8;
+                *(u32x4*)&lds.sc[g][h] = msv;
+                if (pf & PLANE_BIASED) *(u32x4*)&lds.bi[g][h] = mbv;
+            }
+        } else if (!og_vec(op, gcnt)) {  // unaligned output-group rows: one element at a time
+            const uint32_t g0 = kbase >> GSH;
+            for (uint32_t q = tid; q < kRows * gcnt; q += kWg) {
+                const uint32_t r = q / gcnt, g = q % gcnt;
+                const size_t o = (size_t)(r < 8 ? nA + r : nB + r - 8) * op.os + g0 + g;
+                lds.sc[g][r] = ((const uint16_t*)op.scales)[o];
+                if (pf & PLANE_BIASED) lds.bi[g][r] = ((const uint16_t*)op.corr)[o];
+            }
+        } else {
+            const uint32_t per_row = gcnt / 8;
+            if (tid < kRows * per_row) {
+                const uint32_t r = tid / per_row, g8 = (tid % per_row) * 8;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        lds.meta[r8 + e][g] = ((msv[e >> 1] >> (16 * (e & 1))) & 0xffffu) |
-                                              (((mbv[e >> 1] >> (16 * (e & 1))) & 0xffffu) << 16);
-                }
-            } else if (og_vec) {
-                const uint32_t per_row = gcnt / 8;
-                if ((uint32_t)tid < kRows * per_row) {
-                    const uint32_t r = tid / per_row, g8 = (tid % per_row) * 8;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        lds.meta[r][g8 + e] = ((msv[e >> 1] >> (16 * (e & 1))) & 0xffffu) |
-                                              (((mbv[e >> 1] >> (16 * (e & 1))) & 0xffffu) << 16);
-                }
-            } else {  // output-group planes whose rows are not 16-byte aligned: one element per step
-                const uint32_t g0 = kbase >> gshift;
-                for (uint32_t q = tid; q < kRows * gcnt; q += kWg) {
-                    const uint32_t r = q / gcnt, g = q % gcnt;
-                    const size_t o = (size_t)(r < 8 ? nA + r : nB + r - 8) * op.os + g0 + g;
-                    const uint32_t sv = ((const uint16_t*)op.scales)[o];
-                    const uint32_t bv = BIASED ? ((const uint16_t*)op.corr)[o] : 0u;
-                    lds.meta[r][g] = sv | (bv << 16);
+                for (int e = 0; e < 8; ++e) {
+                    lds.sc[g8 + e][r] = (uint16_t)(msv[e >> 1] >> (16 * (e & 1)));
+                    if (pf & PLANE_BIASED) lds.bi[g8 + e][r] = (uint16_t)(mbv[e >> 1] >> (16 * (e & 1)));
                 }
             }
-            // ---- this pass's codes to the wave's LDS block (row-major, padded rows)
+        }
 #pragma unroll
-            for (int i = 0; i < NI; ++i) *(u32x4*)(wstage + (i * RPI + lane / LPR) * ROWB + lcol) = w[i];
+        for (int i = 0; i < NI; ++i) *(u32x4*)(wstage + (i * RPI + lane / LPR) * ROWB + lcol) = w[i];
+    }
+
+    // One step: 4 MFMAs over this lane's 32 codes of row j (16 or 32 bytes).
+    __device__ __forceinline__ void step(int s, const u32x4* const (&asrc)[MB], f32x4 (&C0)[MB], f32x4 (&C1)[MB]) {
+        u32x4 wv[BITS / 4];
+#pragma unroll
+        for (int h = 0; h < BITS / 4; ++h)
+            wv[h] = *(const u32x4*)(wstage + j * ROWB + s * (kStep * BITS / 8) + 4 * BITS * kq + 16 * h);
+        u32x4 a[MB][4];
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[b][t] = asrc[b][t];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            u32x4 bq;
+            if (BITS == 4) {
+                uint32_t u = wv[0][t];
+                if (SIGNED) u ^= 0x88888888u;
+                const uint32_t u8 = u >> 8;
+                bq[0] = u & 0x000F000Fu;   // (q0, q4)
+                bq[1] = u & 0x00F000F0u;   // (16 q1, 16 q5)
+                bq[2] = u8 & 0x000F000Fu;  // (q2, q6)
+                bq[3] = u8 & 0x00F000F0u;  // (16 q3, 16 q7)
+            } else {
+                uint32_t u0 = wv[t >> 1][2 * (t & 1)], u1 = wv[t >> 1][2 * (t & 1) + 1];
+                if (SIGNED) {
+                    u0 ^= 0x80808080u;
+                    u1 ^= 0x80808080u;
+                }
+                bq[0] = u0 & 0x00FF00FFu;         // (q0, q2)
+                bq[1] = (u0 >> 8) & 0x00FF00FFu;  // (q1, q3)
+                bq[2] = u1 & 0x00FF00FFu;         // (q4, q6)
+                bq[3] = (u1 >> 8) & 0x00FF00FFu;  // (q5, q7)
+            }
+            const bf16x8 bv = __builtin_bit_cast(bf16x8, bq);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                f32x4& c = (t & 1) ? C1[b] : C0[b];
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[b][t]), bv, c, 0, 0, 0);
+            }
+        }
+    }
+
+    // Fold one period's accumulator rows into acc: C row i = (m, slot) holds
+    // wave-pass group gbase + slot; acc += s * 2^69 * C + bias_term * xsum.
+    // Groups at or past glim (past the wave's quarter or the K tail) are not
+    // this wave's and are skipped.
+    __device__ __forceinline__ void flush(uint32_t pf, uint32_t gbase, uint32_t glim, f32x4 (&C0)[MB],
+                                          f32x4 (&C1)[MB], f32x4 (&acc)[MB]) {
+        const bool bf = pf & PLANE_BF16, biased = pf & PLANE_BIASED;
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const f32x4 c = C0[b] + C1[b];
+            uint32_t g[4];
+            float xsum[4];
+            if (S >= 4) {
+                const uint32_t g4 = gbase + (4 * kq) % S;
+                const uint32_t m = b * MP + (4 * kq) / S;
+                const f32x4 x4 = *(const f32x4*)&lds.xs[m][g4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    g[q] = g4 + q;
+                    xsum[q] = x4[q];
+                }
+            } else {  // S == 2: rows (2kq, gbase), (2kq, gbase+1), (2kq+1, gbase), (2kq+1, gbase+1)
+                const uint32_t m = b * MP + 2 * kq;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    g[q] = gbase + (q & 1);
+                    xsum[q] = lds.xs[m + (q >> 1)][g[q]];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float sc = plane_f32(lds.sc[g[q]][j], bf);
+                const float bias = biased ? plane_f32(lds.bi[g[q]][j], bf) : -(float)(1 << (BITS - 1)) * sc;
+                const float nv = fmaf(sc * 0x1p69f, c[q], fmaf(bias, xsum[q], acc[b][q]));
+                acc[b][q] = g[q] < glim ? nv : acc[b][q];
+            }
+            C0[b] = C1[b] = f32x4{0, 0, 0, 0};
+        }
+    }
+
+    // Compute one staged pass: NSTEP steps with flushes at period ends.
+    template <bool TAIL>
+    __device__ __forceinline__ void compute(uint32_t pf, uint32_t M, uint32_t kvals, uint32_t gcnt,
+                                            f32x4 (&acc)[MB]) {
+        f32x4 C0[MB], C1[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) C0[b] = C1[b] = f32x4{0, 0, 0, 0};
+        const uint32_t qbase = wave * Q;
+        const uint32_t gw = qbase >> GSH;  // wave's first group within the pass
+        const uint32_t glim = TAIL ? min(gcnt, gw + GPW) : gw + GPW;
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s) {
+            const uint32_t kloc = s * kStep + 32 * kq;  // wave-local k of this lane's 32 values
+            const uint32_t lg = kloc >> GSH;            // wave-local group
+            const u32x4* asrc[MB];
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                const uint32_t m = b * MP + am;
+                bool act = (lg % S) == aslot && m < M;
+                if (TAIL) act = act && qbase + kloc < kvals;
+                asrc[b] = act ? &lds.xp[m][(qbase + kloc) / 8] : lds.zero;
+            }
+            step(s, asrc, C0, C1);
+            if ((s + 1) % PERIOD == 0 || s == NSTEP - 1) flush(pf, gw + (s / PERIOD) * S, glim, C0, C1, acc);
+        }
+    }
+
+    // Walk every pass of a tile whose first pass has been load()ed.
+    template <class XRow, class Next>
+    __device__ __forceinline__ void run(const AffineOp& op, uint32_t pf, uint32_t nA, uint32_t nB, uint32_t M,
+                                        XRow xrow, Next next, bool keep_x = false) {
+        const uint32_t K = op.k;
+        f32x4 acc[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[b] = f32x4{0, 0, 0, 0};
+        for (uint32_t kbase = 0; kbase < K; kbase += PASS) {
+            const uint32_t kvals = min((uint32_t)PASS, K - kbase);
+            const uint32_t gcnt = kvals >> GSH;  // K % GS == 0
+            if (kbase) __syncthreads();          // every wave finished the previous pass's LDS
+            stage(op, pf, nA, nB, kbase, gcnt, keep_x && kbase == 0);
             __syncthreads();
             // the registers are free: the next pass's (or tile's) loads fly while this pass computes
             if (kbase + PASS < K)
-                load(op, nA, nB, M, xrow, kbase + PASS);
+                load(op, pf, nA, nB, M, xrow, kbase + PASS);
             else
                 next();
-
-            // Fold the period's accumulator rows into acc: row i = (m, slot) with
-            // wave-local group pidx*S + slot; adds s * 2^69 * C + bias_term * xsum.
-            // Slots past the wave's groups or past K hold nothing and are skipped.
-            const uint32_t* rmeta = lds.meta[j];
-            const uint32_t glim = min(gcnt, gw + (uint32_t)(Q >> gshift));
-            auto flush = [&](uint32_t pidx) {
-                const uint32_t gb = gw + pidx * S;
-#pragma unroll
-                for (int b = 0; b < MB; ++b) {
-                    uint32_t raw[4], g[4];
-                    float xsum[4];
-                    if (S >= 4) {
-                        const uint32_t g4 = gb + (4 * kq) % S;
-                        const uint32_t m = b * MP + (4 * kq) / S;
-                        const u32x4 r4 = *(const u32x4*)&rmeta[g4];
-                        const f32x4 x4 = *(const f32x4*)&lds.xs[m][g4];
-#pragma unroll
-                        for (int jj = 0; jj < 4; ++jj) {
-                            raw[jj] = r4[jj];
-                            xsum[jj] = x4[jj];
-                            g[jj] = g4 + jj;
-                        }
-                    } else {  // S == 2: rows (2kq, gb), (2kq, gb+1), (2kq+1, gb), (2kq+1, gb+1)
-                        const uint32_t m = b * MP + 2 * kq;
-                        raw[0] = raw[2] = rmeta[gb];
-                        raw[1] = raw[3] = rmeta[gb + 1];
-                        xsum[0] = lds.xs[m][gb];
-                        xsum[1] = lds.xs[m][gb + 1];
-                        xsum[2] = lds.xs[m + 1][gb];
-                        xsum[3] = lds.xs[m + 1][gb + 1];
-                        g[0] = g[2] = gb;
-                        g[1] = g[3] = gb + 1;
-                    }
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const float sc = h2f<BF>(raw[jj] & 0xffffu);
-                        const float bi = BIASED ? h2f<BF>(raw[jj] >> 16) : -(float)(1 << (BITS - 1)) * sc;
-                        const float nv = fmaf(sc * 0x1p69f, C[b][jj], fmaf(bi, xsum[jj], acc[b][jj]));
-                        acc[b][jj] = g[jj] < glim ? nv : acc[b][jj];
-                    }
-                    C[b] = f32x4{0, 0, 0, 0};
-                }
-            };
-#pragma unroll
-            for (int s = 0; s < NSTEP; ++s) {
-                const uint32_t kloc = s * kStep + 32 * kq;  // wave-local k of this lane's 32 values
-                const uint32_t kpos = qbase + kloc;         // pass-relative k
-                const uint32_t lg = kloc >> gshift;         // wave-local group
-                u32x4 a[MB][4];
-#pragma unroll
-                for (int b = 0; b < MB; ++b) {
-                    const uint32_t m = b * MP + am;
-                    const bool act = m < M && (lg % S) == aslot && kpos < kvals;
-                    const u32x4* src = act ? &lds.xp[m][kpos / 8] : lds.zero;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) a[b][t] = src[t];
-                }
-                // this lane's 32 codes: 16 bytes (4-bit) or 32 bytes (8-bit)
-                u32x4 wv[BITS / 4];
-#pragma unroll
-                for (int h = 0; h < BITS / 4; ++h)
-                    wv[h] = *(const u32x4*)(wstage + j * ROWB + s * (kStep * BITS / 8) + 4 * BITS * kq + 16 * h);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    u32x4 bq;
-                    if (BITS == 4) {
-                        uint32_t u = wv[0][t];
-                        if (SIGNED) u ^= 0x88888888u;
-                        const uint32_t u8 = u >> 8;
-                        bq[0] = u & 0x000F000Fu;   // (q0, q4)
-                        bq[1] = u & 0x00F000F0u;   // (16 q1, 16 q5)
-                        bq[2] = u8 & 0x000F000Fu;  // (q2, q6)
-                        bq[3] = u8 & 0x00F000F0u;  // (16 q3, 16 q7)
-                    } else {
-                        uint32_t u0 = wv[t >> 1][2 * (t & 1)], u1 = wv[t >> 1][2 * (t & 1) + 1];
-                        if (SIGNED) {
-                            u0 ^= 0x80808080u;
-                            u1 ^= 0x80808080u;
-                        }
-                        bq[0] = u0 & 0x00FF00FFu;         // (q0, q2)
-                        bq[1] = (u0 >> 8) & 0x00FF00FFu;  // (q1, q3)
-                        bq[2] = u1 & 0x00FF00FFu;         // (q4, q6)
-                        bq[3] = (u1 >> 8) & 0x00FF00FFu;  // (q5, q7)
-                    }
-                    const bf16x8 bv = __builtin_bit_cast(bf16x8, bq);
-#pragma unroll
-                    for (int b = 0; b < MB; ++b)
-                        C[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[b][t]), bv,
-                                                                      C[b], 0, 0, 0);
-                }
-                if ((s + 1) % period == 0) flush(s / period);
-            }
-            if (NSTEP % period) flush(NSTEP / period);  // partial last period of the pass
+            if (kvals == (uint32_t)PASS)
+                compute<false>(pf, M, kvals, gcnt, acc);
+            else
+                compute<true>(pf, M, kvals, gcnt, acc);
         }
-
         // ---- reduce accumulator rows of the same activation row, then across waves
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
@@ -392,13 +422,12 @@ struct TileEngine {
 };
 
 // One tile, loads included (the grouped MoE kernels).
-template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, int P1 = QMM_MFMA_PASS_SMALL_M, int BITS = 4,
-          class XRow>
-__device__ __forceinline__ void mfma_tile(const AffineOp& op, uint32_t nA, uint32_t nB, uint32_t M, XRow xrow,
-                                          MfmaLds<MP, MB, P1, BITS>& lds, uint32_t nib_s, uint32_t one2) {
-    TileEngine<MP, MB, SIGNED, BIASED, BF, P1, BITS> e(lds, nib_s, one2);
-    e.load(op, nA, nB, M, xrow, 0);
-    e.run(op, nA, nB, M, xrow, [] {});
+template <int MP, int MB, int GS, int BITS, bool SIGNED, int P1, class XRow>
+__device__ __forceinline__ void mfma_tile(const AffineOp& op, uint32_t pf, uint32_t nA, uint32_t nB, uint32_t M,
+                                          XRow xrow, MfmaLds<MP, MB, GS, BITS, P1>& lds) {
+    TileEngine<MP, MB, GS, BITS, SIGNED, P1> e(lds);
+    e.load(op, pf, nA, nB, M, xrow, 0);
+    e.run(op, pf, nA, nB, M, xrow, [] {});
 }
 
 }  // namespace mfma

@@ -124,7 +124,6 @@ struct GroupedLaunch {
     const uint32_t* header;  // per-class slot counts
     uint16_t* out;           // up: act [routes][hidden]; down: proj [routes][model]
     uint32_t cls, tiles, active, hidden, model;
-    uint32_t nib_mask, nib_one;
 };
 
 // silu(gate) * value in bf16 steps (gated_act_mul; SiLU as
@@ -138,10 +137,10 @@ __device__ __forceinline__ uint16_t gated_silu(float value_f, float gate_f) {
 }
 
 // ---- 3. grouped up product + gated SiLU. Work item = (slot, tile of 8 value rows).
-template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, int P1>
+template <int MP, int MB, int GS, bool SIGNED, int P1>
 __global__ __launch_bounds__(kWg) void moe_up_mfma(GroupedLaunch launch) {
     (void)launch;
-    __shared__ MfmaLds<MP, MB, P1> lds;
+    __shared__ MfmaLds<MP, MB, GS, 4, P1> lds;
     const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t items = L->header[L->cls] * L->tiles;
     const uint32_t H = L->hidden, A = L->active, model = L->model;
@@ -150,9 +149,8 @@ __global__ __launch_bounds__(kWg) void moe_up_mfma(GroupedLaunch launch) {
         const uint32_t t = item % L->tiles, e = rec[0], cnt = rec[1];
         const uint32_t nA = e * 2 * H + 8 * t, nB = nA + H;
         const uint32_t* routes = rec + 2;
-        mfma_tile<MP, MB, SIGNED, BIASED, BF, P1>(
-            L->op, nA, nB, cnt, [&](uint32_t m) { return (size_t)(routes[m] / A) * model; }, lds, L->nib_mask,
-            L->nib_one);
+        mfma_tile<MP, MB, GS, 4, SIGNED, P1>(
+            L->op, plane_flags(L->op), nA, nB, cnt, [&](uint32_t m) { return (size_t)(routes[m] / A) * model; }, lds);
         for (uint32_t q = threadIdx.x; q < (uint32_t)MP * MB * 8; q += kWg) {
             const uint32_t m = q / 8, i = q % 8;
             if (m >= cnt) continue;
@@ -166,10 +164,10 @@ __global__ __launch_bounds__(kWg) void moe_up_mfma(GroupedLaunch launch) {
 }
 
 // ---- 4. grouped down product. Work item = (slot, tile of 16 output rows).
-template <int MP, int MB, bool SIGNED, bool BIASED, bool BF, int P1>
+template <int MP, int MB, int GS, bool SIGNED, int P1>
 __global__ __launch_bounds__(kWg) void moe_down_mfma(GroupedLaunch launch) {
     (void)launch;
-    __shared__ MfmaLds<MP, MB, P1> lds;
+    __shared__ MfmaLds<MP, MB, GS, 4, P1> lds;
     const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t items = L->header[L->cls] * L->tiles;
     const uint32_t H = L->hidden, model = L->model;
@@ -178,9 +176,8 @@ __global__ __launch_bounds__(kWg) void moe_down_mfma(GroupedLaunch launch) {
         const uint32_t t = item % L->tiles, e = rec[0], cnt = rec[1];
         const uint32_t nA = e * model + 16 * t;
         const uint32_t* routes = rec + 2;
-        mfma_tile<MP, MB, SIGNED, BIASED, BF, P1>(
-            L->op, nA, nA + 8, cnt, [&](uint32_t m) { return (size_t)routes[m] * H; }, lds, L->nib_mask,
-            L->nib_one);
+        mfma_tile<MP, MB, GS, 4, SIGNED, P1>(
+            L->op, plane_flags(L->op), nA, nA + 8, cnt, [&](uint32_t m) { return (size_t)routes[m] * H; }, lds);
         for (uint32_t q = threadIdx.x; q < (uint32_t)MP * MB * kRows; q += kWg) {
             const uint32_t m = q / kRows, r = q % kRows;
             if (m >= cnt) continue;
@@ -208,32 +205,38 @@ __global__ void moe_accumulate_ranks(const uint16_t* proj, const float* weights,
     output[(size_t)row * model + p] = f32_to_bf16_bits(acc);
 }
 
-#define QMM_GROUPED_KERNEL(NAME)                                                                  \
-    template <int MP, int MB, bool SG, bool BI, bool BF, int P1>                                  \
-    struct NAME##_k {                                                                             \
-        static void* fn() { return (void*)&NAME<MP, MB, SG, BI, BF, P1>; }                        \
+#define QMM_GROUPED_KERNEL(NAME)                                  \
+    template <int MP, int MB, int GS, bool SG, int P1>            \
+    struct NAME##_k {                                             \
+        static void* fn() { return (void*)&NAME<MP, MB, GS, SG, P1>; } \
     };
 QMM_GROUPED_KERNEL(moe_up_mfma)
 QMM_GROUPED_KERNEL(moe_down_mfma)
 #undef QMM_GROUPED_KERNEL
 
-template <template <int, int, bool, bool, bool, int> class K, int MP, int MB, int P1>
-void* pick(bool sg, bool bi) {
-    if (sg) return bi ? K<MP, MB, true, true, true, P1>::fn() : K<MP, MB, true, false, true, P1>::fn();
-    return bi ? K<MP, MB, false, true, true, P1>::fn() : K<MP, MB, false, false, true, P1>::fn();
+// Kernel of one (class tile shape, group size, signedness); group size 32 needs
+// 4 slots per activation row, i.e. MP <= 4 (checked by check_bank).
+template <template <int, int, int, bool, int> class K, int MP, int MB, int P1>
+void* pick(uint32_t gs, bool sg) {
+    if (gs == 32) {
+        if constexpr (16 / MP >= 4) return sg ? K<MP, MB, 32, true, P1>::fn() : K<MP, MB, 32, false, P1>::fn();
+        return nullptr;
+    }
+    if (gs == 64) return sg ? K<MP, MB, 64, true, P1>::fn() : K<MP, MB, 64, false, P1>::fn();
+    return sg ? K<MP, MB, 128, true, P1>::fn() : K<MP, MB, 128, false, P1>::fn();
 }
 
 // Kernel for a route-count class; the one- and two-route classes take a pass
 // length matched to K so that all four waves of a tile get work.
-template <template <int, int, bool, bool, bool, int> class K>
-void* pick_class(int cls, bool sg, bool bi, uint32_t k) {
+template <template <int, int, int, bool, int> class K>
+void* pick_class(int cls, uint32_t gs, bool sg, uint32_t k) {
     const bool short_k = k <= 1024;
     switch (cls) {
-    case 0: return short_k ? pick<K, 1, 1, 1024>(sg, bi) : pick<K, 1, 1, 2048>(sg, bi);
-    case 1: return short_k ? pick<K, 2, 1, 1024>(sg, bi) : pick<K, 2, 1, 2048>(sg, bi);
-    case 2: return pick<K, 4, 1, 2048>(sg, bi);
-    case 3: return pick<K, 8, 1, 2048>(sg, bi);
-    default: return pick<K, 8, 2, 2048>(sg, bi);
+    case 0: return short_k ? pick<K, 1, 1, 1024>(gs, sg) : pick<K, 1, 1, 2048>(gs, sg);
+    case 1: return short_k ? pick<K, 2, 1, 1024>(gs, sg) : pick<K, 2, 1, 2048>(gs, sg);
+    case 2: return pick<K, 4, 1, 2048>(gs, sg);
+    case 3: return pick<K, 8, 1, 2048>(gs, sg);
+    default: return pick<K, 8, 2, 2048>(gs, sg);
     }
 }
 
@@ -347,7 +350,7 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
                        header);
     QMM_HIP_CHECK(hipGetLastError());
     // 3./4. grouped products, one launch per route-count class in use
-    const bool sg = a->up.signed_codes != 0, bi = a->up.correction == STARK_QMM_CORRECTION_BIASES;
+    const bool sg = a->up.signed_codes != 0;
     const int top = (int)count_class(max_count);
     for (int pass = 0; pass < 2; ++pass) {
         GroupedLaunch g{};
@@ -359,15 +362,15 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
         g.active = A;
         g.hidden = H;
         g.model = model;
-        g.nib_mask = 0x000F000Fu;
-        g.nib_one = 0x3F803F80u;
         for (int c = 0; c <= top; ++c) {
             g.cls = (uint32_t)c;
             g.table = table + (size_t)c * Lw.max_slots * kRecWords;
             const uint64_t items = (uint64_t)class_slot_bound(c, Lw.routes, E, Lw.max_slots) * g.tiles;
             if (items == 0) continue;
             const uint32_t grid = (uint32_t)std::min<uint64_t>(items, 4096);
-            void* fn = up ? pick_class<moe_up_mfma_k>(c, sg, bi, model) : pick_class<moe_down_mfma_k>(c, sg, bi, H);
+            void* fn = up ? pick_class<moe_up_mfma_k>(c, g.op.group_size, sg, model)
+                          : pick_class<moe_down_mfma_k>(c, g.op.group_size, sg, H);
+            if (!fn) return STARK_QMM_UNSUPPORTED_GROUP_SIZE;
             void* argv[] = {&g};
             QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(grid), dim3(kWg), argv, 0, stream));
         }
