@@ -192,7 +192,7 @@ def config1(args, torch, Q):
     # 36 distinct weight copies (same values, distinct memory) so that every
     # step reads HBM, as successive decode layers do.
     layers = [layer0] + [[{**m, "codes": m["codes"].clone(), "scales": m["scales"].clone(),
-                           "biases": m["biases"].clone()} for m in layer0] for _ in range(LAYERS - 1)]
+                           "biases": m["biases"].clone()} for m in layer0] for _ in range(args.copies - 1)]
     outs = [torch.empty(n, dtype=torch.int16, device="cuda") for _, n, _ in SHAPES]
 
     def layer_args(layer):
@@ -211,7 +211,7 @@ def config1(args, torch, Q):
         copy_calibration(torch)
 
     for i in range(args.warmup):
-        kern.encode_prepared(all_args[i % LAYERS], stream)
+        kern.encode_prepared(all_args[i % args.copies], stream)
     torch.cuda.synchronize()
 
     # timed region: K steps between two events on the launch stream
@@ -219,7 +219,7 @@ def config1(args, torch, Q):
     torch.cuda.synchronize()
     start.record(stream)
     for i in range(args.steps):
-        kern.encode_prepared(all_args[i % LAYERS], stream)
+        kern.encode_prepared(all_args[i % args.copies], stream)
     stop.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(stop)
@@ -229,7 +229,7 @@ def config1(args, torch, Q):
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_lat)]
     for i in range(n_lat):
         evs[i][0].record(stream)
-        kern.encode_prepared(all_args[i % LAYERS], stream)
+        kern.encode_prepared(all_args[i % args.copies], stream)
         evs[i][1].record(stream)
     torch.cuda.synchronize()
     launch_ms = sorted(a.elapsed_time(b) for a, b in evs)
@@ -265,7 +265,7 @@ def config1(args, torch, Q):
         "data": "synthetic: random-init N(0,0.02) weights quantized W4 g64 (BASELINE rule), bf16 N(0,1) activations",
         "config": {
             "workload": "Qwen3-8B layer matvec set q,k,v,o,gate,up,down; MLX-affine W4 g64 bf16 planes; M=1; "
-                        "36 rotating layer copies; one stark_qmm_encode_many launch per step",
+                        f"{args.copies} rotating layer copies; one stark_qmm_encode_many launch per step",
             "bytes_per_step": bytes_step,
             "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
             "matvec_decode_tokens_per_s_36_layers": round(1000.0 / (ms_step * LAYERS), 1),
@@ -467,6 +467,8 @@ def main():
                          "4: prefill dequant-GEMM at M=2048")
     ap.add_argument("--tokens", type=int, nargs="+", default=[1, 4, 16], help="config 3 tokens per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copies", type=int, default=LAYERS,
+                    help="config 1: distinct layer-weight copies the steps rotate through (36 = one Qwen3-8B)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB bitwise_not pass (byte-counter calibration under rocprofv3)")
     args = ap.parse_args()

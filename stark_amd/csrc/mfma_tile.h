@@ -78,7 +78,11 @@ struct Geo {
     static constexpr int GPW = Q / GS;       // groups per wave per pass
     static constexpr int LPR = SEGB / 16;    // lanes per row segment of a code load
     static constexpr int RPI = 64 / LPR;     // rows per code load instruction
-    static constexpr int XV = MR * (PASS / 8);  // activation vectors per pass
+    // Activation window: one activation row stages the x of two passes at
+    // once, so a K of up to XK is staged once per op and kept across the
+    // tile's passes and the workgroup's next tiles of the same op.
+    static constexpr int XK = (MR == 1 ? 2 : 1) * PASS;
+    static constexpr int XV = MR * (XK / 8);  // activation vectors of a window
     static constexpr int XI = (XV + kWg - 1) / kWg;
     static_assert(NI >= 1 && RPI <= 8 && 8 % RPI == 0, "pass too short for 16 rows");
 };
@@ -91,8 +95,8 @@ struct MfmaLds {
     // wave's groups are read (and discarded), hence the S extra entries
     uint16_t sc[G::GPP + G::S][kRows];        // raw scale plane of the tile [group][row]
     uint16_t bi[G::GPP + G::S][kRows];        // raw bias plane
-    u32x4 xp[G::MR][G::PASS / 8];             // activation pairs per 8 values, in MFMA k order
-    float xs[G::MR][G::GPP + G::S];           // activation sum per group
+    u32x4 xp[G::MR][G::XK / 8];               // activation pairs per 8 values, in MFMA k order
+    float xs[G::MR][G::XK / GS + G::S];       // activation sum per group
     float red[4][G::MR][kRows];               // per-wave partial outputs
     u32x4 zero[4];
 };
@@ -120,14 +124,14 @@ struct TileEngine {
     using G = Geo<MP, MB, GS, BITS, P1>;
     static constexpr int S = G::S, MR = G::MR, PASS = G::PASS, Q = G::Q, SEGB = G::SEGB, NI = G::NI;
     static constexpr int NSTEP = G::NSTEP, PERIOD = G::PERIOD, GPS = G::GPS, GPP = G::GPP, GPW = G::GPW;
-    static constexpr int ROWB = G::ROWB, LPR = G::LPR, RPI = G::RPI, XV = G::XV, XI = G::XI;
+    static constexpr int ROWB = G::ROWB, LPR = G::LPR, RPI = G::RPI, XK = G::XK, XV = G::XV, XI = G::XI;
     static constexpr int GSH = GS == 32 ? 5 : GS == 64 ? 6 : 7;
 
     MfmaLds<MP, MB, GS, BITS, P1>& lds;
     uint32_t tid, lane, wave, j, kq, am, aslot, lcol;
     uint8_t* wstage;
     u32x4 w[NI];     // codes of the loaded pass
-    u32x4 xv[XI];    // activations of the loaded pass
+    u32x4 xv[XI];    // activations of the loaded window
     u32x4 msv, mbv;  // scale / bias vectors of the loaded pass
 
     __device__ __forceinline__ explicit TileEngine(MfmaLds<MP, MB, GS, BITS, P1>& l) : lds(l) {
@@ -141,6 +145,21 @@ struct TileEngine {
         lcol = (lane % LPR) * 16;
         wstage = (uint8_t*)lds.stage[wave];
         if (tid < 4) lds.zero[tid] = u32x4{0, 0, 0, 0};
+    }
+
+    // Whether a pass stages activations, and which: the whole K when it fits
+    // the window (at the first pass, unless kept from the previous tile),
+    // else the pass's own k range.
+    static __device__ __forceinline__ bool x_window(uint32_t K, uint32_t kbase, bool keep_x, uint32_t kvals,
+                                                    uint32_t& xk0, uint32_t& xcnt) {
+        const bool whole = K <= (uint32_t)XK;
+        xk0 = whole ? 0 : kbase;
+        xcnt = whole ? K : kvals;
+        return !keep_x && (!whole || kbase == 0);
+    }
+    // first k of the staged window for a pass at kbase
+    static __device__ __forceinline__ uint32_t x_offset(uint32_t K, uint32_t kbase) {
+        return K <= (uint32_t)XK ? kbase : 0;
     }
 
     // Output-group plane rows are read as 16-byte vectors when every row of a
@@ -163,12 +182,13 @@ struct TileEngine {
         const uint32_t K = op.k, kvals = min((uint32_t)PASS, K - kbase);
         const uint32_t g0 = kbase >> GSH;
         const uint32_t row_bytes = K * BITS / 8;
-        if (!keep_x) {
+        uint32_t xk0, xcnt;
+        if (x_window(K, kbase, keep_x, kvals, xk0, xcnt)) {
 #pragma unroll
             for (int i = 0; i < XI; ++i) {
-                const uint32_t v = tid + i * kWg, m = v / (PASS / 8), vi = v % (PASS / 8);
-                const bool ok = v < (uint32_t)XV && m < M && vi * 8 < kvals;
-                xv[i] = *(const u32x4*)((const uint16_t*)op.x + (ok ? xrow(m) + kbase + vi * 8 : 0));
+                const uint32_t v = tid + i * kWg, m = v / (XK / 8), vi = v % (XK / 8);
+                const bool ok = v < (uint32_t)XV && m < M && vi * 8 < xcnt;
+                xv[i] = *(const u32x4*)((const uint16_t*)op.x + (ok ? xrow(m) + xk0 + vi * 8 : 0));
             }
         }
         const uint32_t gcnt = kvals >> GSH;
@@ -202,10 +222,11 @@ struct TileEngine {
     // LDS may still be read).
     __device__ __forceinline__ void stage(const AffineOp& op, uint32_t pf, uint32_t nA, uint32_t nB, uint32_t kbase,
                                           uint32_t gcnt, bool keep_x) {
-        if (!keep_x) {
+        uint32_t xk0, xcnt;
+        if (x_window(op.k, kbase, keep_x, min((uint32_t)PASS, op.k - kbase), xk0, xcnt)) {
 #pragma unroll
             for (int i = 0; i < XI; ++i) {
-                const uint32_t v = tid + i * kWg, m = v / (PASS / 8), vi = v % (PASS / 8);
+                const uint32_t v = tid + i * kWg, m = v / (XK / 8), vi = v % (XK / 8);
                 const u32x4 t = xv[i];
                 float f[8];
 #pragma unroll
@@ -306,7 +327,7 @@ struct TileEngine {
     // wave-pass group gbase + slot; acc += s * 2^69 * C + bias_term * xsum.
     // Groups at or past glim (past the wave's quarter or the K tail) are not
     // this wave's and are skipped.
-    __device__ __forceinline__ void flush(uint32_t pf, uint32_t gbase, uint32_t glim, f32x4 (&C0)[MB],
+    __device__ __forceinline__ void flush(uint32_t pf, uint32_t gbase, uint32_t glim, uint32_t xg0, f32x4 (&C0)[MB],
                                           f32x4 (&C1)[MB], f32x4 (&acc)[MB]) {
         const bool bf = pf & PLANE_BF16, biased = pf & PLANE_BIASED;
 #pragma unroll
@@ -317,7 +338,7 @@ struct TileEngine {
             if (S >= 4) {
                 const uint32_t g4 = gbase + (4 * kq) % S;
                 const uint32_t m = b * MP + (4 * kq) / S;
-                const f32x4 x4 = *(const f32x4*)&lds.xs[m][g4];
+                const f32x4 x4 = *(const f32x4*)&lds.xs[m][xg0 + g4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     g[q] = g4 + q;
@@ -328,7 +349,7 @@ struct TileEngine {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     g[q] = gbase + (q & 1);
-                    xsum[q] = lds.xs[m + (q >> 1)][g[q]];
+                    xsum[q] = lds.xs[m + (q >> 1)][xg0 + g[q]];
                 }
             }
 #pragma unroll
@@ -343,8 +364,9 @@ struct TileEngine {
     }
 
     // Compute one staged pass: NSTEP steps with flushes at period ends.
+    // koff: first k of the pass within the staged activation window
     template <bool TAIL>
-    __device__ __forceinline__ void compute(uint32_t pf, uint32_t M, uint32_t kvals, uint32_t gcnt,
+    __device__ __forceinline__ void compute(uint32_t pf, uint32_t M, uint32_t kvals, uint32_t gcnt, uint32_t koff,
                                             f32x4 (&acc)[MB]) {
         f32x4 C0[MB], C1[MB];
 #pragma unroll
@@ -362,10 +384,11 @@ struct TileEngine {
                 const uint32_t m = b * MP + am;
                 bool act = (lg % S) == aslot && m < M;
                 if (TAIL) act = act && qbase + kloc < kvals;
-                asrc[b] = act ? &lds.xp[m][(qbase + kloc) / 8] : lds.zero;
+                asrc[b] = act ? &lds.xp[m][(koff + qbase + kloc) / 8] : lds.zero;
             }
             step(s, asrc, C0, C1);
-            if ((s + 1) % PERIOD == 0 || s == NSTEP - 1) flush(pf, gw + (s / PERIOD) * S, glim, C0, C1, acc);
+            if ((s + 1) % PERIOD == 0 || s == NSTEP - 1)
+                flush(pf, gw + (s / PERIOD) * S, glim, koff >> GSH, C0, C1, acc);
         }
     }
 
@@ -388,10 +411,11 @@ struct TileEngine {
                 load(op, pf, nA, nB, M, xrow, kbase + PASS);
             else
                 next();
+            const uint32_t koff = x_offset(K, kbase);
             if (kvals == (uint32_t)PASS)
-                compute<false>(pf, M, kvals, gcnt, acc);
+                compute<false>(pf, M, kvals, gcnt, koff, acc);
             else
-                compute<true>(pf, M, kvals, gcnt, acc);
+                compute<true>(pf, M, kvals, gcnt, koff, acc);
         }
         // ---- reduce accumulator rows of the same activation row, then across waves
 #pragma unroll

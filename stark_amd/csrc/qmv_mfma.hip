@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(kWavesPerEu
                 uint32_t u0, m0;
                 rows_of(nxt, u0, m0);
                 const AffineOp& nop = kb->op[nxt >> 24];
-                next_keep_x = (nxt >> 24) == (cur >> 24) && nop.k <= (uint32_t)PASS;
+                next_keep_x = (nxt >> 24) == (cur >> 24) && nop.k <= (uint32_t)Geo<MP, MB, GS, BITS, kP1<BITS>>::XK;
                 e.load(nop, plane_flags(nop), m0, m0 + 8, nop.m, [&](uint32_t m) { return (size_t)m * nop.k; }, 0,
                        next_keep_x);
             }
