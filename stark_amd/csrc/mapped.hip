@@ -92,6 +92,16 @@ __global__ void finite_check_kernel(const float* x, uint64_t n, uint32_t* status
 
 __global__ void zero_word_kernel(uint32_t* w) { *w = 0; }
 
+}  // namespace
+
+stark_qmm_status launch_finite_check(const float* x, uint64_t n, uint32_t* status, hipStream_t stream) {
+    hipLaunchKernelGGL(finite_check_kernel, dim3(64), dim3(256), 0, stream, x, n, status);
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
+
+namespace {
+
 // Build the matvec ops for one mapped operation.
 void expand(const stark_qmm_mapped_op& op, float* out, std::vector<AffineOp>* affine4,
             std::vector<AffineOp>* affine8, std::vector<GgufOp>* gguf) {
@@ -187,11 +197,13 @@ stark_qmm_status run(const stark_qmm_mapped_op* ops, uint32_t count, float* cons
         if (ops[i].format == STARK_QMM_FORMAT_PACKED && !gguf_supported(ops[i].packed_kind))
             return STARK_QMM_UNSUPPORTED;
     }
+    // input finite check (weight_metal.rs:435-440); the GGUF kernels check
+    // the activations they stage themselves
     for (uint32_t i = 0; i < count; ++i) {
-        hipLaunchKernelGGL(finite_check_kernel, dim3(64), dim3(256), 0, stream, ops[i].inputs, ops[i].input_length,
-                           status);
+        if (ops[i].format == STARK_QMM_FORMAT_PACKED) continue;
+        stark_qmm_status st = launch_finite_check(ops[i].inputs, ops[i].input_length, status, stream);
+        if (st != STARK_QMM_OK) return st;
     }
-    QMM_HIP_CHECK(hipGetLastError());
     std::vector<AffineOp> a4, a8;
     std::vector<GgufOp> gg;
     for (uint32_t i = 0; i < count; ++i) expand(ops[i], outputs[i], &a4, &a8, &gg);
@@ -213,7 +225,7 @@ stark_qmm_status run(const stark_qmm_mapped_op* ops, uint32_t count, float* cons
         st = launch_affine_gemv(many.data(), (uint32_t)many.size(), bits, stream);
         if (st != STARK_QMM_OK) return st;
     }
-    return launch_gguf_gemv(gg.data(), (uint32_t)gg.size(), stream);
+    return launch_gguf_gemv(gg.data(), (uint32_t)gg.size(), status, stream);
 }
 
 }  // namespace

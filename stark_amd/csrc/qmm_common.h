@@ -196,9 +196,13 @@ struct GgufOp {
 struct GgufBatch {
     GgufOp op[kMaxBatchOps];
     uint32_t count;
+    uint32_t* status;  // ORed with 1 when an activation is not finite
 };
 bool gguf_supported(uint32_t kind);
-stark_qmm_status launch_gguf_gemv(const GgufOp* ops, uint32_t count, hipStream_t stream);
+// Every op's activations are checked for non-finite values (status |= 1).
+stark_qmm_status launch_gguf_gemv(const GgufOp* ops, uint32_t count, uint32_t* status, hipStream_t stream);
+// status |= 1 when any of x[0..n) is not finite (mapped.hip).
+stark_qmm_status launch_finite_check(const float* x, uint64_t n, uint32_t* status, hipStream_t stream);
 
 // Largest M the GEMV kernel handles in one weight pass.
 constexpr uint32_t kGemvMaxM = 2;

@@ -1,33 +1,48 @@
-// GGUF block-format matvec (Q8_0 = kind 8, Q4_K = kind 12) on gfx950.
+// GGUF block-format matvec / small-M product (Q8_0 = kind 8, Q4_K = kind 12)
+// on the gfx950 matrix cores, for the hybrid operator's f32 activations.
 //
 // Dequantisation is the reference's decode_block
 // (crates/stark-engine/src/engine/hybrid/weights.rs:2923-3012):
 //   Q8_0: w_i = f16(d) * int8(q_i)                          (32 values, 34 bytes)
 //   Q4_K: w   = f16(d) * sc * q - f16(dmin) * m, (sc, m) = scale_min(scales, j)
 //         (weights.rs:2908-2921), 8 sub-blocks of 32 values, 144 bytes
-// Both products are exact in f32, so the factored per-block form
-//   sum_i w_i x_i = d * sum_i q_i x_i              (Q8_0)
-//   sum_j (d*sc_j) * sum_{i in j} q_i x_i - (dmin*m_j) * sum_{i in j} x_i   (Q4_K)
+// Both products are exact in f32, so the factored per-group form
+//   sum_i w_i x_i = d * sum_i q_i x_i                                          (Q8_0)
+//   (d*sc_j) * sum_{i in j} q_i x_i - (dmin*m_j) * sum_{i in j} x_i            (Q4_K)
 // reassociates only the additions, as the reference Metal kernels do
 // (crates/stark-engine/src/engine/hybrid/packed_q8_grouped8_matvec.metal:11-82).
 //
-// Q4_K super-blocks are 16-byte aligned: lanes read them directly (8 lanes per
-// super-block, one 16-byte quant piece each plus the shared 16-byte header).
-// Q8_0 blocks are 34 bytes, so a tile of rows is first copied into LDS with
-// 16-byte loads and each thread then decodes whole blocks from LDS.
-#include "qmm_common.h"
+// Matrix-core form (the affine engine's, mfma_tile.h): sum(q * x) per group on
+// v_mfma_f32_16x16x32_bf16 with the codes as raw bf16 bit patterns (p < 256 is
+// p * 2^-133; Q8_0 codes enter as q + 128, the -128 folded into the bias
+// term; Q4_K high nibbles enter as 16 q with their activations scaled by
+// 2^-4), B columns = the 16 weight rows of a tile, A rows = (activation part,
+// group slot). The activations are f32: each row enters as two bf16 rows,
+// hi = bf16(x) and lo = bf16(x - hi), so |x - hi - lo| <= 2^-18 |x| and the
+// products stay exact; the two parts' sums meet in the reduction. Groups are
+// the 32-value (sub-)blocks; per-group scale and bias are applied once in f32
+// when a period of steps ends.
+//
+// Schedule: one workgroup (4 waves) per 16-row tile; K in passes, each wave a
+// quarter of a pass; a wave loads its quarter of the 16 rows' raw block bytes
+// with 16-byte loads (row-major), writes them to a padded LDS block and reads
+// its operands from there (Q8_0 code runs start 2 bytes into a block and are
+// realigned with v_alignbyte). Block headers are decoded to per-group f32
+// scale and bias in LDS once per pass. The next pass's loads are issued as
+// soon as the current pass sits in LDS.
+#include "mfma_tile.h"
 
 namespace qmm {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kRows = 32;  // rows per workgroup tile
-
-template <int B>
-__device__ __forceinline__ float ubyte(uint32_t w) {
-    return (float)((w >> (8 * B)) & 0xffu);
-}
+using mfma::bf16x8;
+using mfma::f32x4;
+using mfma::kBufNt;
+using mfma::kRows;
+using mfma::kStep;
+using mfma::kWg;
+using mfma::perm;
 
 __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, uint32_t i) { return (w[i >> 2] >> (8 * (i & 3))) & 0xffu; }
 
@@ -39,221 +54,6 @@ __device__ __forceinline__ void scale_min(const uint32_t* s, uint32_t j, float* 
     } else {
         *sc = (float)((byte_of(s, j + 4) & 15u) | ((byte_of(s, j - 4) >> 6) << 4));
         *mn = (float)((byte_of(s, j + 4) >> 4) | ((byte_of(s, j) >> 6) << 4));
-    }
-}
-
-__device__ __forceinline__ const GgufOp& pick(const GgufBatch& b, uint32_t bid, GgufOp* tmp) {
-    int oi = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxBatchOps; ++i)
-        if (i < (int)b.count && bid >= b.op[i].block_begin) oi = i;
-    *tmp = b.op[0];
-#pragma unroll
-    for (int i = 1; i < kMaxBatchOps; ++i)
-        if (oi == i) *tmp = b.op[i];
-    return *tmp;
-}
-
-// ------------------------------------------------------------------ Q4_K
-// Pass = 8 super-blocks (2048 values); lane = 8*sb + piece.
-template <int MT>
-__global__ __launch_bounds__(kThreads) void q4k_gemv(GgufBatch batch) {
-    GgufOp tmp;
-    const GgufOp& op = pick(batch, blockIdx.x, &tmp);
-    const uint32_t N = op.n, K = op.k;
-    const uint32_t nrb = (N + kRows - 1) / kRows;
-    const uint32_t lb = blockIdx.x - op.block_begin;
-    const uint32_t mtile = lb / nrb;
-    const uint32_t n0 = (lb - mtile * nrb) * kRows;
-    const uint32_t m0 = mtile * MT;
-    const int mcount = min((int)MT, (int)(op.m - m0));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t nsb = K / 256;
-    const size_t row_bytes = (size_t)nsb * 144;
-    const int sbl = lane >> 3, piece = lane & 7;
-    const int part = piece >> 1;
-    const int l0 = 16 * (piece & 1);
-    const uint32_t j_lo = 2 * part, j_hi = 2 * part + 1;
-    constexpr int RW = kRows / 4;
-
-    float acc[RW][MT];
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
-
-    for (uint32_t sb0 = 0; sb0 < nsb; sb0 += 8) {
-        const uint32_t sb = sb0 + sbl;
-        const bool ok = sb < nsb;
-        // activations of this lane: 16 values for the low nibbles, 16 for the high
-        float xl[MT][16], xh[MT][16], sl[MT], sh[MT];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            sl[m] = sh[m] = 0.0f;
-            const size_t base = (size_t)(m0 + m) * K + (size_t)sb * 256 + part * 64 + l0;
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const bool v = ok && m < mcount;
-                xl[m][t] = v ? load_as_f32(op.x, op.x_dt, base + t) : 0.0f;
-                xh[m][t] = v ? load_as_f32(op.x, op.x_dt, base + 32 + t) : 0.0f;
-                sl[m] += xl[m][t];
-                sh[m] += xh[m][t];
-            }
-        }
-#pragma unroll 2
-        for (int r = 0; r < RW; ++r) {
-            const uint32_t n = n0 + wave * RW + r;
-            if (n >= N || !ok) continue;
-            const uint8_t* blk = op.blocks + (size_t)n * row_bytes + (size_t)sb * 144;
-            const u32x4 hdr = load_stream(blk);
-            const u32x4 q = load_stream(blk + 16 + 16 * piece);
-            const float d = f16_bits_to_f32(hdr[0] & 0xffffu);
-            const float dmin = f16_bits_to_f32(hdr[0] >> 16);
-            const uint32_t sc3[3] = {hdr[1], hdr[2], hdr[3]};
-            float sc_lo, m_lo, sc_hi, m_hi;
-            scale_min(sc3, j_lo, &sc_lo, &m_lo);
-            scale_min(sc3, j_hi, &sc_hi, &m_hi);
-            const float dl = d * sc_lo, dh = d * sc_hi, ml = dmin * m_lo, mh = dmin * m_hi;
-            const uint32_t qw[4] = {q[0], q[1], q[2], q[3]};
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                float dot_lo = 0.0f, dot_hi = 0.0f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const uint32_t lo = qw[w] & 0x0F0F0F0Fu, hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
-                    dot_lo = fmaf(ubyte<0>(lo), xl[m][4 * w + 0], dot_lo);
-                    dot_lo = fmaf(ubyte<1>(lo), xl[m][4 * w + 1], dot_lo);
-                    dot_lo = fmaf(ubyte<2>(lo), xl[m][4 * w + 2], dot_lo);
-                    dot_lo = fmaf(ubyte<3>(lo), xl[m][4 * w + 3], dot_lo);
-                    dot_hi = fmaf(ubyte<0>(hi), xh[m][4 * w + 0], dot_hi);
-                    dot_hi = fmaf(ubyte<1>(hi), xh[m][4 * w + 1], dot_hi);
-                    dot_hi = fmaf(ubyte<2>(hi), xh[m][4 * w + 2], dot_hi);
-                    dot_hi = fmaf(ubyte<3>(hi), xh[m][4 * w + 3], dot_hi);
-                }
-                float a = acc[r][m];
-                a = fmaf(dl, dot_lo, a);
-                a = fmaf(-ml, sl[m], a);
-                a = fmaf(dh, dot_hi, a);
-                a = fmaf(-mh, sh[m], a);
-                acc[r][m] = a;
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const uint32_t n = n0 + wave * RW + r;
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const float v = wave_sum(acc[r][m]);
-            if (lane == 0 && n < N && m < mcount) store_from_f32(op.d, op.d_dt, (size_t)(m0 + m) * N + n, v);
-        }
-    }
-}
-
-// ------------------------------------------------------------------ Q8_0
-// Pass = 32 blocks (1024 values, 1088 bytes per row); the 32-row tile of the
-// pass is staged in LDS (34 KiB) with 16-byte loads. Thread t decodes block
-// t % 32 of rows t/32 + 8i.
-constexpr int kQ8PassBlocks = 32;
-constexpr int kQ8PassBytes = kQ8PassBlocks * 34;
-
-template <int MT>
-__global__ __launch_bounds__(kThreads) void q8_0_gemv(GgufBatch batch) {
-    __shared__ __align__(16) uint32_t tile[kRows * kQ8PassBytes / 4];
-    GgufOp tmp;
-    const GgufOp& op = pick(batch, blockIdx.x, &tmp);
-    const uint32_t N = op.n, K = op.k;
-    const uint32_t nrb = (N + kRows - 1) / kRows;
-    const uint32_t lb = blockIdx.x - op.block_begin;
-    const uint32_t mtile = lb / nrb;
-    const uint32_t n0 = (lb - mtile * nrb) * kRows;
-    const uint32_t m0 = mtile * MT;
-    const int mcount = min((int)MT, (int)(op.m - m0));
-    const int tid = threadIdx.x;
-    const uint32_t nb = K / 32;
-    const size_t row_bytes = (size_t)nb * 34;
-    const int b = tid & 31;
-    const int r0 = tid >> 5;
-
-    float acc[4][MT];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[i][m] = 0.0f;
-
-    for (uint32_t blk0 = 0; blk0 < nb; blk0 += kQ8PassBlocks) {
-        const uint32_t nblk = min((uint32_t)kQ8PassBlocks, nb - blk0);
-        const uint32_t pass_bytes = nblk * 34;  // multiple of 16 when nblk % 8 == 0
-        const uint32_t vecs = (pass_bytes + 15) / 16;
-        __syncthreads();
-        for (uint32_t i = tid; i < kRows * vecs; i += kThreads) {
-            const uint32_t r = i / vecs, v = i - r * vecs;
-            const uint32_t n = n0 + r;
-            u32x4 val = {0, 0, 0, 0};
-            if (n < N) val = load_stream(op.blocks + (size_t)n * row_bytes + (size_t)blk0 * 34 + (size_t)v * 16);
-            *(u32x4*)(tile + (r * kQ8PassBytes + v * 16) / 4) = val;
-        }
-        __syncthreads();
-        const bool ok = (uint32_t)b < nblk;
-        float x[MT][32], xs[MT];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            xs[m] = 0.0f;
-            const size_t base = (size_t)(m0 + m) * K + (size_t)(blk0 + b) * 32;
-#pragma unroll
-            for (int t = 0; t < 32; ++t) {
-                x[m][t] = (ok && m < mcount) ? load_as_f32(op.x, op.x_dt, base + t) : 0.0f;
-                xs[m] += x[m][t];
-            }
-        }
-        if (!ok) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = r0 + 8 * i;
-            const uint32_t off = r * kQ8PassBytes + b * 34;  // byte offset; even
-            const uint32_t* p = tile + (off >> 2);
-            uint32_t dw[9];
-#pragma unroll
-            for (int q = 0; q < 9; ++q) dw[q] = p[q];
-            float d;
-            uint32_t qs[8];
-            if ((off & 3) == 0) {
-                d = f16_bits_to_f32(dw[0] & 0xffffu);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) qs[q] = __builtin_amdgcn_alignbyte(dw[q + 1], dw[q], 2);
-            } else {
-                d = f16_bits_to_f32(dw[0] >> 16);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) qs[q] = dw[q + 1];
-            }
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                // signed bytes: q = u - 128 with u = byte ^ 0x80
-                float dot = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const uint32_t u = qs[q] ^ 0x80808080u;
-                    dot = fmaf(ubyte<0>(u), x[m][4 * q + 0], dot);
-                    dot = fmaf(ubyte<1>(u), x[m][4 * q + 1], dot);
-                    dot = fmaf(ubyte<2>(u), x[m][4 * q + 2], dot);
-                    dot = fmaf(ubyte<3>(u), x[m][4 * q + 3], dot);
-                }
-                dot = fmaf(-128.0f, xs[m], dot);
-                acc[i][m] = fmaf(d, dot, acc[i][m]);
-            }
-        }
-    }
-    // reduce the 32 block-threads of each row (lanes b = 0..31 of a half-wave)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t n = n0 + r0 + 8 * i;
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            float v = acc[i][m];
-#pragma unroll
-            for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-            if (b == 0 && n < N && m < mcount) store_from_f32(op.d, op.d_dt, (size_t)(m0 + m) * N + n, v);
-        }
     }
 }
 
@@ -297,33 +97,379 @@ __global__ void gguf_generic(GgufOp op) {
     store_from_f32(op.d, op.d_dt, (size_t)m * op.n + n, s);
 }
 
-template <typename F>
-stark_qmm_status launch_batched(const GgufOp* ops, uint32_t count, int mt, F launch) {
+
+// ------------------------------------------------------------------ geometry
+// M real rows take MR = 2M activation rows (hi/lo); MP rows per MFMA block.
+template <int KIND, int MP, int MB>
+struct GGeo {
+    static constexpr int BE = KIND == 12 ? 256 : 32;   // values per block
+    static constexpr int BB = KIND == 12 ? 144 : 34;   // bytes per block
+    static constexpr int MR = MP * MB;
+    static constexpr int RR = MR / 2;                  // real rows
+    static constexpr int S = 16 / MP;                  // group slots per activation row
+    static constexpr int GS = 32;
+    static constexpr int GPS = kStep / GS;             // 4 groups per step
+    static_assert(S >= GPS, "slots");
+    static constexpr int PERIOD = S / GPS;
+    static constexpr int PASS = MR <= 4 ? 2048 : 1024;  // k values per pass
+    static constexpr int Q = PASS / 4;                  // per wave
+    static constexpr int BPW = Q / BE;                  // blocks per wave per pass
+    static constexpr int SEGB = BPW * BB;               // bytes of a row per wave per pass
+    static constexpr int PPR = SEGB / 16;               // 16-byte pieces per row
+    static constexpr int NI = (kRows * PPR + 63) / 64;  // loads per lane
+    static constexpr int ROWB = SEGB + 16;              // padded LDS row
+    static constexpr int NSTEP = Q / kStep;
+    static constexpr int GPP = PASS / GS, GPW = Q / GS;
+    static constexpr int XV = RR * (PASS / 8);          // 8-value activation chunks per pass
+    static constexpr int XI = (XV + kWg - 1) / kWg;
+    static_assert(SEGB % 16 == 0 && BPW >= 1, "pass geometry");
+};
+
+template <int KIND, int MP, int MB>
+struct GLds {
+    using G = GGeo<KIND, MP, MB>;
+    u32x4 stage[4][kRows * G::ROWB / 16];  // raw block bytes, per wave [16][ROWB]
+    float sc[G::GPP + G::S][kRows];        // per (group, row) scale
+    float bi[G::GPP + G::S][kRows];        // per (group, row) bias term (Q4_K)
+    u32x4 xp[G::MR][G::PASS / 8];          // activation rows (hi, lo per real row), 8-bit pair order
+    float xs[G::MR][G::GPP + G::S];        // per-group activation sums
+    float red[4][G::RR][kRows];
+    u32x4 zero[4];
+};
+
+__device__ __forceinline__ uint32_t f32_to_bf16_rne_bits(float f) { return f32_to_bf16_bits(f); }
+
+// One tile of a GGUF product: op rows n0..n0+15, real activation rows 0..M-1.
+template <int KIND, int MP, int MB>
+struct GEngine {
+    using G = GGeo<KIND, MP, MB>;
+    static constexpr int S = G::S, MR = G::MR, RR = G::RR, PASS = G::PASS, Q = G::Q, BE = G::BE, BB = G::BB;
+    static constexpr int SEGB = G::SEGB, PPR = G::PPR, NI = G::NI, ROWB = G::ROWB, NSTEP = G::NSTEP;
+    static constexpr int PERIOD = G::PERIOD, GPP = G::GPP, GPW = G::GPW, XV = G::XV, XI = G::XI, BPW = G::BPW;
+
+    GLds<KIND, MP, MB>& lds;
+    uint32_t tid, lane, wave, j, kq, am, aslot;
+    uint8_t* wstage;
+    u32x4 w[NI];
+    u32x4 xa[XI], xb[XI];  // 8 f32 activations per chunk
+
+    __device__ __forceinline__ explicit GEngine(GLds<KIND, MP, MB>& l) : lds(l) {
+        tid = threadIdx.x;
+        lane = tid & 63;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        j = lane & 15;
+        kq = lane >> 4;
+        am = j / S;
+        aslot = j % S;
+        wstage = (uint8_t*)lds.stage[wave];
+        if (tid < 4) lds.zero[tid] = u32x4{0, 0, 0, 0};
+    }
+
+    // Issue the pass's loads: raw block bytes of the wave's quarter of the 16
+    // rows (pieces past the pass's blocks read as zero through the buffer
+    // resource) and the f32 activation chunks.
+    __device__ __forceinline__ void load(const GgufOp& op, uint32_t n0, uint32_t M, uint32_t kbase) {
+        const uint32_t K = op.k, kvals = min((uint32_t)PASS, K - kbase);
+        const uint32_t row_bytes = K / BE * BB;
+        const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(op.blocks + (size_t)n0 * row_bytes), 0, (int)(kRows * row_bytes), 0x00020000);
+        const uint32_t vbytes = kvals / BE * BB;  // valid bytes of a row in this pass
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t p = i * 64 + lane, r = p / PPR, c = (p % PPR) * 16;
+            const uint32_t col = wave * SEGB + c;
+            const uint32_t vo = p < (uint32_t)(kRows * PPR) && col < vbytes ? r * row_bytes + col + kbase / BE * BB
+                                                                            : 0x80000000u;
+            w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(crs, vo, 0, kBufNt));
+        }
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const uint32_t v = tid + i * kWg, r = v / (PASS / 8), c = v % (PASS / 8);
+            const bool ok = v < (uint32_t)XV && r < M && c * 8 < kvals;
+            const float* src = (const float*)op.x + (ok ? (size_t)r * K + kbase + c * 8 : 0);
+            xa[i] = *(const u32x4*)src;
+            xb[i] = *(const u32x4*)(src + 4);
+        }
+    }
+
+    // Stage codes and activations, then (after a barrier) decode the pass's
+    // block headers into per-group scale and bias.
+    __device__ __forceinline__ void stage(uint32_t kvals, uint32_t M, uint32_t* status) {
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t p = i * 64 + lane;
+            if (p < (uint32_t)(kRows * PPR)) *(u32x4*)(wstage + (p / PPR) * ROWB + (p % PPR) * 16) = w[i];
+        }
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const uint32_t v = tid + i * kWg, r = v / (PASS / 8), c = v % (PASS / 8);
+            float x[8], hi[8], lo[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = __uint_as_float(xa[i][e]);
+                x[4 + e] = __uint_as_float(xb[i][e]);
+            }
+            // Q4_K: values 32..63 of every 64 meet the high nibbles (16 q)
+            const float sc = (KIND == 12 && ((c * 8) & 32)) ? 0x1p60f : 0x1p64f;
+            float shi = 0.0f, slo = 0.0f;
+            if (v < (uint32_t)XV && r < M && c * 8 < kvals) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(x[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t hb = f32_to_bf16_rne_bits(x[e]);
+                const float h = __uint_as_float(hb << 16);
+                const uint32_t lb = f32_to_bf16_rne_bits(x[e] - h);
+                const float l = __uint_as_float(lb << 16);
+                shi += h;
+                slo += l;
+                hi[e] = h * sc;
+                lo[e] = l * sc;
+            }
+            // 8-bit pair order (x0,x2)(x1,x3)(x4,x6)(x5,x7)
+            u32x4 ph, pl;
+            ph[0] = perm(__float_as_uint(hi[2]), __float_as_uint(hi[0]), 0x07060302u);
+            ph[1] = perm(__float_as_uint(hi[3]), __float_as_uint(hi[1]), 0x07060302u);
+            ph[2] = perm(__float_as_uint(hi[6]), __float_as_uint(hi[4]), 0x07060302u);
+            ph[3] = perm(__float_as_uint(hi[7]), __float_as_uint(hi[5]), 0x07060302u);
+            pl[0] = perm(__float_as_uint(lo[2]), __float_as_uint(lo[0]), 0x07060302u);
+            pl[1] = perm(__float_as_uint(lo[3]), __float_as_uint(lo[1]), 0x07060302u);
+            pl[2] = perm(__float_as_uint(lo[6]), __float_as_uint(lo[4]), 0x07060302u);
+            pl[3] = perm(__float_as_uint(lo[7]), __float_as_uint(lo[5]), 0x07060302u);
+            // the 4 chunks of a 32-value group sit in consecutive lanes
+            shi += __shfl_xor(shi, 1, 64);
+            shi += __shfl_xor(shi, 2, 64);
+            slo += __shfl_xor(slo, 1, 64);
+            slo += __shfl_xor(slo, 2, 64);
+            if (v < (uint32_t)XV) {
+                lds.xp[2 * r][c] = ph;
+                lds.xp[2 * r + 1][c] = pl;
+                if ((c & 3) == 0) {
+                    lds.xs[2 * r][c >> 2] = shi;
+                    lds.xs[2 * r + 1][c >> 2] = slo;
+                }
+            }
+        }
+        // the reference's input finite check (weight_metal.rs:435-440)
+        if (__any(bad) && lane == 0) atomicOr(status, 1u);
+    }
+
+    // Per-group scale and bias of the pass from the staged block headers.
+    __device__ __forceinline__ void decode_meta(uint32_t kvals) {
+        const uint32_t nblk = kvals / BE;  // blocks of a row in this pass
+        if (KIND == 12) {
+            for (uint32_t t = tid; t < kRows * nblk; t += kWg) {
+                const uint32_t r = t % kRows, b = t / kRows;
+                const uint8_t* blk = (const uint8_t*)lds.stage[b / BPW] + r * ROWB + (b % BPW) * BB;
+                const u32x4 h = *(const u32x4*)blk;
+                const float d = f16_bits_to_f32(h[0] & 0xffffu), dmin = f16_bits_to_f32(h[0] >> 16);
+                const uint32_t q3[3] = {h[1], h[2], h[3]};
+#pragma unroll
+                for (uint32_t jj = 0; jj < 8; ++jj) {
+                    float scj, mj;
+                    scale_min(q3, jj, &scj, &mj);
+                    lds.sc[b * 8 + jj][r] = d * scj;
+                    lds.bi[b * 8 + jj][r] = -(dmin * mj);
+                }
+            }
+        } else {
+            for (uint32_t t = tid; t < kRows * nblk; t += kWg) {
+                const uint32_t r = t % kRows, b = t / kRows;
+                const uint8_t* blk = (const uint8_t*)lds.stage[b / BPW] + r * ROWB + (b % BPW) * BB;
+                const float d = f16_bits_to_f32(*(const uint16_t*)blk);
+                lds.sc[b][r] = d;
+                lds.bi[b][r] = -128.0f * d;  // codes enter as q + 128
+            }
+        }
+    }
+
+    // This lane's 32 codes of step s as 4 MFMA operands, and each operand's
+    // wave-local group and first value.
+    __device__ __forceinline__ void codes(int s, u32x4 (&bq)[4], uint32_t (&grp)[4], uint32_t (&e0)[4]) const {
+        const uint8_t* row = wstage + j * ROWB;
+        if (KIND == 12) {
+            const uint32_t sb = s / 2, p = 2 * (s % 2) + kq / 2, l0 = 16 * (kq % 2);
+            const u32x4 u = *(const u32x4*)(row + sb * BB + 16 + p * 32 + l0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t a = u[2 * (t >> 1)], b = u[2 * (t >> 1) + 1];
+                const uint32_t m = (t & 1) ? 0x00F000F0u : 0x000F000Fu;
+                bq[t][0] = a & m;
+                bq[t][1] = (a >> 8) & m;
+                bq[t][2] = b & m;
+                bq[t][3] = (b >> 8) & m;
+                grp[t] = sb * 8 + 2 * p + (t & 1);
+                e0[t] = sb * 256 + p * 64 + 32 * (t & 1) + l0 + 8 * (t >> 1);
+            }
+        } else {
+            const uint32_t lb = s * 4 + kq;                 // block of this lane
+            const uint32_t start = lb * BB + 2;             // first code byte
+            const uint32_t* base = (const uint32_t*)(row + (start & ~3u));
+            const uint32_t sh = start & 3u;                 // 0 or 2
+            uint32_t d9[9];
+#pragma unroll
+            for (int q = 0; q < 9; ++q) d9[q] = base[q];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                uint32_t a = __builtin_amdgcn_alignbyte(d9[2 * t + 1], d9[2 * t], sh) ^ 0x80808080u;
+                uint32_t b = __builtin_amdgcn_alignbyte(d9[2 * t + 2], d9[2 * t + 1], sh) ^ 0x80808080u;
+                bq[t][0] = a & 0x00FF00FFu;
+                bq[t][1] = (a >> 8) & 0x00FF00FFu;
+                bq[t][2] = b & 0x00FF00FFu;
+                bq[t][3] = (b >> 8) & 0x00FF00FFu;
+                grp[t] = lb;
+                e0[t] = lb * 32 + 8 * t;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void flush(uint32_t gbase, uint32_t glim, f32x4 (&C0)[MB], f32x4 (&C1)[MB],
+                                          f32x4 (&acc)[MB]) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const f32x4 c = C0[b] + C1[b];
+            const uint32_t g4 = gbase + (4 * kq) % S;
+            const uint32_t a = b * MP + (4 * kq) / S;
+            const f32x4 x4 = *(const f32x4*)&lds.xs[a][g4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float nv = fmaf(lds.sc[g4 + q][j] * 0x1p69f, c[q], fmaf(lds.bi[g4 + q][j], x4[q], acc[b][q]));
+                acc[b][q] = g4 + q < glim ? nv : acc[b][q];
+            }
+            C0[b] = C1[b] = f32x4{0, 0, 0, 0};
+        }
+    }
+
+    template <bool TAIL>
+    __device__ __forceinline__ void compute(uint32_t M, uint32_t kvals, f32x4 (&acc)[MB]) {
+        f32x4 C0[MB], C1[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) C0[b] = C1[b] = f32x4{0, 0, 0, 0};
+        const uint32_t qbase = wave * Q, gw = wave * GPW;
+        const uint32_t glim = TAIL ? min(kvals / 32, gw + GPW) : gw + GPW;
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s) {
+            u32x4 bq[4];
+            uint32_t grp[4], e0[4];
+            codes(s, bq, grp, e0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int b = 0; b < MB; ++b) {
+                    const uint32_t r = b * (MP / 2) + am / 2;  // real row of A row j
+                    bool act = grp[t] % S == aslot && r < M;
+                    if (TAIL) act = act && qbase + e0[t] < kvals;
+                    const u32x4 a = act ? lds.xp[b * MP + am][(qbase + e0[t]) / 8] : lds.zero[0];
+                    f32x4& cc = (t & 1) ? C1[b] : C0[b];
+                    cc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                               __builtin_bit_cast(bf16x8, bq[t]), cc, 0, 0, 0);
+                }
+            }
+            if ((s + 1) % PERIOD == 0 || s == NSTEP - 1) flush(gw + (s / PERIOD) * S, glim, C0, C1, acc);
+        }
+    }
+
+    __device__ __forceinline__ void run(const GgufOp& op, uint32_t n0, uint32_t M, uint32_t* status) {
+        const uint32_t K = op.k;
+        f32x4 acc[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[b] = f32x4{0, 0, 0, 0};
+        load(op, n0, M, 0);
+        for (uint32_t kbase = 0; kbase < K; kbase += PASS) {
+            const uint32_t kvals = min((uint32_t)PASS, K - kbase);
+            if (kbase) __syncthreads();
+            stage(kvals, M, status);
+            __syncthreads();
+            if (kbase + PASS < K) load(op, n0, M, kbase + PASS);
+            decode_meta(kvals);
+            __syncthreads();
+            if (kvals == (uint32_t)PASS)
+                compute<false>(M, kvals, acc);
+            else
+                compute<true>(M, kvals, acc);
+        }
+        // lane's slots sum to one activation row's share; hi and lo rows meet
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            float v = (acc[b][0] + acc[b][1]) + (acc[b][2] + acc[b][3]);
+            if (S == 8) {  // kq 0,1: hi; kq 2,3: lo
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                if (kq == 0) lds.red[wave][b * (MP / 2)][j] = v;
+            } else {  // S == 4: lane row a = kq; real row kq / 2
+                v += __shfl_xor(v, 16, 64);
+                if ((kq & 1) == 0) lds.red[wave][b * (MP / 2) + kq / 2][j] = v;
+            }
+        }
+        __syncthreads();
+    }
+};
+
+template <int KIND, int MP, int MB>
+__global__ __launch_bounds__(kWg) void gguf_mfma(GgufBatch batch) {
+    (void)batch;
+    __shared__ GLds<KIND, MP, MB> lds;
+    const GgufBatch* kb = (const GgufBatch*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t oi = 0;
+    for (uint32_t i = 1; i < kb->count; ++i)
+        if (blockIdx.x >= kb->op[i].block_begin) oi = i;
+    const GgufOp& op = kb->op[oi];
+    const uint32_t N = op.n;
+    const uint32_t t0 = (blockIdx.x - op.block_begin) * kRows;
+    const uint32_t n0 = min(t0, N - kRows);  // last tile moved back to end at N
+    GEngine<KIND, MP, MB> e(lds);
+    e.run(op, n0, op.m, kb->status);
+    constexpr int RR = MP * MB / 2;
+    for (uint32_t t = threadIdx.x; t < (uint32_t)RR * kRows; t += kWg) {
+        const uint32_t m = t / kRows, r = t % kRows, n = n0 + r;
+        if (m >= op.m || n < t0) continue;
+        const float v = (lds.red[0][m][r] + lds.red[1][m][r]) + (lds.red[2][m][r] + lds.red[3][m][r]);
+        store_from_f32(op.d, op.d_dt, (size_t)m * N + n, v);
+    }
+}
+
+template <int KIND, int MP, int MB>
+stark_qmm_status launch_mfma(const GgufOp* ops, uint32_t count, uint32_t* status, hipStream_t stream) {
     GgufBatch batch{};
+    batch.status = status;
     uint32_t blocks = 0;
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = ops[i];
         batch.op[i].block_begin = blocks;
-        blocks += ((ops[i].n + kRows - 1) / kRows) * ((ops[i].m + mt - 1) / mt);
+        blocks += (ops[i].n + kRows - 1) / kRows;
     }
     batch.count = count;
-    if (blocks) launch(batch, blocks);
+    if (blocks) hipLaunchKernelGGL((gguf_mfma<KIND, MP, MB>), dim3(blocks), dim3(kWg), 0, stream, batch);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
 }
 
-bool fast_eligible(const GgufOp& o) {
-    if (((uintptr_t)o.blocks & 15) != 0) return false;
-    if (o.kind == 12) return o.k % 256 == 0;
-    return o.k % 256 == 0;  // Q8_0: rows of 8-block multiples stay 16-byte aligned
+template <int KIND>
+stark_qmm_status launch_class(int c, const GgufOp* ops, uint32_t count, uint32_t* status, hipStream_t stream) {
+    switch (c) {
+    case 0: return launch_mfma<KIND, 2, 1>(ops, count, status, stream);
+    case 1: return launch_mfma<KIND, 4, 1>(ops, count, status, stream);
+    case 2: return launch_mfma<KIND, 4, 2>(ops, count, status, stream);
+    default: return launch_mfma<KIND, 4, 4>(ops, count, status, stream);
+    }
 }
+
+// matrix-core kernel: f32 activations, 16-byte aligned rows, at least one tile
+bool mfma_ok(const GgufOp& o) {
+    if (((uintptr_t)o.blocks & 15) || ((uintptr_t)o.x & 15) || o.k % 256 || o.n < (uint32_t)kRows) return false;
+    return o.x_dt == STARK_QMM_F32;
+}
+
+int m_class(uint32_t m) { return m <= 1 ? 0 : m <= 2 ? 1 : m <= 4 ? 2 : 3; }
 
 }  // namespace
 
 bool gguf_supported(uint32_t kind) { return kind == 8 || kind == 12; }
 
-stark_qmm_status launch_gguf_gemv(const GgufOp* ops, uint32_t count, hipStream_t stream) {
-    std::vector<GgufOp> q4, q8;
+stark_qmm_status launch_gguf_gemv(const GgufOp* ops, uint32_t count, uint32_t* status, hipStream_t stream) {
+    std::vector<GgufOp> cls[2][4];
     for (uint32_t i = 0; i < count; ++i) {
         GgufOp o = ops[i];
         if (o.x_dt == 0 && o.d_dt == 0) {
@@ -331,32 +477,35 @@ stark_qmm_status launch_gguf_gemv(const GgufOp* ops, uint32_t count, hipStream_t
             o.d_dt = STARK_QMM_F32;
         }
         if (o.n == 0 || o.m == 0) continue;
-        if (!fast_eligible(o)) {
+        if (!mfma_ok(o)) {
+            if (o.x_dt == STARK_QMM_F32) {
+                const stark_qmm_status st = launch_finite_check((const float*)o.x, (uint64_t)o.m * o.k, status, stream);
+                if (st != STARK_QMM_OK) return st;
+            }
             hipLaunchKernelGGL(gguf_generic, dim3((o.n + 255) / 256, o.m), dim3(256), 0, stream, o);
             QMM_HIP_CHECK(hipGetLastError());
             continue;
         }
-        (o.kind == 12 ? q4 : q8).push_back(o);
-    }
-    for (int kind : {12, 8}) {
-        std::vector<GgufOp>& v = kind == 12 ? q4 : q8;
-        for (size_t s = 0; s < v.size(); s += kMaxBatchOps) {
-            const uint32_t c = (uint32_t)std::min<size_t>(kMaxBatchOps, v.size() - s);
-            bool mt2 = false;
-            for (uint32_t i = 0; i < c; ++i) mt2 |= v[s + i].m >= 2;
-            const int mt = mt2 ? 2 : 1;
-            stark_qmm_status st = launch_batched(v.data() + s, c, mt, [&](const GgufBatch& b, uint32_t blocks) {
-                if (kind == 12) {
-                    if (mt2) hipLaunchKernelGGL(q4k_gemv<2>, dim3(blocks), dim3(kThreads), 0, stream, b);
-                    else hipLaunchKernelGGL(q4k_gemv<1>, dim3(blocks), dim3(kThreads), 0, stream, b);
-                } else {
-                    if (mt2) hipLaunchKernelGGL(q8_0_gemv<2>, dim3(blocks), dim3(kThreads), 0, stream, b);
-                    else hipLaunchKernelGGL(q8_0_gemv<1>, dim3(blocks), dim3(kThreads), 0, stream, b);
-                }
-            });
-            if (st != STARK_QMM_OK) return st;
+        // up to 8 activation rows per product; more rows are split
+        const size_t xsz = 4, dsz = o.d_dt == STARK_QMM_F32 ? 4 : 2;
+        for (uint32_t m0 = 0; m0 < o.m; m0 += 8) {
+            GgufOp p = o;
+            p.m = std::min<uint32_t>(8, o.m - m0);
+            p.x = (const uint8_t*)o.x + (size_t)m0 * o.k * xsz;
+            p.d = (uint8_t*)o.d + (size_t)m0 * o.n * dsz;
+            cls[o.kind == 12][m_class(p.m)].push_back(p);
         }
     }
+    for (int q4 = 0; q4 < 2; ++q4)
+        for (int c = 0; c < 4; ++c) {
+            std::vector<GgufOp>& v = cls[q4][c];
+            for (size_t s = 0; s < v.size(); s += kMaxBatchOps) {
+                const uint32_t n = (uint32_t)std::min<size_t>(kMaxBatchOps, v.size() - s);
+                const stark_qmm_status st = q4 ? launch_class<12>(c, v.data() + s, n, status, stream)
+                                               : launch_class<8>(c, v.data() + s, n, status, stream);
+                if (st != STARK_QMM_OK) return st;
+            }
+        }
     return STARK_QMM_OK;
 }
 
