@@ -408,7 +408,7 @@ struct GEngine {
 };
 
 template <int KIND, int MP, int MB>
-__global__ __launch_bounds__(kWg) void gguf_mfma(GgufBatch batch) {
+__global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(MB >= 4 ? 2 : (MB >= 2 || MP >= 4 || KIND == 8) ? 2 : 3))) void gguf_mfma(GgufBatch batch) {
     (void)batch;
     __shared__ GLds<KIND, MP, MB> lds;
     const GgufBatch* kb = (const GgufBatch*)__builtin_amdgcn_kernarg_segment_ptr();
