@@ -58,18 +58,8 @@ QMM_DEVICE float wave_sum(float v) {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// 16-byte load of weight codes that are read exactly once per launch
-// (QMM_STREAM_NT=0 builds plain cached loads instead of nontemporal ones).
-#ifndef QMM_STREAM_NT
-#define QMM_STREAM_NT 1
-#endif
-QMM_DEVICE u32x4 load_stream(const void* p) {
-#if QMM_STREAM_NT
-    return __builtin_nontemporal_load((const u32x4*)p);
-#else
-    return *(const u32x4*)p;
-#endif
-}
+// 16-byte nontemporal load of weight codes that are read exactly once per launch.
+QMM_DEVICE u32x4 load_stream(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
 
 // (a & mask) | orv in one VALU op: gfx950 VOP3 takes no literal, so the mask
 // rides in an SGPR and the or-value in a VGPR.

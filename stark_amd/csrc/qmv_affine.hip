@@ -573,12 +573,10 @@ stark_qmm_status launch_affine_gemv(const AffineOp* ops_in, uint32_t count_in, i
     std::vector<AffineOp> mfma, decode, others;
     for (uint32_t i = 0; i < count_in; ++i) {
         const AffineOp& o = ops_in[i];
-#ifndef QMM_DISABLE_MFMA
         if (mfma_eligible(o, bits)) {
             mfma.push_back(o);
             continue;
         }
-#endif
         (decode_eligible(o, bits) ? decode : others).push_back(o);
     }
     if (!mfma.empty()) {

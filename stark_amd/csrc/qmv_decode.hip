@@ -20,12 +20,6 @@
 // 16-byte aligned buffers, M <= 2.
 #include "qmm_common.h"
 
-// Build-time switch for performance attribution only (0 = normal): 1 skips the
-// activation loads, 2 skips the metadata loads, 3 skips the dot products.
-#ifndef QMM_DECODE_EXPERIMENT
-#define QMM_DECODE_EXPERIMENT 0
-#endif
-
 namespace qmm {
 
 namespace {
@@ -186,10 +180,6 @@ __global__ __launch_bounds__(kWgThreads) void qmv_w4_decode(AffineBatch batch) {
                     pr[d][2] = ((u >> 5) & nib) | one2;
                     pr[d][3] = ((u >> 9) & nib) | one2;
                 }
-#if QMM_DECODE_EXPERIMENT == 3
-                acc[r][0] += __uint_as_float(pr[0][0] ^ pr[1][1] ^ pr[2][2] ^ pr[3][3] ^ xr[0][r]) + e.x;
-                continue;
-#endif
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     float d0 = dot2_bf16(pr[0][0], xr[m][0], 0.0f);
