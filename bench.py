@@ -455,6 +455,57 @@ def config4(args, torch, Q):
                       "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_MFMA_BF16_TFLOPS,
                                    "unit": "TFLOP/s", "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4),
                                    "traffic": None}}))
+    if args.decode_tokens:
+        decode_line(args, torch)
+
+
+def decode_line(args, torch):
+    """Config 4 (decode part): random-init Qwen3-8B architecture (36 layers,
+    32/8 heads of 128, intermediate 12288, vocab 151936; W4 g64 projections,
+    W8 g64 lm_head, bf16 KV cache), a 4096-token context whose KV rows are
+    synthetic N(0,1), then greedy tokens generated one HIP-graph replay each.
+    Value: generated tokens per second over the timed tokens."""
+    from stark_amd import decode as DEC
+    cfg = DEC.Qwen3Config()
+    ctx, gen_tokens = 4096, args.decode_tokens
+    m = DEC.Qwen3Decoder(cfg, capacity=ctx + gen_tokens + 8, seed=SEED + 40)
+    m.fill_context(ctx, seed=SEED + 41)
+    m.step()  # eager: builds the library's per-shape schedules
+    torch.cuda.synchronize()
+    graph = m.capture()
+    warm = 3
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    timed_tokens = gen_tokens - 1 - warm
+    a.record(stream)
+    for _ in range(timed_tokens):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / timed_tokens
+    assert int(m.pos.item()) == ctx + gen_tokens, "device position did not advance once per token"
+    tps = 1000.0 / ms
+    H, I, hd = cfg.hidden, cfg.intermediate, cfg.head_dim
+    layer_bytes = algorithmic_bytes()
+    lm_bytes = cfg.vocab * H * (1 + 4 / GROUP) + H * 2 + cfg.vocab * 4
+    mid = ctx + gen_tokens // 2
+    kv_bytes = cfg.layers * 2 * cfg.kv_heads * mid * hd * 2
+    per_token = cfg.layers * layer_bytes + lm_bytes + kv_bytes + H * 2
+    gbs = per_token * tps / 1e9
+    print(json.dumps({"metric": "Qwen3-8B W4 end-to-end greedy decode tokens/s", "value": round(tps, 1),
+                      "unit": "tokens/s", "n_gpus": 1, "steps": timed_tokens, "warmup": warm + 1,
+                      "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                      "dtype": "bf16",
+                      "data": "synthetic: random-init weights (W4 g64, W8 g64 lm_head), KV of a 4096-token context "
+                              "filled N(0,1), uniform random prompt token",
+                      "config": {"workload": f"config 4 decode: {gen_tokens} greedy tokens after a {ctx}-token "
+                                             "context, one HIP graph replay per token",
+                                 "hbm_bytes_per_token_algorithmic": per_token},
+                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
 
 
 def main():
@@ -466,6 +517,8 @@ def main():
                     help="1: Qwen3-8B W4 layer set (headline); 2: 8-bit / Q8_0 / Q4_K; 3: Qwen3-30B-A3B MoE layer; "
                          "4: prefill dequant-GEMM at M=2048")
     ap.add_argument("--tokens", type=int, nargs="+", default=[1, 4, 16], help="config 3 tokens per step")
+    ap.add_argument("--decode-tokens", type=int, default=256,
+                    help="config 4: greedy tokens generated after the 4096-token context (0 skips the decode line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copies", type=int, default=LAYERS,
                     help="config 1: distinct layer-weight copies the steps rotate through (36 = one Qwen3-8B)")

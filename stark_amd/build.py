@@ -1,4 +1,6 @@
-"""Compile the HIP sources under stark_amd/csrc into stark_amd/libstark_qmm.so (gfx950)."""
+"""Compile the HIP sources under stark_amd/csrc into stark_amd/libstark_qmm.so (gfx950),
+and the decode-step kernels of the end-to-end stand-in (stark_amd/csrc_decode) into
+stark_amd/libstark_decode.so."""
 from __future__ import annotations
 
 import concurrent.futures as cf
@@ -11,6 +13,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libstark_qmm.so")
+CSRC_DECODE = os.path.join(HERE, "csrc_decode")
+DECODE_LIB = os.path.join(HERE, "libstark_decode.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [
@@ -32,18 +36,24 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 8) -> str:
-    os.makedirs(OBJ, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    with cf.ThreadPoolExecutor(max_workers=min(jobs, len(sources))) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB + ".tmp"
+def _link(objs, lib):
+    tmp = lib + ".tmp"
     r = subprocess.run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp],
                        capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
+
+
+def build(jobs: int = 8) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    decode_sources = sorted(glob.glob(os.path.join(CSRC_DECODE, "*.hip")))
+    with cf.ThreadPoolExecutor(max_workers=min(jobs, len(sources) + len(decode_sources))) as ex:
+        objs = list(ex.map(_compile, sources + decode_sources))
+    _link(objs[len(sources):], DECODE_LIB)
+    return _link(objs[:len(sources)], LIB)
 
 
 if __name__ == "__main__":

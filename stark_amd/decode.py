@@ -1,0 +1,215 @@
+"""End-to-end decode stand-in for BASELINE config 4: a random-init
+Qwen3-architecture decoder whose every weight product runs through the
+quantized matrix-product library (libstark_qmm: 4-bit MLX-affine layer
+projections, an 8-bit lm_head), with the decode-step kernels of
+libstark_decode around them (RMSNorm, per-head q/k norm + RoPE + KV write,
+GQA flash-decoding attention over a bf16 cache, gated SiLU, greedy argmax).
+
+A token step is one fixed sequence of launches that reads the position from
+device memory, so it is captured once in a HIP graph and replayed per token.
+
+Not a Stark component: Stark's own decoder is its Rust model runtime
+(crates/stark-engine/src/encodable_block/transformer_layer.rs). This module
+exists to measure tokens/s of the quantized path in a real decode loop.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import torch
+
+from . import qmm as Q
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(HERE, "libstark_decode.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+        L = C.CDLL(path)
+        vp, u32, f32, ip = C.c_void_p, C.c_uint32, C.c_float, C.c_void_p
+        L.stark_decode_rms_norm.argtypes = [vp, vp, vp, u32, f32, vp]
+        L.stark_decode_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, vp, ip, u32, u32, u32, f32, f32, vp]
+        L.stark_decode_attn_chunks.argtypes = [u32]
+        L.stark_decode_attn_chunks.restype = u32
+        L.stark_decode_attention.argtypes = [vp, vp, vp, vp, vp, vp, ip, u32, u32, u32, vp]
+        L.stark_decode_silu_mul.argtypes = [vp, vp, vp, u32, vp]
+        L.stark_decode_argmax.argtypes = [vp, u32, ip, ip, ip, u32, vp]
+        L.stark_decode_embed.argtypes = [vp, ip, vp, u32, u32, vp]
+        _LIB = L
+    return _LIB
+
+
+def _ok(st, what):
+    if st != 0:
+        raise RuntimeError(f"{what}: status {st}")
+
+
+@dataclass
+class Qwen3Config:
+    hidden: int = 4096
+    layers: int = 36
+    q_heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 12288
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+    group: int = 64
+
+
+def quantize_affine_gpu(w: torch.Tensor, bits: int = 4, group: int = 64):
+    """MLX affine by BASELINE's rule: per group scale = (max - min)/(2^bits - 1)
+    and bias = min as bf16, q = clamp(round((w - bias)/scale)); codes
+    little-endian (low nibble first for 4-bit); planes in the converter's
+    group-output layout [G][N] (N % 4 == 0). Returns (codes u8, scales, biases)
+    with the planes as int16 bit patterns."""
+    n, k = w.shape
+    g = w.view(n, k // group, group)
+    mn, mx = g.amin(dim=2), g.amax(dim=2)
+    levels = (1 << bits) - 1
+    s = ((mx - mn) / float(levels)).to(torch.bfloat16)
+    b = mn.to(torch.bfloat16)
+    sf, bf = s.float().unsqueeze(2), b.float().unsqueeze(2)
+    q = torch.where(sf > 0, torch.round((g - bf) / torch.where(sf > 0, sf, torch.ones_like(sf))),
+                    torch.zeros_like(g)).clamp(0, levels).to(torch.uint8).view(n, k)
+    codes = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous() if bits == 4 else q.contiguous()
+    return codes, s.t().contiguous().view(torch.int16), b.t().contiguous().view(torch.int16)
+
+
+class Qwen3Decoder:
+    """Random-init Qwen3-architecture decoder on one GPU (bf16 activations and
+    KV cache; weights quantized W4 g64, lm_head W8 g64; embeddings bf16)."""
+
+    def __init__(self, cfg: Qwen3Config, capacity: int, seed: int = 0, device: str = "cuda"):
+        self.cfg, self.cap = cfg, capacity
+        H, I, hd = cfg.hidden, cfg.intermediate, cfg.head_dim
+        qd, kd = cfg.q_heads * hd, cfg.kv_heads * hd
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        dev = torch.device(device)
+
+        def randn(*shape, std=0.02):
+            return torch.randn(*shape, generator=gen, device=dev) * std
+
+        def qmat(n, k, bits=4):
+            codes, s, b = quantize_affine_gpu(randn(n, k), bits, cfg.group)
+            return dict(n=n, k=k, bits=bits, codes=codes, scales=s, biases=b)
+
+        def norm_w(n):
+            return (1.0 + randn(n, std=0.05)).to(torch.bfloat16)
+
+        self.embed = randn(cfg.vocab, H).to(torch.bfloat16)
+        self.layers = []
+        for _ in range(cfg.layers):
+            self.layers.append(dict(
+                attn_norm=norm_w(H), mlp_norm=norm_w(H), q_norm=norm_w(hd), k_norm=norm_w(hd),
+                q=qmat(qd, H), k=qmat(kd, H), v=qmat(kd, H), o=qmat(H, qd),
+                gate=qmat(I, H), up=qmat(I, H), down=qmat(H, I),
+                kcache=torch.zeros(cfg.kv_heads, capacity, hd, dtype=torch.bfloat16, device=dev),
+                vcache=torch.zeros(cfg.kv_heads, capacity, hd, dtype=torch.bfloat16, device=dev)))
+        self.final_norm = norm_w(H)
+        self.lm_head = qmat(cfg.vocab, H, bits=8)
+        # activations and scratch
+        bf16 = torch.bfloat16
+        self.x = torch.zeros(H, dtype=bf16, device=dev)
+        self.h = torch.zeros(H, dtype=bf16, device=dev)
+        self.q = torch.zeros(qd, dtype=bf16, device=dev)
+        self.k = torch.zeros(kd, dtype=bf16, device=dev)
+        self.v = torch.zeros(kd, dtype=bf16, device=dev)
+        self.attn = torch.zeros(qd, dtype=bf16, device=dev)
+        self.g = torch.zeros(I, dtype=bf16, device=dev)
+        self.u = torch.zeros(I, dtype=bf16, device=dev)
+        self.a = torch.zeros(I, dtype=bf16, device=dev)
+        self.logits = torch.zeros(cfg.vocab, dtype=torch.float32, device=dev)
+        nch = lib().stark_decode_attn_chunks(capacity)
+        self.po = torch.zeros(cfg.q_heads * nch * hd, dtype=torch.float32, device=dev)
+        self.pml = torch.zeros(cfg.q_heads * nch * 2, dtype=torch.float32, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.history = torch.zeros(capacity + 1, dtype=torch.int32, device=dev)
+        self.kern4 = Q.MatmulKernel(Q.BF16, Q.BF16, Q.BF16)
+        self.kern_lm = Q.MatmulKernel(Q.BF16, Q.BF16, Q.F32)
+        self._prepare()
+        self.graph = None
+
+    def _args(self, mat, a, d, accumulate=False):
+        return Q.MatmulArguments(
+            a=a, m=1, n=mat["n"], k=mat["k"], d=d,
+            b=Q.QuantizedB(codes=mat["codes"], scales=mat["scales"], correction_data=mat["biases"],
+                           mode=Q.MODE_U4 if mat["bits"] == 4 else Q.MODE_U8, group_size=self.cfg.group,
+                           params=Q.QuantParams(Q.GROUP_OUTPUT, mat["n"], mat["k"] // self.cfg.group)),
+            d_transform=Q.MatmulDOps(accumulate=accumulate))
+
+    def _prepare(self):
+        K4 = self.kern4
+        self.batches = []
+        for L in self.layers:
+            self.batches.append(dict(
+                qkv=K4.prepare_many([self._args(L["q"], self.h, self.q), self._args(L["k"], self.h, self.k),
+                                     self._args(L["v"], self.h, self.v)]),
+                o=K4.prepare_many([self._args(L["o"], self.attn, self.x, accumulate=True)]),
+                gu=K4.prepare_many([self._args(L["gate"], self.h, self.g), self._args(L["up"], self.h, self.u)]),
+                down=K4.prepare_many([self._args(L["down"], self.a, self.x, accumulate=True)])))
+        self.lm_batch = self.kern_lm.prepare_many([self._args(self.lm_head, self.h, self.logits)])
+
+    def fill_context(self, length: int, seed: int = 1):
+        """Synthetic KV for a prompt of `length` tokens (values N(0, 1) in bf16)
+        and the position set to `length`; the last prompt token is drawn
+        uniformly from the vocabulary."""
+        gen = torch.Generator(device=self.x.device)
+        gen.manual_seed(seed)
+        for L in self.layers:
+            L["kcache"][:, :length].normal_(0, 1, generator=gen)
+            L["vcache"][:, :length].normal_(0, 1, generator=gen)
+        self.pos.fill_(length)
+        self.token.fill_(int(torch.randint(0, self.cfg.vocab, (1,), generator=gen, device=self.x.device).item()))
+
+    def step(self, stream=None):
+        """One greedy token: embed the current token, run every layer at the
+        current position, lm_head, argmax; advances the device position."""
+        cfg, D = self.cfg, lib()
+        s = stream if stream is not None else torch.cuda.current_stream()
+        sp = C.c_void_p(s.cuda_stream)
+        H, I = cfg.hidden, cfg.intermediate
+        p = lambda t: C.c_void_p(t.data_ptr())
+        _ok(D.stark_decode_embed(p(self.embed), p(self.token), p(self.x), H, cfg.vocab, sp), "embed")
+        for L, B in zip(self.layers, self.batches):
+            _ok(D.stark_decode_rms_norm(p(self.x), p(L["attn_norm"]), p(self.h), H, cfg.eps, sp), "attn_norm")
+            self.kern4.encode_prepared(B["qkv"], s)
+            _ok(D.stark_decode_qk_norm_rope(p(self.q), p(self.k), p(self.v), p(L["q_norm"]), p(L["k_norm"]),
+                                            p(L["kcache"]), p(L["vcache"]), p(self.pos), cfg.q_heads, cfg.kv_heads,
+                                            self.cap, cfg.rope_theta, cfg.eps, sp), "qk_norm_rope")
+            _ok(D.stark_decode_attention(p(self.q), p(L["kcache"]), p(L["vcache"]), p(self.po), p(self.pml),
+                                         p(self.attn), p(self.pos), cfg.q_heads, cfg.kv_heads, self.cap, sp),
+                "attention")
+            self.kern4.encode_prepared(B["o"], s)
+            _ok(D.stark_decode_rms_norm(p(self.x), p(L["mlp_norm"]), p(self.h), H, cfg.eps, sp), "mlp_norm")
+            self.kern4.encode_prepared(B["gu"], s)
+            _ok(D.stark_decode_silu_mul(p(self.g), p(self.u), p(self.a), I, sp), "silu_mul")
+            self.kern4.encode_prepared(B["down"], s)
+        _ok(D.stark_decode_rms_norm(p(self.x), p(self.final_norm), p(self.h), H, cfg.eps, sp), "final_norm")
+        self.kern_lm.encode_prepared(self.lm_batch, s)
+        _ok(D.stark_decode_argmax(p(self.logits), cfg.vocab, p(self.token), p(self.pos), p(self.history),
+                             self.history.numel(), sp),
+            "argmax")
+
+    def capture(self):
+        """Capture one token step in a graph (after one eager step has built
+        the library's per-shape schedules)."""
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self.step(s)
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = g
+        return g
