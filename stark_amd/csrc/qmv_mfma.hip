@@ -99,31 +99,39 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(kWavesPerEu
     }
 }
 
+// Workgroups of `kern` that fit the device at once (a multiple of 8), cached
+// per (kernel, device).
 template <class Kern>
 uint32_t persistent_grid(Kern kern) {
-    static int cached = 0;
-    if (!cached) {
-        int dev = 0, cus = 0, per_cu = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kWg, 0) != hipSuccess)
-            return 0;
-        cached = std::max(8, cus * std::max(per_cu, 1) / 8 * 8);
-    }
-    return (uint32_t)cached;
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, uint32_t> cache;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair((const void*)kern, dev);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kWg, 0) != hipSuccess)
+        return 0;
+    const uint32_t grid = (uint32_t)std::max(8, cus * std::max(per_cu, 1) / 8 * 8);
+    cache.emplace(key, grid);
+    return grid;
 }
 
 // Device copy of the schedule of a shape set (ops in launch order: tile
-// count and K each) for `grid` workgroups, built on first use and kept for
-// the life of the process (a few KiB per distinct shape set and device).
-bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* out) {
+// count and K each) for `grid` workgroups and tiles of `rows` rows, built on
+// first use and kept for the life of the process (a few KiB per distinct
+// shape set and device). The tiles that share the 128-byte lines of the
+// group-output planes (64 rows) go to one XCD.
+bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* out, uint32_t rows = kRows) {
     static std::mutex mu;
     static std::map<std::vector<uint32_t>, Schedule> cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
-    std::vector<uint32_t> key{(uint32_t)dev, grid};
+    std::vector<uint32_t> key{(uint32_t)dev, grid, rows};
     for (uint32_t i = 0; i < count; ++i) {
-        key.push_back((ops[i].n + kRows - 1) / kRows);
+        key.push_back((ops[i].n + rows - 1) / rows);
         key.push_back(ops[i].k);
     }
     std::lock_guard<std::mutex> lock(mu);
@@ -135,14 +143,16 @@ bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* 
     const uint32_t per_xcd = grid / 8;
     std::vector<std::vector<uint32_t>> lists(grid);
     std::vector<uint64_t> load(grid, 0);
-    // tiles per XCD in quad order; ops are already longest-K first, so a
-    // stable walk deals the costliest tiles first
+    // tiles per XCD in line-group order; ops are already longest-K first, so
+    // a stable walk deals the costliest tiles first
     std::vector<std::vector<std::pair<uint32_t, uint32_t>>> xcd_tiles(8);  // (entry, cost)
+    const uint32_t per_line = std::max(1u, 64 / rows);
     uint32_t quad = 0;
     for (uint32_t i = 0; i < count; ++i) {
-        const uint32_t tiles = (ops[i].n + kRows - 1) / kRows;
-        for (uint32_t t0 = 0; t0 < tiles; t0 += 4, ++quad)
-            for (uint32_t t = t0; t < std::min(tiles, t0 + 4); ++t) xcd_tiles[quad % 8].push_back({(i << 24) | t, ops[i].k});
+        const uint32_t tiles = (ops[i].n + rows - 1) / rows;
+        for (uint32_t t0 = 0; t0 < tiles; t0 += per_line, ++quad)
+            for (uint32_t t = t0; t < std::min(tiles, t0 + per_line); ++t)
+                xcd_tiles[quad % 8].push_back({(i << 24) | t, ops[i].k});
     }
     for (uint32_t x = 0; x < 8; ++x) {
         for (const auto& et : xcd_tiles[x]) {
@@ -171,6 +181,333 @@ bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* 
     cache.emplace(std::move(key), s);
     *out = s;
     return true;
+}
+
+// ---------------------------------------------------------------------------
+// Streaming kernel for one activation row of 4-bit codes, group size 64 and
+// K % 4096 == 0 (the decode shapes). Same arithmetic as TileEngine -- codes as
+// raw bf16 bit patterns, one-hot activation rows per group slot, one f32 flush
+// per group -- with a load layout built for HBM streaming:
+//  - Split columns. B column c = 8*hh + r of the MFMA holds row r of an 8-row
+//    subtile, byte half hh of a 128-byte block: lane r + 8*hh + 16*kb loads the
+//    16 bytes at 16*(4*hh + kb) of the block. One load instruction then covers
+//    128 contiguous bytes (whole cache lines) of each of 8 rows, and the codes
+//    go straight from the load into the MFMA operand with no LDS transpose.
+//    A rows 8*hh .. 8*hh+7 are the 8 group slots of byte half hh (x at that
+//    half's positions); the C entries that pair one half's activations with
+//    the other half's codes are never read.
+//  - Tiles of 32 rows (4 subtiles), units of 1024 k. A unit is 16 steps
+//    (4 k-blocks of 256 x 4 subtiles, 16 KiB of codes) and one flush period
+//    (16 groups per row, 8 per byte half). Wave w takes chunks w, w+4, ... of
+//    every tile; the four waves of a workgroup meet once per tile, at an
+//    LDS-only barrier. The scale and bias planes of a unit are 16 groups x 32
+//    rows: half cache lines in the group-output layout, whose other half is
+//    the neighbouring tile's, scheduled on the same XCD.
+//  - Loads in flight. A ring of 8 step registers, refilled 8 steps ahead
+//    across unit, tile and barrier boundaries (8 KiB per wave in flight). Two
+//    workgroups per CU: more bytes in flight only lengthen the queues.
+//  - Activations are staged per wave (no barrier) into one of kXR regions
+//    tagged (op, chunk), so consecutive tiles of an op reuse them; the plane
+//    vectors of a unit are loaded with the unit and pass through a
+//    wave-private LDS block at the flush.
+constexpr int kXR = 3;         // activation regions per wave
+constexpr int kTR = 32;        // tile rows
+constexpr int kUnitK = 1024;   // k values per unit (16 groups of 64)
+constexpr int kListLds = 256;  // schedule entries staged in LDS at kernel start
+
+struct StreamLds {
+    u32x4 xp[4][kXR][kUnitK / 8];  // activation pairs (x0,x4)(x1,x5).. per 8 values; x*2^64, odd values x*2^60
+    float xs[4][kXR][kUnitK / 64];  // activation sum per group
+    f32x4 pl[4][kTR * 8];          // (scale * 2^69, bias term) of [row][group] of the wave's unit
+    float red[2][4][kTR];           // per-wave row sums, double-buffered by tile parity
+    u32x4 zero[4][4];
+    uint32_t list[kListLds];        // the workgroup's first kListLds schedule entries
+};
+
+template <int AUX = 0>
+__device__ __forceinline__ u32x4 buf_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)bytes, 0x00020000);
+}
+
+template <bool SIGNED>
+__global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void qmv_stream(AffineBatch batch, Schedule sched) {
+    (void)batch;
+    constexpr uint32_t UB = kUnitK / 2;    // bytes of a row per unit
+    constexpr uint32_t OOB = 0x80000000u;  // buffer offset past every resource: reads zero, no traffic
+    constexpr uint32_t PLANE = 0x7fffffffu;  // plane resources: addressed by the op's strides
+    __shared__ StreamLds lds;
+    const AffineBatch* kb_ = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
+    typedef const __attribute__((address_space(4))) uint32_t cu32;
+    const uint32_t lo = ((cu32*)sched.begin)[blockIdx.x], hi = ((cu32*)sched.begin)[blockIdx.x + 1];
+    if (lo >= hi) return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // lane roles: c16 = B/C column = (byte half hh, subtile row r), kb = k block
+    const uint32_t c16 = lane & 15, kb = lane >> 4, hh = c16 >> 3, r = lane & 7;
+    const uint32_t piece = 16 * (4 * hh + kb);  // this lane's 16 bytes of a row's 128-byte block
+    if (lane < 4) lds.zero[wave][lane] = u32x4{0, 0, 0, 0};
+    // The workgroup's schedule entries go to LDS once, so that no unit waits on
+    // a scalar miss for its successor.
+    for (uint32_t t = tid; t < min(hi - lo, (uint32_t)kListLds); t += kWg) lds.list[t] = sched.tiles[lo + t];
+    __syncthreads();
+    const auto entry = [&](uint32_t t) {
+        return t - lo < (uint32_t)kListLds ? __builtin_amdgcn_readfirstlane(lds.list[t - lo])
+                                           : ((cu32*)sched.tiles)[t];
+    };
+    const auto tile_row = [&](const AffineOp& op, uint32_t e) {  // first bank row of the tile
+        return min((e & 0xffffffu) * kTR, op.n - kTR);
+    };
+
+    u32x4 ring[8];
+    u32x4 xv[2], pls, plb;  // plb reads zero when the op has no bias plane
+    // Activations (when need_x) and plane vectors of unit (op, tile at n0, chunk c).
+    const auto issue_aux = [&](const AffineOp& op, uint32_t n0, uint32_t c, bool need_x) {
+        const __amdgpu_buffer_rsrc_t xr = rsrc(op.x, op.k * 2);
+        const uint32_t xo = need_x ? (c * kUnitK + lane * 8) * 2 : OOB;
+        xv[0] = buf_load(xr, xo);
+        xv[1] = buf_load(xr, xo + 1024);
+        // group-output [G][N4]: lane = (group, quarter of the 32 rows);
+        // output-group [N][G]: lane = (row, half of the 16 groups)
+        const size_t off = op.os == 1 ? (size_t)(c * 16 + ((lane >> 2) & 15)) * op.gs + n0 + 8 * (lane & 3)
+                                      : (size_t)(n0 + ((lane >> 1) & 31)) * op.os + c * 16 + 8 * (lane & 1);
+        pls = buf_load(rsrc(op.scales, PLANE), (uint32_t)off * 2);
+        plb = buf_load(rsrc(op.corr, PLANE),
+                       op.corr_kind == STARK_QMM_CORRECTION_BIASES ? (uint32_t)off * 2 : OOB);
+    };
+    const auto code_rsrc = [&](const AffineOp& op, uint32_t n0) {
+        return rsrc(op.codes + (size_t)n0 * (op.k / 2), kTR * (op.k / 2));
+    };
+    // step v of a unit: k block v / 4 of subtile v % 4
+    const auto step_soff = [&](const AffineOp& op, int v) { return (uint32_t)(8 * (v % 4)) * (op.k / 2) + (v / 4) * 128; };
+
+    uint32_t i = lo, ri = 0, e = entry(lo);
+    const AffineOp* opp = &kb_->op[e >> 24];
+    __amdgpu_buffer_rsrc_t cr;
+    uint32_t vo;
+    {
+        const uint32_t n0 = tile_row(*opp, e);
+        issue_aux(*opp, n0, wave, true);
+        cr = code_rsrc(*opp, n0);
+        vo = r * (opp->k / 2) + wave * UB + piece;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) ring[s] = buf_load<kBufNt>(cr, vo, step_soff(*opp, s));
+    }
+    uint32_t tg0 = ~0u, tg1 = ~0u, tg2 = ~0u;  // (op << 16 | chunk) held by each activation region
+    const auto tag_of = [&](uint32_t rg) { return rg == 0 ? tg0 : rg == 1 ? tg1 : tg2; };
+    f32x4 acc[4] = {};
+    uint32_t par = 0;
+    for (;;) {
+        const AffineOp& op = *opp;
+        const uint32_t R = op.k / (4 * kUnitK);
+        const uint32_t t0 = (e & 0xffffffu) * kTR, n0 = min(t0, op.n - kTR);
+        const uint32_t c = wave + 4 * ri;
+        const uint32_t rg = ri % kXR;
+        const uint32_t tag = ((e >> 24) << 16) | c;
+        u32x4* xpw = lds.xp[wave][rg];
+        float* xsw = lds.xs[wave][rg];
+        if (tag_of(rg) != tag) {  // stage this unit's activations (loaded with the unit)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const u32x4 t = xv[m];
+                float f[8];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    f[2 * q] = __uint_as_float(t[q] << 16) * 0x1p64f;
+                    f[2 * q + 1] = __uint_as_float(t[q] & 0xffff0000u) * 0x1p60f;
+                }
+                u32x4 pq;  // (x0,x4)(x1,x5)(x2,x6)(x3,x7), as the codes unpack
+                pq[0] = perm(__float_as_uint(f[4]), __float_as_uint(f[0]), 0x07060302u);
+                pq[1] = perm(__float_as_uint(f[5]), __float_as_uint(f[1]), 0x07060302u);
+                pq[2] = perm(__float_as_uint(f[6]), __float_as_uint(f[2]), 0x07060302u);
+                pq[3] = perm(__float_as_uint(f[7]), __float_as_uint(f[3]), 0x07060302u);
+                xpw[lane + 64 * m] = pq;
+                float sm = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sm = dot2_bf16(t[q], 0x3F803F80u, sm);
+                sm += __shfl_xor(sm, 1, 64);
+                sm += __shfl_xor(sm, 2, 64);
+                sm += __shfl_xor(sm, 4, 64);
+                if ((lane & 7) == 0) xsw[8 * m + (lane >> 3)] = sm;
+            }
+            tg0 = rg == 0 ? tag : tg0;
+            tg1 = rg == 1 ? tag : tg1;
+            tg2 = rg == 2 ? tag : tg2;
+        }
+        {  // plane vectors -> f32 (scale * 2^69, bias term) pairs at [row][group]
+            const bool bf = op.w_dt == STARK_QMM_BF16, biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
+            float sv[8], bv[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t hs = (pls[q >> 1] >> (16 * (q & 1))) & 0xffffu;
+                const uint32_t hb = (plb[q >> 1] >> (16 * (q & 1))) & 0xffffu;
+                const float sc = plane_f32(hs, bf);
+                sv[q] = sc * 0x1p69f;
+                bv[q] = biased ? plane_f32(hb, bf) : -8.0f * sc;
+            }
+            float2* pw = (float2*)lds.pl[wave];
+            if (op.os == 1) {  // lane = (group, rows 8*quarter ..)
+                const uint32_t g = (lane >> 2) & 15, r0 = 8 * (lane & 3);
+                if (lane < 64) {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) pw[(r0 + q) * 16 + g] = float2{sv[q], bv[q]};
+                }
+            } else {  // lane = (row, groups 8*half ..)
+                const uint32_t row = (lane >> 1) & 31, g0 = 8 * (lane & 1);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) pw[row * 16 + g0 + q] = float2{sv[q], bv[q]};
+            }
+        }
+
+        // ---- next unit: issue its activation and plane loads now; its code
+        // loads refill the ring from step 8 on
+        uint32_t ni = i, nr = ri + 1;
+        if (nr == R) {
+            ni = i + 1;
+            nr = 0;
+        }
+        const bool more = ni < hi;
+        const uint32_t ne = more ? entry(ni) : e;
+        const uint32_t nc = more ? wave + 4 * nr : c;
+        const AffineOp& nop = kb_->op[ne >> 24];
+        const uint32_t nn0 = tile_row(nop, ne);
+        issue_aux(nop, nn0, nc, more && tag_of(nr % kXR) != (((ne >> 24) << 16) | nc));
+        const __amdgpu_buffer_rsrc_t ncr = code_rsrc(nop, nn0);
+        const uint32_t nvo = more ? r * (nop.k / 2) + nc * UB + piece : OOB;
+
+        // ---- the unit's 16 steps
+        f32x4 C0[4] = {}, C1[4] = {};
+        const u32x4* zero = lds.zero[wave];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int st = u % 4, ks = u / 4, sl = u % 8;
+            // unpack this step's codes, then refill the ring slot: the
+            // scheduling barrier keeps the refill after the last read of the
+            // slot, so the slot keeps its registers across units (a copy of a
+            // register with a load in flight would wait for every load)
+            u32x4 bq[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                uint32_t w = ring[sl][t];
+                if (SIGNED) w ^= 0x88888888u;
+                const uint32_t w8 = w >> 8;
+                bq[t][0] = w & 0x000F000Fu;   // (q0, q4)
+                bq[t][1] = w & 0x00F000F0u;   // (16 q1, 16 q5)
+                bq[t][2] = w8 & 0x000F000Fu;  // (q2, q6)
+                bq[t][3] = w8 & 0x00F000F0u;  // (16 q3, 16 q7)
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (u < 8)
+                ring[sl] = buf_load<kBufNt>(cr, vo, step_soff(op, u + 8));
+            else
+                ring[sl] = buf_load<kBufNt>(ncr, nvo, step_soff(nop, u - 8));
+            // A row c16 = (byte half hh, slot r): x of this lane's k block when
+            // the block's group (4ks + 2hh + kb/2 of the unit) sits in slot r
+            const u32x4* src = r == 2 * ks + (kb >> 1) ? xpw + 32 * ks + 16 * hh + 4 * kb : zero;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                f32x4& cc = (t & 1) ? C1[st] : C0[st];
+                cc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, src[t]),
+                                                             __builtin_bit_cast(bf16x8, bq[t]), cc, 0, 0, 0);
+            }
+        }
+        cr = ncr;
+        vo = nvo;
+
+        // ---- flush: C row 4kb+q of column (hh, r) is slot 4(kb&1)+q of byte
+        // half kb>>1, i.e. unit group gb + 4(q>>1) + (q&1) of row r, with
+        // gb = 8(kb&1) + 2hh (meaningful where kb>>1 == hh; the other lanes'
+        // sums are dropped at the tile end)
+        {
+            const uint32_t gb = 8 * (kb & 1) + 2 * hh;
+            const float2 xa = *(const float2*)&xsw[gb];
+            const float2 xb = *(const float2*)&xsw[gb + 4];
+            const float xq[4] = {xa.x, xa.y, xb.x, xb.y};
+            const f32x4* pw = lds.pl[wave];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const f32x4 cs = C0[st] + C1[st];
+                const uint32_t row = 8 * st + r;
+                const f32x4 pa = pw[(row * 16 + gb) / 2], pb = pw[(row * 16 + gb + 4) / 2];  // (s, b) of 2 groups each
+                const float sq[4] = {pa[0], pa[2], pb[0], pb[2]}, bq[4] = {pa[1], pa[3], pb[1], pb[3]};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[st][q] = fmaf(sq[q], cs[q], fmaf(bq[q], xq[q], acc[st][q]));
+            }
+        }
+
+        // ---- tile end: the row sums of the four waves meet in LDS, then the D-ops
+        if (ri + 1 == R) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                float v = (acc[st][0] + acc[st][1]) + (acc[st][2] + acc[st][3]);
+                v = (kb >> 1) == hh ? v : 0.0f;  // lanes whose C rows pair the other byte half hold no row
+                v += __shfl_xor(v, 8, 64);
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                if (lane < 8) lds.red[par][wave][8 * st + lane] = v;
+                acc[st] = f32x4{0, 0, 0, 0};
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (tid < (uint32_t)kTR) {
+                const uint32_t n = n0 + tid;
+                if (n >= t0) {  // rows of the previous tile (shifted last tile) are not written again
+                    float o = op.ab_scale * ((lds.red[par][0][tid] + lds.red[par][1][tid]) +
+                                             (lds.red[par][2][tid] + lds.red[par][3][tid]));
+                    if (op.flags & FLAG_ACCUMULATE) o += load_as_f32(op.d, op.d_dt, n);
+                    if (op.bias) o += load_as_f32(op.bias, op.w_dt, n);
+                    if (op.flags & FLAG_SOFT_CAP) o = op.soft_cap * tanhf(o / op.soft_cap);
+                    store_from_f32(op.d, op.d_dt, n, o);
+                }
+            }
+            par ^= 1;
+        }
+        if (!more) break;
+        i = ni;
+        ri = nr;
+        e = ne;
+        opp = &nop;
+    }
+}
+
+// Whether a batch of 4-bit ops takes the streaming kernel (one activation
+// row, group size 64, K a multiple of 4096, at least one 32-row tile).
+bool stream_eligible(const AffineOp* ops, uint32_t count) {
+    for (uint32_t i = 0; i < count; ++i)
+        if (ops[i].m != 1 || ops[i].group_size != 64 || ops[i].k % (4 * kUnitK) || ops[i].n < (uint32_t)kTR)
+            return false;
+    return count > 0;
+}
+
+template <bool SIGNED>
+stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t stream) {
+    std::vector<AffineOp> sorted(ops, ops + count);
+    std::stable_sort(sorted.begin(), sorted.end(), [](const AffineOp& a, const AffineOp& b) { return a.k > b.k; });
+    AffineBatch batch{};
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        batch.op[i] = sorted[i];
+        tiles += (sorted[i].n + kTR - 1) / kTR;
+    }
+    batch.count = count;
+    batch.total = tiles;
+    if (tiles == 0) return STARK_QMM_OK;
+    auto kern = qmv_stream<SIGNED>;
+    int dev = 0, cus = 0;
+    QMM_HIP_CHECK(hipGetDevice(&dev));
+    QMM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    // two workgroups (eight waves) per CU, a multiple of the 8 XCDs
+    const uint32_t grid = std::min(std::min(persistent_grid(kern), (uint32_t)std::max(8, cus * 2 / 8 * 8)),
+                                   (tiles + 7) / 8 * 8);
+    Schedule sched;
+    if (grid == 0 || !schedule_for(sorted.data(), count, grid, &sched, kTR)) return STARK_QMM_DEVICE_FAILURE;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kWg), 0, stream, batch, sched);
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
 }
 
 template <int MP, int MB, int GS, int BITS, bool SIGNED>
@@ -208,6 +545,8 @@ stark_qmm_status launch_gs(const AffineOp* o, uint32_t n, hipStream_t st) {
                                               : launch_one<MP, MB, 32, BITS, false>(o, n, st);
         return STARK_QMM_UNSUPPORTED_GROUP_SIZE;
     case 64:
+        if constexpr (MP == 1 && MB == 1 && BITS == 4)
+            if (stream_eligible(o, n)) return sg ? launch_stream<true>(o, n, st) : launch_stream<false>(o, n, st);
         return sg ? launch_one<MP, MB, 64, BITS, true>(o, n, st) : launch_one<MP, MB, 64, BITS, false>(o, n, st);
     default:
         return sg ? launch_one<MP, MB, 128, BITS, true>(o, n, st) : launch_one<MP, MB, 128, BITS, false>(o, n, st);

@@ -265,6 +265,66 @@ def test_streaming_kernel_d_ops_on_shifted_tile(qmm, oracle):
     run_case(qmm, oracle, m=2, n=40, k=2048, accumulate=True, soft_cap=2.0, d_dt=H.BF16, seed=9)
 
 
+@pytest.mark.parametrize("n,k", [(16, 4096), (40, 4096), (72, 8192), (1000, 12288), (3072, 4096), (24, 16384)])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_decode_stream_kernel_shapes(qmm, oracle, n, k, bits, layout):
+    """Shapes of the one-row streaming kernel (M = 1, group 64, K % 4096 == 0):
+    one to four 1024-k units per wave and tile (K = 16384 cycles the three
+    activation regions), a shifted last tile (N % 16 != 0), both plane
+    layouts, 4- and 8-bit codes."""
+    run_case(qmm, oracle, m=1, n=n, k=k, bits=bits, layout=layout, seed=n + k + bits + 3 * layout)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("correction,signed", [(0, False), (1, True), (0, True)])
+def test_decode_stream_kernel_corrections(qmm, oracle, bits, correction, signed):
+    run_case(qmm, oracle, m=1, n=72, k=4096, bits=bits, correction=correction, signed=signed, quantizer=False,
+             seed=15)
+    run_case(qmm, oracle, m=1, n=72, k=8192, bits=bits, correction=correction, signed=signed, quantizer=False,
+             w_dt=H.F16, layout=1, seed=16)
+
+
+def test_decode_stream_kernel_d_ops_on_shifted_tile(qmm, oracle):
+    """N=40: the last 16-row tile overlaps the previous one; accumulate must add once."""
+    run_case(qmm, oracle, m=1, n=40, k=4096, ab_scale=0.5, accumulate=True, with_bias=True, d_dt=H.F32, seed=18)
+    run_case(qmm, oracle, m=1, n=40, k=8192, bits=8, accumulate=True, soft_cap=2.0, d_dt=H.BF16, seed=19)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_decode_stream_kernel_layer_set_against_oracle(qmm, oracle, bits):
+    """One launch over a reduced layer set (q, k, v, o, gate, up, down): ops of
+    one K with distinct activations and ops sharing one activation vector;
+    every output against the oracle (the per-wave activation regions are tagged
+    by op and chunk)."""
+    rng = np.random.default_rng(21 + bits)
+    shapes = [(256, 4096), (64, 4096), (64, 4096), (256, 4096), (512, 4096), (512, 4096), (256, 12288)]
+    xs = {4096: H.activations(oracle, rng, 1, 4096), 12288: H.activations(oracle, rng, 1, 12288)}
+    kern = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    args, wants = [], []
+    for i, (n, k) in enumerate(shapes):
+        W = H.affine_weights(oracle, rng, n, k, bits, 64, layout=i % 2)
+        x = xs[k] if i in (1, 2) else H.activations(oracle, rng, 1, k)  # k_proj and v_proj share x
+        st, want = oracle.matmul(a=x, m=1, n=n, k=k, codes=W["codes"], scales=W["scales"], correction=1,
+                                 correction_data=W["corr"], layout=i % 2, row_count=n, group_count=k // 64,
+                                 bits=bits, group_size=64, output_dt=H.BF16, threads=8)
+        assert st == 0
+        mode = qmm.MODE_U4 if bits == 4 else qmm.MODE_U8
+        args.append(qmm.MatmulArguments(
+            a=H.to_dev(x), m=1, n=n, k=k, d=torch_empty(n, H.BF16),
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(i % 2, n, k // 64), mode=mode,
+                             correction_data=H.to_dev(W["corr"]))))
+        mag = H.dequant_magnitude(oracle, W["codes"], W["scales"], W["corr"], n, k, bits, 64, i % 2, 1, H.BF16, x,
+                                  H.BF16, 1, out_n=n)
+        wants.append((want, mag))
+    kern.encode_many(args)
+    torch.cuda.synchronize()
+    for i, (a, (want, mag)) in enumerate(zip(args, wants)):
+        got = H.load(oracle, H.from_dev(a.d, np.uint16), H.BF16)
+        check(got, H.load(oracle, want, H.BF16), mag=mag, label=f"op {i} bits {bits}")
+
+
 @pytest.mark.parametrize("n,k,gs", [(80, 4160, 32), (64, 8192 + 512, 64), (1040, 12288, 128), (3072, 1024, 64),
                                     (96, 96, 32)])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16])
