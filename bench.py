@@ -278,7 +278,7 @@ def config1(args, torch, Q):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": "qmv_mfma<1, 1, 64, 4, false> (one persistent launch per step)",
+            "kernel": "qmv_stream<false> (one persistent launch per step)",
         },
         "cpu_baseline": cpu,
     }

@@ -17,7 +17,8 @@
 namespace {
 
 constexpr int kHd = 128;      // head dim
-constexpr int kChunk = 128;   // attention positions per partial workgroup
+constexpr int kChunk = 64;    // attention positions per partial workgroup
+constexpr int kMaxChunks = 1024;  // chunks the reduction takes (capacity <= 65536)
 
 __device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -40,20 +41,50 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // out = x * rsqrt(mean(x^2) + eps) * w, one row of n (n % 256 == 0), 256 threads.
+// Every load of a thread is a 16-byte vector issued before the first use (the
+// row is read once; rows up to 8192 stay in registers for the second pass).
 __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out,
                                                        uint32_t n, float eps) {
+    constexpr int kKeep = 4;  // vectors of 8 values kept per thread
     __shared__ float part[4];
-    const uint32_t t = threadIdx.x;
+    const uint32_t t = threadIdx.x, nv = n / 8;
+    const uint4* xv = (const uint4*)x;
+    uint4 keep[kKeep];
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) keep[j] = t + j * 256 < nv ? xv[t + j * 256] : uint4{0, 0, 0, 0};
     float ss = 0.0f;
-    for (uint32_t i = t; i < n; i += 256) {
-        const float v = bf(x[i]);
-        ss += v * v;
-    }
+    const auto sq = [&](const uint4& u) {
+        const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float a = __uint_as_float(wd[e] << 16), b = __uint_as_float(wd[e] & 0xffff0000u);
+            ss = fmaf(a, a, fmaf(b, b, ss));
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) sq(keep[j]);
+    for (uint32_t i = t + kKeep * 256; i < nv; i += 256) sq(xv[i]);
     ss = wave_sum(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
     __syncthreads();
     const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)n + eps);
-    for (uint32_t i = t; i < n; i += 256) out[i] = to_bf(bf(to_bf(bf(x[i]) * inv)) * bf(w[i]));
+    const auto emit = [&](uint32_t i, const uint4& u) {
+        const uint4 wv = ((const uint4*)w)[i];
+        const uint32_t xd[4] = {u.x, u.y, u.z, u.w}, wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        uint32_t od[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float a = __uint_as_float(xd[e] << 16), b = __uint_as_float(xd[e] & 0xffff0000u);
+            const uint16_t lo = to_bf(bf(to_bf(a * inv)) * __uint_as_float(wd[e] << 16));
+            const uint16_t hi = to_bf(bf(to_bf(b * inv)) * __uint_as_float(wd[e] & 0xffff0000u));
+            od[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        ((uint4*)out)[i] = uint4{od[0], od[1], od[2], od[3]};
+    };
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j)
+        if (t + j * 256 < nv) emit(t + j * 256, keep[j]);
+    for (uint32_t i = t + kKeep * 256; i < nv; i += 256) emit(i, xv[i]);
 }
 
 // Per-head RMSNorm of q and k, rotate-half RoPE at *pos, and the k/v write
@@ -91,121 +122,129 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(uint16_t* q, const uin
 }
 
 // Flash-decoding partials: workgroup (kv head g, chunk c) scores its GQA
-// group's query heads against positions [c*kChunk, min(len, (c+1)*kChunk)),
+// group's G query heads against positions [c*kChunk, min(len, (c+1)*kChunk)),
 // len = *pos + 1, and writes the unnormalised partial output with its max and
-// sum. 256 threads; group size G = qh / kvh <= 8.
+// sum. 64*G threads: wave h is query head h of the group. The K and V tiles of
+// the chunk (kChunk x 128 bf16 each) are read with 16-byte loads issued
+// together into LDS (K rows padded so that the row-per-lane score reads spread
+// over the banks); scores, softmax and PV then run from LDS.
 template <int G>
-__global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* q, const uint16_t* kcache,
-                                                           const uint16_t* vcache, float* po, float* pml,
-                                                           const int32_t* pos_ptr, uint32_t kvh, uint32_t cap,
-                                                           uint32_t nchunks, float scale) {
+__global__ __launch_bounds__(64 * G) void attn_partial_kernel(const uint16_t* q, const uint16_t* kcache,
+                                                              const uint16_t* vcache, float* po, float* pml,
+                                                              const int32_t* pos_ptr, uint32_t kvh, uint32_t cap,
+                                                              uint32_t nchunks, float scale) {
+    constexpr int kRowK = kHd / 2 + 4;  // padded K row, in u32 (bf16 pairs)
+    constexpr int kVec = kChunk * kHd / 8;  // 16-byte vectors per tile
+    __shared__ uint32_t ks[kChunk * kRowK];
+    __shared__ uint32_t vs[kChunk * kHd / 2];
     __shared__ float qs[G][kHd];
-    __shared__ float w[G][kChunk];
-    __shared__ float red[G][4];
-    const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+    __shared__ float ws[G][kChunk];
+    const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63, h = t >> 6;
     const uint32_t len = min((uint32_t)*pos_ptr + 1, cap);
     const uint32_t p0 = c * kChunk;
-    float* out_o = po + ((size_t)(g * G) * nchunks + c) * kHd;
     if (p0 >= len) return;  // chunk past the context: the reduction skips it
     const uint32_t np = min((uint32_t)kChunk, len - p0);
-    for (uint32_t e = t; e < G * kHd; e += 256) qs[e / kHd][e % kHd] = bf(q[(size_t)(g * G) * kHd + e]);
-    __syncthreads();
-    // scores: thread t -> position t / 2, half t % 2 (64 dims)
     {
-        const uint32_t p = t >> 1, half = t & 1;
-        float s[G];
+        constexpr int kPer = (kVec + 64 * G - 1) / (64 * G);
+        const uint4* kg = (const uint4*)(kcache + ((size_t)g * cap + p0) * kHd);
+        const uint4* vg = (const uint4*)(vcache + ((size_t)g * cap + p0) * kHd);
+        uint4 kv[kPer], vv[kPer];
 #pragma unroll
-        for (int h = 0; h < G; ++h) s[h] = 0.0f;
-        if (p < np) {
-            const uint4* kr = (const uint4*)(kcache + ((size_t)g * cap + p0 + p) * kHd + half * 64);
+        for (int j = 0; j < kPer; ++j) {
+            const uint32_t v = t + j * 64 * G;
+            const bool ok = v < (uint32_t)kVec && v / (kHd / 8) < np;  // rows past the context read nothing
+            kv[j] = ok ? kg[v] : uint4{0, 0, 0, 0};
+            vv[j] = ok ? vg[v] : uint4{0, 0, 0, 0};
+        }
+        const uint32_t qd = lane * 2;
+        const uint32_t qw = *(const uint32_t*)(q + ((size_t)(g * G + h)) * kHd + qd);
+        qs[h][qd] = __uint_as_float(qw << 16);
+        qs[h][qd + 1] = __uint_as_float(qw & 0xffff0000u);
 #pragma unroll
-            for (int v8 = 0; v8 < 8; ++v8) {
-                const uint4 u = kr[v8];
-                const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float k0 = __uint_as_float(wd[e] << 16), k1 = __uint_as_float(wd[e] & 0xffff0000u);
-                    const uint32_t d = half * 64 + v8 * 8 + 2 * e;
-#pragma unroll
-                    for (int h = 0; h < G; ++h) s[h] = fmaf(qs[h][d], k0, fmaf(qs[h][d + 1], k1, s[h]));
-                }
+        for (int j = 0; j < kPer; ++j) {
+            const uint32_t v = t + j * 64 * G;
+            if (v < (uint32_t)kVec) {
+                const uint32_t row = v / (kHd / 8), col = (v % (kHd / 8)) * 4;
+                *(uint4*)&ks[row * kRowK + col] = kv[j];
+                *(uint4*)&vs[row * (kHd / 2) + col] = vv[j];
             }
         }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            s[h] += __shfl_xor(s[h], 1, 64);
-            if (half == 0 && p < kChunk) w[h][p] = p < np ? s[h] * scale : -INFINITY;
-        }
     }
     __syncthreads();
-    // per head: max and exp-sum over the chunk (threads 0..127 hold w[h][t])
-    float m[G], l[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float v = t < kChunk ? w[h][t] : -INFINITY;
-        v = wave_max(v);
-        if ((t & 63) == 0) red[h][t >> 6] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < G; ++h) m[h] = fmaxf(red[h][0], red[h][1]);
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float e = 0.0f;
-        if (t < kChunk) {
-            e = t < np ? __expf(w[h][t] - m[h]) : 0.0f;
-            w[h][t] = e;
+    // scores: lane = position, wave = head
+    float s = -INFINITY;
+    if (lane < np) {
+        const uint32_t* kr = &ks[lane * kRowK];
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int d2 = 0; d2 < kHd / 2; d2 += 2) {
+            const uint2 u = *(const uint2*)&kr[d2];
+            acc = fmaf(qs[h][2 * d2], __uint_as_float(u.x << 16), acc);
+            acc = fmaf(qs[h][2 * d2 + 1], __uint_as_float(u.x & 0xffff0000u), acc);
+            acc = fmaf(qs[h][2 * d2 + 2], __uint_as_float(u.y << 16), acc);
+            acc = fmaf(qs[h][2 * d2 + 3], __uint_as_float(u.y & 0xffff0000u), acc);
         }
-        e = wave_sum(e);
-        if ((t & 63) == 0) red[h][t >> 6] = e;
+        s = acc * scale;
     }
+    const float m = wave_max(s);
+    const float e = lane < np ? __expf(s - m) : 0.0f;
+    const float l = wave_sum(e);
+    ws[h][lane] = e;
     __syncthreads();
-#pragma unroll
-    for (int h = 0; h < G; ++h) l[h] = red[h][0] + red[h][1];
-    // PV: thread t -> dim t % 128, heads of parity t / 128
-    {
-        const uint32_t d = t % kHd, hp = t / kHd;
-        float o[G / 2 > 0 ? G / 2 : 1];
-#pragma unroll
-        for (int q2 = 0; q2 < (G > 1 ? G / 2 : 1); ++q2) o[q2] = 0.0f;
-        const uint16_t* vr = vcache + ((size_t)g * cap + p0) * kHd + d;
-        for (uint32_t p = 0; p < np; ++p) {
-            const float vv = bf(vr[(size_t)p * kHd]);
-#pragma unroll
-            for (int q2 = 0; q2 < (G > 1 ? G / 2 : 1); ++q2) {
-                const int h = G > 1 ? 2 * q2 + hp : 0;
-                o[q2] = fmaf(w[h][p], vv, o[q2]);
-            }
-        }
-#pragma unroll
-        for (int q2 = 0; q2 < (G > 1 ? G / 2 : 1); ++q2) {
-            const int h = G > 1 ? 2 * q2 + hp : 0;
-            if (G == 1 && hp) continue;
-            po[((size_t)(g * G + h) * nchunks + c) * kHd + d] = o[q2];
-        }
+    // PV: lane = dims 2*lane, 2*lane + 1
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 8
+    for (uint32_t p = 0; p < np; ++p) {
+        const uint32_t u = vs[p * (kHd / 2) + lane];
+        const float wp = ws[h][p];
+        o0 = fmaf(wp, __uint_as_float(u << 16), o0);
+        o1 = fmaf(wp, __uint_as_float(u & 0xffff0000u), o1);
     }
-    if (t < G) {
-        pml[((size_t)(g * G + t) * nchunks + c) * 2 + 0] = m[t];
-        pml[((size_t)(g * G + t) * nchunks + c) * 2 + 1] = l[t];
-    }
-    (void)out_o;
+    const size_t row = (size_t)(g * G + h) * nchunks + c;
+    *(float2*)&po[row * kHd + 2 * lane] = float2{o0, o1};
+    if (lane == 0) *(float2*)&pml[row * 2] = float2{m, l};
 }
 
 // Combine the chunks of each query head: out = sum_c o_c e^(m_c - m) / sum_c l_c e^(m_c - m).
+// The chunk maxima and sums are read in parallel first; the weighted sum of
+// the partial outputs then issues its loads eight chunks at a time.
 __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const float* pml, uint16_t* out,
                                                           const int32_t* pos_ptr, uint32_t nchunks, uint32_t cap) {
+    __shared__ float fs[kMaxChunks];
+    __shared__ float red[2];
     const uint32_t h = blockIdx.x, d = threadIdx.x;
     const uint32_t len = min((uint32_t)*pos_ptr + 1, cap);
     const uint32_t nc = min(nchunks, (len + kChunk - 1) / kChunk);
-    float m = -INFINITY;
-    for (uint32_t c = 0; c < nc; ++c) m = fmaxf(m, pml[((size_t)h * nchunks + c) * 2]);
-    float l = 0.0f, o = 0.0f;
-    for (uint32_t c = 0; c < nc; ++c) {
-        const float f = __expf(pml[((size_t)h * nchunks + c) * 2] - m);
-        l = fmaf(pml[((size_t)h * nchunks + c) * 2 + 1], f, l);
-        o = fmaf(po[((size_t)h * nchunks + c) * kHd + d], f, o);
+    const float2* ml = (const float2*)pml + (size_t)h * nchunks;
+    float mx = -INFINITY;
+    for (uint32_t c = d; c < nc; c += 128) mx = fmaxf(mx, ml[c].x);
+    mx = wave_max(mx);
+    if ((d & 63) == 0) red[d >> 6] = mx;
+    __syncthreads();
+    const float m = fmaxf(red[0], red[1]);
+    __syncthreads();
+    float l = 0.0f;
+    for (uint32_t c = d; c < nc; c += 128) {
+        const float2 v = ml[c];
+        const float f = __expf(v.x - m);
+        fs[c] = f;
+        l = fmaf(v.y, f, l);
     }
+    l = wave_sum(l);
+    if ((d & 63) == 0) red[d >> 6] = l;
+    __syncthreads();
+    l = red[0] + red[1];
+    const float* col = po + (size_t)h * nchunks * kHd + d;
+    float o = 0.0f;
+    uint32_t c = 0;
+    for (; c + 8 <= nc; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = col[(size_t)(c + j) * kHd];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o = fmaf(v[j], fs[c + j], o);
+    }
+    for (; c < nc; ++c) o = fmaf(col[(size_t)c * kHd], fs[c], o);
     out[(size_t)h * kHd + d] = to_bf(o / l);
 }
 
@@ -301,9 +340,10 @@ int stark_decode_attention(const void* q, const void* kcache, const void* vcache
     const uint32_t nchunks = (cap + kChunk - 1) / kChunk, G = qh / kvh;
     const float scale = 1.0f / sqrtf((float)kHd);
     hipStream_t s = (hipStream_t)stream;
+    if (nchunks > (uint32_t)kMaxChunks) return 1;
     const dim3 grid(kvh, nchunks);
 #define QMM_ATTN(GG)                                                                                              \
-    hipLaunchKernelGGL(attn_partial_kernel<GG>, grid, dim3(256), 0, s, (const uint16_t*)q, (const uint16_t*)kcache, \
+    hipLaunchKernelGGL(attn_partial_kernel<GG>, grid, dim3(64 * GG), 0, s, (const uint16_t*)q, (const uint16_t*)kcache, \
                        (const uint16_t*)vcache, po, pml, pos, kvh, cap, nchunks, scale)
     switch (G) {
     case 1: QMM_ATTN(1); break;
