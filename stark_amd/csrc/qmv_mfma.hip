@@ -213,7 +213,7 @@ bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* 
 constexpr int kXR = 3;         // activation regions per wave
 constexpr int kTR = 32;        // tile rows
 constexpr int kUnitK = 1024;   // k values per unit (16 groups of 64)
-constexpr int kListLds = 256;  // schedule entries staged in LDS at kernel start
+constexpr int kListLds = kWg;  // schedule entries staged in LDS at kernel start (one per thread)
 
 struct StreamLds {
     u32x4 xp[4][kXR][kUnitK / 8];  // activation pairs (x0,x4)(x1,x5).. per 8 values; x*2^64, odd values x*2^60
@@ -231,6 +231,12 @@ __device__ __forceinline__ u32x4 buf_load(__amdgpu_buffer_rsrc_t r, uint32_t vof
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 template <bool SIGNED>
@@ -251,9 +257,9 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const uint32_t piece = 16 * (4 * hh + kb);  // this lane's 16 bytes of a row's 128-byte block
     if (lane < 4) lds.zero[wave][lane] = u32x4{0, 0, 0, 0};
     // The workgroup's schedule entries go to LDS once, so that no unit waits on
-    // a scalar miss for its successor.
-    for (uint32_t t = tid; t < min(hi - lo, (uint32_t)kListLds); t += kWg) lds.list[t] = sched.tiles[lo + t];
-    __syncthreads();
+    // a scalar miss for its successor. Their load is issued first and written
+    // to LDS after the first unit's loads are on their way (kListLds == kWg).
+    const uint32_t list_v = tid < min(hi - lo, (uint32_t)kListLds) ? sched.tiles[lo + tid] : 0u;
     const auto entry = [&](uint32_t t) {
         return t - lo < (uint32_t)kListLds ? __builtin_amdgcn_readfirstlane(lds.list[t - lo])
                                            : ((cu32*)sched.tiles)[t];
@@ -284,7 +290,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     // step v of a unit: k block v / 4 of subtile v % 4
     const auto step_soff = [&](const AffineOp& op, int v) { return (uint32_t)(8 * (v % 4)) * (op.k / 2) + (v / 4) * 128; };
 
-    uint32_t i = lo, ri = 0, e = entry(lo);
+    uint32_t i = lo, ri = 0, e = ((cu32*)sched.tiles)[lo];
     const AffineOp* opp = &kb_->op[e >> 24];
     __amdgpu_buffer_rsrc_t cr;
     uint32_t vo;
@@ -296,6 +302,8 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
 #pragma unroll
         for (int s = 0; s < 8; ++s) ring[s] = buf_load<kBufNt>(cr, vo, step_soff(*opp, s));
     }
+    lds.list[tid] = list_v;
+    lds_barrier();
     uint32_t tg0 = ~0u, tg1 = ~0u, tg2 = ~0u;  // (op << 16 | chunk) held by each activation region
     const auto tag_of = [&](uint32_t rg) { return rg == 0 ? tg0 : rg == 1 ? tg1 : tg2; };
     f32x4 acc[4] = {};
@@ -450,9 +458,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 if (lane < 8) lds.red[par][wave][8 * st + lane] = v;
                 acc[st] = f32x4{0, 0, 0, 0};
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            lds_barrier();
             if (tid < (uint32_t)kTR) {
                 const uint32_t n = n0 + tid;
                 if (n >= t0) {  // rows of the previous tile (shifted last tile) are not written again
