@@ -240,7 +240,7 @@ def config1(args, torch, Q):
     value = bytes_step / (ms_step * 1e-3) / 1e9
     achieved = bytes_step / (mean_launch_ms * 1e-3) / 1e9
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "qmv_mfma_w4_layerset_pmc.md")
+    tfile = os.path.join(ROOT, "profiles", "qmv_stream_w4_layerset_pmc.md")
     if os.path.exists(tfile):
         import re
         hit = re.search(r"hbm_bytes_per_launch\s*=\s*(\d+)", open(tfile).read())
