@@ -248,6 +248,132 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
     out[(size_t)h * kHd + d] = to_bf(o / l);
 }
 
+// Per-head RMSNorm + rotate-half RoPE of one head (128 values, lane owns dims
+// i and i + 64), the arithmetic of qk_norm_rope_kernel: returns the rotated
+// pair rounded to bf16.
+__device__ __forceinline__ void norm_rope_pair(float a, float b, const uint16_t* w, uint32_t i, int32_t pos,
+                                               float theta, float eps, uint16_t& ra, uint16_t& rb) {
+    const float inv = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)kHd + eps);
+    const float na = bf(to_bf(bf(to_bf(a * inv)) * bf(w[i])));
+    const float nb = bf(to_bf(bf(to_bf(b * inv)) * bf(w[i + 64])));
+    const float freq = powf(theta, -2.0f * (float)i / (float)kHd);
+    float sn, cs;
+    sincosf((float)pos * freq, &sn, &cs);
+    ra = to_bf(na * cs - nb * sn);
+    rb = to_bf(nb * cs + na * sn);
+}
+
+// Attention of one decode step with the q/k norm + RoPE + KV write and the
+// chunk reduction folded in: workgroup (kv head g, chunk c), 64*G threads,
+// wave h = query head h of the group.
+//  - every workgroup normalises and rotates its G query heads itself;
+//  - the workgroup whose chunk holds the new position builds that K row
+//    (norm + RoPE) and V row, uses them in place of the cache rows and writes
+//    them to the cache (later steps read them from there);
+//  - partial output, max and sum per chunk as attn_partial_kernel
+//    (attn_reduce_kernel combines the chunks; an in-kernel last-workgroup
+//    reduction needs a device-scope fence per workgroup, which writes back
+//    the XCD's L2 and costs more than the second launch).
+template <int G>
+__global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, const uint16_t* knew,
+                                                            const uint16_t* vnew, const uint16_t* qw,
+                                                            const uint16_t* kw, uint16_t* kcache, uint16_t* vcache,
+                                                            float* po, float* pml, const int32_t* pos_ptr, uint32_t kvh, uint32_t cap,
+                                                            uint32_t nchunks, float scale, float theta, float eps) {
+    constexpr int kRowK = kHd / 2 + 4;
+    constexpr int kVec = kChunk * kHd / 8;
+    __shared__ uint32_t ks[kChunk * kRowK];
+    __shared__ uint32_t vs[kChunk * kHd / 2];
+    __shared__ float qs[G][kHd];
+    __shared__ float ws[G][kChunk];
+    const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63, h = t >> 6;
+    const int32_t pos = *pos_ptr;
+    const uint32_t len = min((uint32_t)pos + 1, cap);
+    const uint32_t p0 = c * kChunk;
+    if (p0 >= len) return;  // chunk past the context
+    const uint32_t np = min((uint32_t)kChunk, len - p0);
+    const bool own_row = (uint32_t)pos < cap && (uint32_t)pos >= p0 && (uint32_t)pos < p0 + kChunk;
+    {
+        constexpr int kPer = (kVec + 64 * G - 1) / (64 * G);
+        const uint4* kg = (const uint4*)(kcache + ((size_t)g * cap + p0) * kHd);
+        const uint4* vg = (const uint4*)(vcache + ((size_t)g * cap + p0) * kHd);
+        uint4 kv[kPer], vv[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const uint32_t v = t + j * 64 * G, row = v / (kHd / 8);
+            const bool ok = v < (uint32_t)kVec && row < np && !(own_row && p0 + row == (uint32_t)pos);
+            kv[j] = ok ? kg[v] : uint4{0, 0, 0, 0};
+            vv[j] = ok ? vg[v] : uint4{0, 0, 0, 0};
+        }
+        // query head g*G + h: norm + RoPE
+        {
+            const uint16_t* src = q + (size_t)(g * G + h) * kHd;
+            uint16_t ra, rb;
+            norm_rope_pair(bf(src[lane]), bf(src[lane + 64]), qw, lane, pos, theta, eps, ra, rb);
+            qs[h][lane] = bf(ra);
+            qs[h][lane + 64] = bf(rb);
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const uint32_t v = t + j * 64 * G;
+            if (v < (uint32_t)kVec) {
+                const uint32_t row = v / (kHd / 8), col = (v % (kHd / 8)) * 4;
+                *(uint4*)&ks[row * kRowK + col] = kv[j];
+                *(uint4*)&vs[row * (kHd / 2) + col] = vv[j];
+            }
+        }
+        if (own_row && h == 0) {  // the new position's K (norm + RoPE) and V rows
+            const uint32_t r = (uint32_t)pos - p0;
+            uint16_t ra, rb;
+            const uint16_t* ksrc = knew + (size_t)g * kHd;
+            norm_rope_pair(bf(ksrc[lane]), bf(ksrc[lane + 64]), kw, lane, pos, theta, eps, ra, rb);
+            const uint16_t va = vnew[(size_t)g * kHd + lane], vb = vnew[(size_t)g * kHd + lane + 64];
+            uint16_t* ks16 = (uint16_t*)&ks[r * kRowK];
+            uint16_t* vs16 = (uint16_t*)&vs[r * (kHd / 2)];
+            ks16[lane] = ra;
+            ks16[lane + 64] = rb;
+            vs16[lane] = va;
+            vs16[lane + 64] = vb;
+            const size_t crow = ((size_t)g * cap + (uint32_t)pos) * kHd;
+            kcache[crow + lane] = ra;
+            kcache[crow + lane + 64] = rb;
+            vcache[crow + lane] = va;
+            vcache[crow + lane + 64] = vb;
+        }
+    }
+    __syncthreads();
+    float s = -INFINITY;
+    if (lane < np) {
+        const uint32_t* kr = &ks[lane * kRowK];
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int d2 = 0; d2 < kHd / 2; d2 += 2) {
+            const uint2 u = *(const uint2*)&kr[d2];
+            acc = fmaf(qs[h][2 * d2], __uint_as_float(u.x << 16), acc);
+            acc = fmaf(qs[h][2 * d2 + 1], __uint_as_float(u.x & 0xffff0000u), acc);
+            acc = fmaf(qs[h][2 * d2 + 2], __uint_as_float(u.y << 16), acc);
+            acc = fmaf(qs[h][2 * d2 + 3], __uint_as_float(u.y & 0xffff0000u), acc);
+        }
+        s = acc * scale;
+    }
+    const float m = wave_max(s);
+    const float e = lane < np ? __expf(s - m) : 0.0f;
+    const float l = wave_sum(e);
+    ws[h][lane] = e;
+    __syncthreads();
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 8
+    for (uint32_t p = 0; p < np; ++p) {
+        const uint32_t u = vs[p * (kHd / 2) + lane];
+        const float wp = ws[h][p];
+        o0 = fmaf(wp, __uint_as_float(u << 16), o0);
+        o1 = fmaf(wp, __uint_as_float(u & 0xffff0000u), o1);
+    }
+    const size_t prow = (size_t)(g * G + h) * nchunks + c;
+    *(float2*)&po[prow * kHd + 2 * lane] = float2{o0, o1};
+    if (lane == 0) *(float2*)&pml[prow * 2] = float2{m, l};
+}
+
 // a = silu(g) * u in bf16 steps (gated_act_mul semantics).
 __global__ void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* out, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -353,6 +479,31 @@ int stark_decode_attention(const void* q, const void* kcache, const void* vcache
     default: return 1;
     }
 #undef QMM_ATTN
+    hipLaunchKernelGGL(attn_reduce_kernel, dim3(qh), dim3(kHd), 0, s, po, pml, (uint16_t*)out, pos, nchunks, cap);
+    return hipGetLastError() == hipSuccess ? 0 : 10;
+}
+
+int stark_decode_attention_fused(const void* q, const void* k, const void* v, const void* qw, const void* kw,
+                                 void* kcache, void* vcache, float* po, float* pml, void* out, const int32_t* pos,
+                                 uint32_t qh, uint32_t kvh, uint32_t cap, float theta, float eps, void* stream) {
+    if (kvh == 0 || qh % kvh || cap == 0) return 1;
+    if ((cap + kChunk - 1) / kChunk > (uint32_t)kMaxChunks) return 1;
+    const uint32_t nchunks = (cap + kChunk - 1) / kChunk, G = qh / kvh;
+    const float scale = 1.0f / sqrtf((float)kHd);
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(kvh, nchunks);
+#define QMM_ATTN_F(GG)                                                                                          \
+    hipLaunchKernelGGL(attn_fused_kernel<GG>, grid, dim3(64 * GG), 0, s, (const uint16_t*)q, (const uint16_t*)k, \
+                       (const uint16_t*)v, (const uint16_t*)qw, (const uint16_t*)kw, (uint16_t*)kcache,          \
+                       (uint16_t*)vcache, po, pml, pos, kvh, cap, nchunks, scale, theta, eps)
+    switch (G) {
+    case 1: QMM_ATTN_F(1); break;
+    case 2: QMM_ATTN_F(2); break;
+    case 4: QMM_ATTN_F(4); break;
+    case 8: QMM_ATTN_F(8); break;
+    default: return 1;
+    }
+#undef QMM_ATTN_F
     hipLaunchKernelGGL(attn_reduce_kernel, dim3(qh), dim3(kHd), 0, s, po, pml, (uint16_t*)out, pos, nchunks, cap);
     return hipGetLastError() == hipSuccess ? 0 : 10;
 }

@@ -39,6 +39,8 @@ def lib():
         L.stark_decode_attn_chunks.argtypes = [u32]
         L.stark_decode_attn_chunks.restype = u32
         L.stark_decode_attention.argtypes = [vp, vp, vp, vp, vp, vp, ip, u32, u32, u32, vp]
+        L.stark_decode_attention_fused.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ip, u32, u32, u32,
+                                                   f32, f32, vp]
         L.stark_decode_silu_mul.argtypes = [vp, vp, vp, u32, vp]
         L.stark_decode_argmax.argtypes = [vp, u32, ip, ip, ip, u32, vp]
         L.stark_decode_embed.argtypes = [vp, ip, vp, u32, u32, vp]
@@ -184,12 +186,10 @@ class Qwen3Decoder:
         for L, B in zip(self.layers, self.batches):
             _ok(D.stark_decode_rms_norm(p(self.x), p(L["attn_norm"]), p(self.h), H, cfg.eps, sp), "attn_norm")
             self.kern4.encode_prepared(B["qkv"], s)
-            _ok(D.stark_decode_qk_norm_rope(p(self.q), p(self.k), p(self.v), p(L["q_norm"]), p(L["k_norm"]),
-                                            p(L["kcache"]), p(L["vcache"]), p(self.pos), cfg.q_heads, cfg.kv_heads,
-                                            self.cap, cfg.rope_theta, cfg.eps, sp), "qk_norm_rope")
-            _ok(D.stark_decode_attention(p(self.q), p(L["kcache"]), p(L["vcache"]), p(self.po), p(self.pml),
-                                         p(self.attn), p(self.pos), cfg.q_heads, cfg.kv_heads, self.cap, sp),
-                "attention")
+            # q/k norm + RoPE, KV write and attention partials in one launch, then the chunk reduction
+            _ok(D.stark_decode_attention_fused(p(self.q), p(self.k), p(self.v), p(L["q_norm"]), p(L["k_norm"]),
+                                               p(L["kcache"]), p(L["vcache"]), p(self.po), p(self.pml), p(self.attn), p(self.pos), cfg.q_heads, cfg.kv_heads, self.cap,
+                                               cfg.rope_theta, cfg.eps, sp), "attention")
             self.kern4.encode_prepared(B["o"], s)
             _ok(D.stark_decode_rms_norm(p(self.x), p(L["mlp_norm"]), p(self.h), H, cfg.eps, sp), "mlp_norm")
             self.kern4.encode_prepared(B["gu"], s)

@@ -111,6 +111,44 @@ def test_attention(D, qh, kvh, pos):
     torch.testing.assert_close(out.float(), want, rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("qh,kvh", [(32, 8), (8, 8), (16, 8), (64, 8)])
+@pytest.mark.parametrize("pos", [0, 63, 64, 300, 1023, 1024])
+def test_attention_fused_matches_two_kernels(D, qh, kvh, pos):
+    """stark_decode_attention_fused (q/k norm + RoPE + KV write folded into the
+    attention partials) against stark_decode_qk_norm_rope followed by
+    stark_decode_attention on the same inputs; two calls in a row, the second
+    at the next position; pos == capacity: a full cache takes no new row."""
+    torch.manual_seed(qh * 7 + pos)
+    cap = 1024
+    nch = D.lib().stark_decode_attn_chunks(cap)
+    qw = (1 + 0.1 * torch.randn(128, device="cuda")).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(128, device="cuda")).to(torch.bfloat16)
+    kc = torch.randn(kvh, cap, 128, device="cuda").to(torch.bfloat16)
+    vc = torch.randn(kvh, cap, 128, device="cuda").to(torch.bfloat16)
+    kc2, vc2 = kc.clone(), vc.clone()
+    for step in range(2):
+        p_ = min(pos + step, cap)
+        q = torch.randn(qh * 128, device="cuda").to(torch.bfloat16)
+        k = torch.randn(kvh * 128, device="cuda").to(torch.bfloat16)
+        v = torch.randn(kvh * 128, device="cuda").to(torch.bfloat16)
+        p = torch.tensor([p_], dtype=torch.int32, device="cuda")
+        po = torch.empty(qh * nch * 128, device="cuda")
+        pml = torch.empty(qh * nch * 2, device="cuda")
+        out = torch.empty(qh * 128, dtype=torch.bfloat16, device="cuda")
+        assert D.lib().stark_decode_attention_fused(_p(q), _p(k), _p(v), _p(qw), _p(kw), _p(kc), _p(vc), _p(po),
+                                                    _p(pml), _p(out), _p(p), qh, kvh, cap, 1e6, 1e-6, _s()) == 0
+        q2 = q.clone()
+        po2, pml2 = torch.empty_like(po), torch.empty_like(pml)
+        out2 = torch.empty_like(out)
+        assert D.lib().stark_decode_qk_norm_rope(_p(q2), _p(k), _p(v), _p(qw), _p(kw), _p(kc2), _p(vc2), _p(p), qh,
+                                                 kvh, cap, 1e6, 1e-6, _s()) == 0
+        assert D.lib().stark_decode_attention(_p(q2), _p(kc2), _p(vc2), _p(po2), _p(pml2), _p(out2), _p(p), qh, kvh,
+                                              cap, _s()) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+        torch.testing.assert_close(out.float(), out2.float(), rtol=1e-2, atol=1e-2)
+
+
 def test_attention_rejects_bad_heads(D):
     z = C.c_void_p(0)
     assert D.lib().stark_decode_attention(z, z, z, z, z, z, z, 32, 0, 64, _s()) == 1
