@@ -40,7 +40,7 @@ __device__ __forceinline__ float plane_f32(const void* p, size_t i) {
 
 // BITS: 4 or 8. CORR: 0 symmetric, 1 biases. BF: bf16 (else f16) planes.
 template <int BITS, int CORR, bool SIGNED, bool BF>
-__global__ __launch_bounds__(256) void qgemm_mfma(AffineOp op) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
     __shared__ GemmLds lds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -152,20 +152,37 @@ __global__ __launch_bounds__(256) void qgemm_mfma(AffineOp op) {
         }
     };
 
-    // One register stage: step s computes from LDS buffer s%2 while the loads
-    // of step s+1 are in flight; they then go to the other buffer.
+    // Two register stages: step s computes from LDS buffer s%2 while step s+1
+    // (loaded during step s-1) is dequantised into the other buffer and step
+    // s+2's global loads fly; the barriers order LDS only, so those loads stay
+    // in flight across them.
+    const auto lds_barrier = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
     const uint32_t steps = K / kBK;
-    Stage st;
-    load_step(st, 0);
-    store_step(st, 0);
-    __syncthreads();
-    for (uint32_t s = 0; s < steps; ++s) {
-        const int cur = s & 1;
-        if (s + 1 < steps) load_step(st, (s + 1) * kBK);
-        compute(cur);
-        if (s + 1 < steps) store_step(st, cur ^ 1);
-        __syncthreads();
+    // Branch-free body (a conditional load would make the compiler wait for
+    // every load before the next dequantisation): the step indices of the
+    // prefetches are clamped, so the last ones re-read the final step's tile
+    // into a buffer that is not computed again.
+    Stage sa, sb;
+    load_step(sa, 0);
+    load_step(sb, min(1u, steps - 1) * kBK);
+    store_step(sa, 0);
+    lds_barrier();
+    uint32_t s = 0;
+    for (; s + 2 <= steps; s += 2) {
+        load_step(sa, min(s + 2, steps - 1) * kBK);
+        compute(0);
+        store_step(sb, 1);
+        lds_barrier();
+        load_step(sb, min(s + 3, steps - 1) * kBK);
+        compute(1);
+        store_step(sa, 0);
+        lds_barrier();
     }
+    if (s < steps) compute(0);  // odd step count: the last step sits in buffer 0
 
     // ---- epilogue: C[i][j] of a 16x16 block sits in lane j + 16*(i/4), element i%4
 #pragma unroll
