@@ -106,7 +106,10 @@ struct GGeo {
     static constexpr int BB = KIND == 12 ? 144 : 34;   // bytes per block
     static constexpr int MR = MP * MB;
     static constexpr int RR = MR / 2;                  // real rows
-    static constexpr int S = 16 / MP;                  // group slots per activation row
+    // MP == 16 is the dense form: all 16 activation rows in every MFMA, one
+    // MFMA per 32-value group (no slots; S only sizes the LDS arrays)
+    static constexpr bool DENSE = MP == 16;
+    static constexpr int S = DENSE ? 4 : 16 / MP;      // group slots per activation row
     static constexpr int GS = 32;
     static constexpr int GPS = kStep / GS;             // 4 groups per step
     static_assert(S >= GPS, "slots");
@@ -342,6 +345,64 @@ struct GEngine {
         }
     }
 
+    // Dense form: this lane's 8 codes (values 8*kq .. 8*kq+7) of wave-local
+    // group gl as one MFMA B operand in 8-bit pair order.
+    __device__ __forceinline__ u32x4 codes_dense(uint32_t gl) const {
+        const uint8_t* row = wstage + j * ROWB;
+        uint32_t a, b, m;
+        if (KIND == 12) {
+            const uint32_t sb = gl / 8, jj = gl % 8;  // super-block, sub-block
+            const uint2 u = *(const uint2*)(row + sb * BB + 16 + (jj / 2) * 32 + 8 * kq);
+            a = u.x;
+            b = u.y;
+            m = (jj & 1) ? 0x00F000F0u : 0x000F000Fu;  // high nibbles stay at bit 4 (16 q)
+        } else {
+            const uint32_t start = gl * BB + 2 + 8 * kq;  // first code byte
+            const uint32_t* base = (const uint32_t*)(row + (start & ~3u));
+            const uint32_t sh = start & 3u;               // 0 or 2
+            a = __builtin_amdgcn_alignbyte(base[1], base[0], sh) ^ 0x80808080u;  // q + 128
+            b = __builtin_amdgcn_alignbyte(base[2], base[1], sh) ^ 0x80808080u;
+            m = 0x00FF00FFu;
+        }
+        return u32x4{a & m, (a >> 8) & m, b & m, (b >> 8) & m};
+    }
+
+    // Dense form: per step 4 groups, one MFMA each over all 16 activation rows
+    // (A row i = real row i/2, hi or lo), flushed at once: lane (j, kq) holds
+    // C rows 4kq .. 4kq+3, i.e. real rows 2kq and 2kq+1 with their hi and lo
+    // parts, which it adds before the group's scale and bias.
+    template <bool TAIL>
+    __device__ __forceinline__ void compute_dense(uint32_t kvals, f32x4 (&acc)[MB]) {
+        const uint32_t qbase = wave * Q, gw = wave * GPW;
+        const uint32_t glim = TAIL ? min(kvals / 32, gw + GPW) : gw + GPW;
+        const uint32_t ar = j;  // A row of this lane
+        const uint32_t m0 = 2 * kq, m1 = 2 * kq + 1;
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s) {
+            f32x4 c[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t gl = 4 * s + t;
+                const u32x4 bq = codes_dense(gl);
+                const bool act = !TAIL || gw + gl < glim;
+                const u32x4 a = act ? lds.xp[ar][(qbase + gl * 32 + 8 * kq) / 8] : lds.zero[0];
+                c[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                             __builtin_bit_cast(bf16x8, bq), f32x4{0, 0, 0, 0}, 0, 0,
+                                                             0);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t g = gw + 4 * s + t;
+                if (TAIL && g >= glim) continue;
+                const float sc = lds.sc[g][j] * 0x1p69f, bi = lds.bi[g][j];
+                const float x0 = lds.xs[2 * m0][g] + lds.xs[2 * m0 + 1][g];
+                const float x1 = lds.xs[2 * m1][g] + lds.xs[2 * m1 + 1][g];
+                acc[0][0] = fmaf(sc, c[t][0] + c[t][1], fmaf(bi, x0, acc[0][0]));
+                acc[0][1] = fmaf(sc, c[t][2] + c[t][3], fmaf(bi, x1, acc[0][1]));
+            }
+        }
+    }
+
     template <bool TAIL>
     __device__ __forceinline__ void compute(uint32_t M, uint32_t kvals, f32x4 (&acc)[MB]) {
         f32x4 C0[MB], C1[MB];
@@ -385,10 +446,23 @@ struct GEngine {
             if (kbase + PASS < K) load(op, n0, M, kbase + PASS);
             decode_meta(kvals);
             __syncthreads();
-            if (kvals == (uint32_t)PASS)
-                compute<false>(M, kvals, acc);
-            else
-                compute<true>(M, kvals, acc);
+            if constexpr (G::DENSE) {
+                if (kvals == (uint32_t)PASS)
+                    compute_dense<false>(kvals, acc);
+                else
+                    compute_dense<true>(kvals, acc);
+            } else {
+                if (kvals == (uint32_t)PASS)
+                    compute<false>(M, kvals, acc);
+                else
+                    compute<true>(M, kvals, acc);
+            }
+        }
+        if constexpr (G::DENSE) {  // real rows 2kq and 2kq+1 of column j
+            lds.red[wave][2 * kq][j] = acc[0][0];
+            lds.red[wave][2 * kq + 1][j] = acc[0][1];
+            __syncthreads();
+            return;
         }
         // lane's slots sum to one activation row's share; hi and lo rows meet
 #pragma unroll
@@ -451,8 +525,7 @@ stark_qmm_status launch_class(int c, const GgufOp* ops, uint32_t count, uint32_t
     switch (c) {
     case 0: return launch_mfma<KIND, 2, 1>(ops, count, status, stream);
     case 1: return launch_mfma<KIND, 4, 1>(ops, count, status, stream);
-    case 2: return launch_mfma<KIND, 4, 2>(ops, count, status, stream);
-    default: return launch_mfma<KIND, 4, 4>(ops, count, status, stream);
+    default: return launch_mfma<KIND, 16, 1>(ops, count, status, stream);  // M = 3 .. 8: dense
     }
 }
 
