@@ -110,6 +110,8 @@ struct GGeo {
     // MFMA per 32-value group (no slots; S only sizes the LDS arrays)
     static constexpr bool DENSE = MP == 16;
     static constexpr int S = DENSE ? 4 : 16 / MP;      // group slots per activation row
+    // the dense form runs TPW 16-row tiles per pass under one activation stage
+    static constexpr int TPW = DENSE ? 2 : 1;
     static constexpr int GS = 32;
     static constexpr int GPS = kStep / GS;             // 4 groups per step
     static_assert(S >= GPS, "slots");
@@ -123,6 +125,7 @@ struct GGeo {
     static constexpr int ROWB = SEGB + 16;              // padded LDS row
     static constexpr int NSTEP = Q / kStep;
     static constexpr int GPP = PASS / GS, GPW = Q / GS;
+    static constexpr int GX = DENSE ? GPP : GPP + S;    // group entries of the LDS tables
     static constexpr int XV = RR * (PASS / 8);          // 8-value activation chunks per pass
     static constexpr int XI = (XV + kWg - 1) / kWg;
     static_assert(SEGB % 16 == 0 && BPW >= 1, "pass geometry");
@@ -131,12 +134,14 @@ struct GGeo {
 template <int KIND, int MP, int MB>
 struct GLds {
     using G = GGeo<KIND, MP, MB>;
-    u32x4 stage[4][kRows * G::ROWB / 16];  // raw block bytes, per wave [16][ROWB]
-    float sc[G::GPP + G::S][kRows];        // per (group, row) scale
-    float bi[G::GPP + G::S][kRows];        // per (group, row) bias term (Q4_K)
-    u32x4 xp[G::MR][G::PASS / 8];          // activation rows (hi, lo per real row), 8-bit pair order
-    float xs[G::MR][G::GPP + G::S];        // per-group activation sums
-    float red[4][G::RR][kRows];
+    union {
+        u32x4 stage[G::TPW][4][kRows * G::ROWB / 16];  // raw block bytes, per tile and wave [16][ROWB]
+        float red[G::TPW][4][G::RR][kRows];            // per-wave results, after the last pass
+    };
+    float sc[G::TPW][G::GX][kRows];  // per (group, row) scale
+    float bi[G::TPW][G::GX][kRows];  // per (group, row) bias term
+    u32x4 xp[G::MR][G::PASS / 8];    // activation rows (hi, lo per real row), 8-bit pair order
+    float xs[G::MR][G::GX];          // per-group activation sums
     u32x4 zero[4];
 };
 
@@ -149,11 +154,11 @@ struct GEngine {
     static constexpr int S = G::S, MR = G::MR, RR = G::RR, PASS = G::PASS, Q = G::Q, BE = G::BE, BB = G::BB;
     static constexpr int SEGB = G::SEGB, PPR = G::PPR, NI = G::NI, ROWB = G::ROWB, NSTEP = G::NSTEP;
     static constexpr int PERIOD = G::PERIOD, GPP = G::GPP, GPW = G::GPW, XV = G::XV, XI = G::XI, BPW = G::BPW;
+    static constexpr int TPW = G::TPW;
 
     GLds<KIND, MP, MB>& lds;
     uint32_t tid, lane, wave, j, kq, am, aslot;
-    uint8_t* wstage;
-    u32x4 w[NI];
+    u32x4 w[TPW][NI];
     u32x4 xa[XI], xb[XI];  // 8 f32 activations per chunk
 
     __device__ __forceinline__ explicit GEngine(GLds<KIND, MP, MB>& l) : lds(l) {
@@ -164,26 +169,29 @@ struct GEngine {
         kq = lane >> 4;
         am = j / S;
         aslot = j % S;
-        wstage = (uint8_t*)lds.stage[wave];
         if (tid < 4) lds.zero[tid] = u32x4{0, 0, 0, 0};
     }
 
     // Issue the pass's loads: raw block bytes of the wave's quarter of the 16
     // rows (pieces past the pass's blocks read as zero through the buffer
     // resource) and the f32 activation chunks.
-    __device__ __forceinline__ void load(const GgufOp& op, uint32_t n0, uint32_t M, uint32_t kbase) {
+    __device__ __forceinline__ void load(const GgufOp& op, const uint32_t (&n0)[TPW], uint32_t M, uint32_t kbase) {
         const uint32_t K = op.k, kvals = min((uint32_t)PASS, K - kbase);
         const uint32_t row_bytes = K / BE * BB;
-        const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(op.blocks + (size_t)n0 * row_bytes), 0, (int)(kRows * row_bytes), 0x00020000);
         const uint32_t vbytes = kvals / BE * BB;  // valid bytes of a row in this pass
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const uint32_t p = i * 64 + lane, r = p / PPR, c = (p % PPR) * 16;
-            const uint32_t col = wave * SEGB + c;
-            const uint32_t vo = p < (uint32_t)(kRows * PPR) && col < vbytes ? r * row_bytes + col + kbase / BE * BB
-                                                                            : 0x80000000u;
-            w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(crs, vo, 0, kBufNt));
+        for (int tt = 0; tt < TPW; ++tt) {
+            const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(op.blocks + (size_t)n0[tt] * row_bytes), 0, (int)(kRows * row_bytes), 0x00020000);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t p = i * 64 + lane, r = p / PPR, c = (p % PPR) * 16;
+                const uint32_t col = wave * SEGB + c;
+                const uint32_t vo = p < (uint32_t)(kRows * PPR) && col < vbytes
+                                        ? r * row_bytes + col + kbase / BE * BB
+                                        : 0x80000000u;
+                w[tt][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(crs, vo, 0, kBufNt));
+            }
         }
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
@@ -200,9 +208,13 @@ struct GEngine {
     __device__ __forceinline__ void stage(uint32_t kvals, uint32_t M, uint32_t* status) {
         bool bad = false;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const uint32_t p = i * 64 + lane;
-            if (p < (uint32_t)(kRows * PPR)) *(u32x4*)(wstage + (p / PPR) * ROWB + (p % PPR) * 16) = w[i];
+        for (int tt = 0; tt < TPW; ++tt) {
+            uint8_t* ws = (uint8_t*)lds.stage[tt][wave];
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t p = i * 64 + lane;
+                if (p < (uint32_t)(kRows * PPR)) *(u32x4*)(ws + (p / PPR) * ROWB + (p % PPR) * 16) = w[tt][i];
+            }
         }
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
@@ -263,9 +275,9 @@ struct GEngine {
     __device__ __forceinline__ void decode_meta(uint32_t kvals) {
         const uint32_t nblk = kvals / BE;  // blocks of a row in this pass
         if (KIND == 12) {
-            for (uint32_t t = tid; t < kRows * nblk; t += kWg) {
-                const uint32_t r = t % kRows, b = t / kRows;
-                const uint8_t* blk = (const uint8_t*)lds.stage[b / BPW] + r * ROWB + (b % BPW) * BB;
+            for (uint32_t t = tid; t < kRows * nblk * TPW; t += kWg) {
+                const uint32_t r = t % kRows, b = (t / kRows) % nblk, tt = t / (kRows * nblk);
+                const uint8_t* blk = (const uint8_t*)lds.stage[tt][b / BPW] + r * ROWB + (b % BPW) * BB;
                 const u32x4 h = *(const u32x4*)blk;
                 const float d = f16_bits_to_f32(h[0] & 0xffffu), dmin = f16_bits_to_f32(h[0] >> 16);
                 const uint32_t q3[3] = {h[1], h[2], h[3]};
@@ -273,17 +285,17 @@ struct GEngine {
                 for (uint32_t jj = 0; jj < 8; ++jj) {
                     float scj, mj;
                     scale_min(q3, jj, &scj, &mj);
-                    lds.sc[b * 8 + jj][r] = d * scj;
-                    lds.bi[b * 8 + jj][r] = -(dmin * mj);
+                    lds.sc[tt][b * 8 + jj][r] = d * scj;
+                    lds.bi[tt][b * 8 + jj][r] = -(dmin * mj);
                 }
             }
         } else {
-            for (uint32_t t = tid; t < kRows * nblk; t += kWg) {
-                const uint32_t r = t % kRows, b = t / kRows;
-                const uint8_t* blk = (const uint8_t*)lds.stage[b / BPW] + r * ROWB + (b % BPW) * BB;
+            for (uint32_t t = tid; t < kRows * nblk * TPW; t += kWg) {
+                const uint32_t r = t % kRows, b = (t / kRows) % nblk, tt = t / (kRows * nblk);
+                const uint8_t* blk = (const uint8_t*)lds.stage[tt][b / BPW] + r * ROWB + (b % BPW) * BB;
                 const float d = f16_bits_to_f32(*(const uint16_t*)blk);
-                lds.sc[b][r] = d;
-                lds.bi[b][r] = -128.0f * d;  // codes enter as q + 128
+                lds.sc[tt][b][r] = d;
+                lds.bi[tt][b][r] = -128.0f * d;  // codes enter as q + 128
             }
         }
     }
@@ -291,7 +303,7 @@ struct GEngine {
     // This lane's 32 codes of step s as 4 MFMA operands, and each operand's
     // wave-local group and first value.
     __device__ __forceinline__ void codes(int s, u32x4 (&bq)[4], uint32_t (&grp)[4], uint32_t (&e0)[4]) const {
-        const uint8_t* row = wstage + j * ROWB;
+        const uint8_t* row = (const uint8_t*)lds.stage[0][wave] + j * ROWB;
         if (KIND == 12) {
             const uint32_t sb = s / 2, p = 2 * (s % 2) + kq / 2, l0 = 16 * (kq % 2);
             const u32x4 u = *(const u32x4*)(row + sb * BB + 16 + p * 32 + l0);
@@ -338,7 +350,8 @@ struct GEngine {
             const f32x4 x4 = *(const f32x4*)&lds.xs[a][g4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float nv = fmaf(lds.sc[g4 + q][j] * 0x1p69f, c[q], fmaf(lds.bi[g4 + q][j], x4[q], acc[b][q]));
+                const float nv =
+                    fmaf(lds.sc[0][g4 + q][j] * 0x1p69f, c[q], fmaf(lds.bi[0][g4 + q][j], x4[q], acc[b][q]));
                 acc[b][q] = g4 + q < glim ? nv : acc[b][q];
             }
             C0[b] = C1[b] = f32x4{0, 0, 0, 0};
@@ -347,8 +360,8 @@ struct GEngine {
 
     // Dense form: this lane's 8 codes (values 8*kq .. 8*kq+7) of wave-local
     // group gl as one MFMA B operand in 8-bit pair order.
-    __device__ __forceinline__ u32x4 codes_dense(uint32_t gl) const {
-        const uint8_t* row = wstage + j * ROWB;
+    __device__ __forceinline__ u32x4 codes_dense(int tt, uint32_t gl) const {
+        const uint8_t* row = (const uint8_t*)lds.stage[tt][wave] + j * ROWB;
         uint32_t a, b, m;
         if (KIND == 12) {
             const uint32_t sb = gl / 8, jj = gl % 8;  // super-block, sub-block
@@ -367,38 +380,46 @@ struct GEngine {
         return u32x4{a & m, (a >> 8) & m, b & m, (b >> 8) & m};
     }
 
-    // Dense form: per step 4 groups, one MFMA each over all 16 activation rows
-    // (A row i = real row i/2, hi or lo), flushed at once: lane (j, kq) holds
-    // C rows 4kq .. 4kq+3, i.e. real rows 2kq and 2kq+1 with their hi and lo
-    // parts, which it adds before the group's scale and bias.
+    // Dense form: per step and tile 4 groups, one MFMA each over all 16
+    // activation rows (A row i = real row i/2, hi or lo; the A operand serves
+    // every tile), flushed at once: lane (j, kq) holds C rows 4kq .. 4kq+3,
+    // i.e. real rows 2kq and 2kq+1 with their hi and lo parts, which it adds
+    // before the group's scale and bias.
     template <bool TAIL>
-    __device__ __forceinline__ void compute_dense(uint32_t kvals, f32x4 (&acc)[MB]) {
+    __device__ __forceinline__ void compute_dense(uint32_t kvals, f32x4 (&acc)[TPW]) {
         const uint32_t qbase = wave * Q, gw = wave * GPW;
         const uint32_t glim = TAIL ? min(kvals / 32, gw + GPW) : gw + GPW;
         const uint32_t ar = j;  // A row of this lane
         const uint32_t m0 = 2 * kq, m1 = 2 * kq + 1;
 #pragma unroll
         for (int s = 0; s < NSTEP; ++s) {
-            f32x4 c[4];
+            u32x4 a[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const uint32_t gl = 4 * s + t;
-                const u32x4 bq = codes_dense(gl);
                 const bool act = !TAIL || gw + gl < glim;
-                const u32x4 a = act ? lds.xp[ar][(qbase + gl * 32 + 8 * kq) / 8] : lds.zero[0];
-                c[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                             __builtin_bit_cast(bf16x8, bq), f32x4{0, 0, 0, 0}, 0, 0,
-                                                             0);
+                a[t] = act ? lds.xp[ar][(qbase + gl * 32 + 8 * kq) / 8] : lds.zero[0];
             }
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t g = gw + 4 * s + t;
-                if (TAIL && g >= glim) continue;
-                const float sc = lds.sc[g][j] * 0x1p69f, bi = lds.bi[g][j];
-                const float x0 = lds.xs[2 * m0][g] + lds.xs[2 * m0 + 1][g];
-                const float x1 = lds.xs[2 * m1][g] + lds.xs[2 * m1 + 1][g];
-                acc[0][0] = fmaf(sc, c[t][0] + c[t][1], fmaf(bi, x0, acc[0][0]));
-                acc[0][1] = fmaf(sc, c[t][2] + c[t][3], fmaf(bi, x1, acc[0][1]));
+            for (int tt = 0; tt < TPW; ++tt) {
+                f32x4 c[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const u32x4 bq = codes_dense(tt, 4 * s + t);
+                    c[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[t]),
+                                                                 __builtin_bit_cast(bf16x8, bq), f32x4{0, 0, 0, 0},
+                                                                 0, 0, 0);
+                }
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t g = gw + 4 * s + t;
+                    if (TAIL && g >= glim) continue;
+                    const float sc = lds.sc[tt][g][j] * 0x1p69f, bi = lds.bi[tt][g][j];
+                    const float x0 = lds.xs[2 * m0][g] + lds.xs[2 * m0 + 1][g];
+                    const float x1 = lds.xs[2 * m1][g] + lds.xs[2 * m1 + 1][g];
+                    acc[tt][0] = fmaf(sc, c[t][0] + c[t][1], fmaf(bi, x0, acc[tt][0]));
+                    acc[tt][1] = fmaf(sc, c[t][2] + c[t][3], fmaf(bi, x1, acc[tt][1]));
+                }
             }
         }
     }
@@ -432,11 +453,11 @@ struct GEngine {
         }
     }
 
-    __device__ __forceinline__ void run(const GgufOp& op, uint32_t n0, uint32_t M, uint32_t* status) {
+    __device__ __forceinline__ void run(const GgufOp& op, const uint32_t (&n0)[TPW], uint32_t M, uint32_t* status) {
         const uint32_t K = op.k;
-        f32x4 acc[MB];
+        f32x4 acc[MB * TPW];
 #pragma unroll
-        for (int b = 0; b < MB; ++b) acc[b] = f32x4{0, 0, 0, 0};
+        for (int b = 0; b < MB * TPW; ++b) acc[b] = f32x4{0, 0, 0, 0};
         load(op, n0, M, 0);
         for (uint32_t kbase = 0; kbase < K; kbase += PASS) {
             const uint32_t kvals = min((uint32_t)PASS, K - kbase);
@@ -458,9 +479,13 @@ struct GEngine {
                     compute<true>(M, kvals, acc);
             }
         }
+        __syncthreads();  // the results overwrite the code stage
         if constexpr (G::DENSE) {  // real rows 2kq and 2kq+1 of column j
-            lds.red[wave][2 * kq][j] = acc[0][0];
-            lds.red[wave][2 * kq + 1][j] = acc[0][1];
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+                lds.red[tt][wave][2 * kq][j] = acc[tt][0];
+                lds.red[tt][wave][2 * kq + 1][j] = acc[tt][1];
+            }
             __syncthreads();
             return;
         }
@@ -471,10 +496,10 @@ struct GEngine {
             if (S == 8) {  // kq 0,1: hi; kq 2,3: lo
                 v += __shfl_xor(v, 16, 64);
                 v += __shfl_xor(v, 32, 64);
-                if (kq == 0) lds.red[wave][b * (MP / 2)][j] = v;
+                if (kq == 0) lds.red[0][wave][b * (MP / 2)][j] = v;
             } else {  // S == 4: lane row a = kq; real row kq / 2
                 v += __shfl_xor(v, 16, 64);
-                if ((kq & 1) == 0) lds.red[wave][b * (MP / 2) + kq / 2][j] = v;
+                if ((kq & 1) == 0) lds.red[0][wave][b * (MP / 2) + kq / 2][j] = v;
             }
         }
         __syncthreads();
@@ -491,15 +516,20 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(MB >= 4 ? 2
         if (blockIdx.x >= kb->op[i].block_begin) oi = i;
     const GgufOp& op = kb->op[oi];
     const uint32_t N = op.n;
-    const uint32_t t0 = (blockIdx.x - op.block_begin) * kRows;
-    const uint32_t n0 = min(t0, N - kRows);  // last tile moved back to end at N
+    constexpr int TPW = GGeo<KIND, MP, MB>::TPW, RR = MP * MB / 2;
+    // tile tt covers rows n0[tt] .. +15 and writes those from t0 + 16 tt on; a
+    // tile past N moves back to end at N, so every row is written once
+    const uint32_t t0 = (blockIdx.x - op.block_begin) * kRows * TPW;
+    uint32_t n0[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) n0[tt] = min(t0 + kRows * tt, N - kRows);
     GEngine<KIND, MP, MB> e(lds);
     e.run(op, n0, op.m, kb->status);
-    constexpr int RR = MP * MB / 2;
-    for (uint32_t t = threadIdx.x; t < (uint32_t)RR * kRows; t += kWg) {
-        const uint32_t m = t / kRows, r = t % kRows, n = n0 + r;
-        if (m >= op.m || n < t0) continue;
-        const float v = (lds.red[0][m][r] + lds.red[1][m][r]) + (lds.red[2][m][r] + lds.red[3][m][r]);
+    for (uint32_t t = threadIdx.x; t < (uint32_t)(TPW * RR * kRows); t += kWg) {
+        const uint32_t tt = t / (RR * kRows), m = (t / kRows) % RR, r = t % kRows;
+        const uint32_t n = min(t0 + kRows * tt, N - kRows) + r;
+        if (m >= op.m || n < t0 + kRows * tt) continue;
+        const float v = (lds.red[tt][0][m][r] + lds.red[tt][1][m][r]) + (lds.red[tt][2][m][r] + lds.red[tt][3][m][r]);
         store_from_f32(op.d, op.d_dt, (size_t)m * N + n, v);
     }
 }
@@ -512,7 +542,7 @@ stark_qmm_status launch_mfma(const GgufOp* ops, uint32_t count, uint32_t* status
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = ops[i];
         batch.op[i].block_begin = blocks;
-        blocks += (ops[i].n + kRows - 1) / kRows;
+        blocks += (ops[i].n + kRows * GGeo<KIND, MP, MB>::TPW - 1) / (kRows * GGeo<KIND, MP, MB>::TPW);
     }
     batch.count = count;
     if (blocks) hipLaunchKernelGGL((gguf_mfma<KIND, MP, MB>), dim3(blocks), dim3(kWg), 0, stream, batch);

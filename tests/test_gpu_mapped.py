@@ -56,6 +56,14 @@ def test_packed_small_m(qmm, oracle, kind, m):
 
 
 @pytest.mark.parametrize("kind", [8, 12])
+@pytest.mark.parametrize("n,k,m", [(16, 2304, 3), (40, 1280, 8), (300, 256, 6), (48, 4096, 4)])
+def test_packed_small_m_ragged(qmm, oracle, kind, n, k, m):
+    """Row counts that leave the last pair of 16-row tiles partial or shifted
+    back, and K with a partial last pass."""
+    _run_packed(qmm, oracle, kind, n, k, m, seed=n + k + m + kind)
+
+
+@pytest.mark.parametrize("kind", [8, 12])
 def test_packed_bf16_exact_inputs(qmm, oracle, kind):
     _run_packed(qmm, oracle, kind, 256, 4096, 1, seed=5 + kind, xkind="bf16")
 
