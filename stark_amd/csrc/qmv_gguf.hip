@@ -145,7 +145,12 @@ struct GLds {
     u32x4 zero[4];
 };
 
-__device__ __forceinline__ uint32_t f32_to_bf16_rne_bits(float f) { return f32_to_bf16_bits(f); }
+// two f32 to bf16 (round to nearest even) in one word, the first in the low half
+__device__ __forceinline__ uint32_t bf16_pack(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
 
 // One tile of a GGUF product: op rows n0..n0+15, real activation rows 0..M-1.
 template <int KIND, int MP, int MB>
@@ -219,7 +224,7 @@ struct GEngine {
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
             const uint32_t v = tid + i * kWg, r = v / (PASS / 8), c = v % (PASS / 8);
-            float x[8], hi[8], lo[8];
+            float x[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 x[e] = __uint_as_float(xa[i][e]);
@@ -227,32 +232,29 @@ struct GEngine {
             }
             // Q4_K: values 32..63 of every 64 meet the high nibbles (16 q)
             const float sc = (KIND == 12 && ((c * 8) & 32)) ? 0x1p60f : 0x1p64f;
-            float shi = 0.0f, slo = 0.0f;
             if (v < (uint32_t)XV && r < M && c * 8 < kvals) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(x[e]);
             }
+            // hi = bf16(x sc) = bf16(x) sc and lo = bf16(x sc - hi) through the
+            // hardware round-to-nearest-even pack; sc is a power of two, so the
+            // sums of the scaled parts times 1/sc are the sums of the parts
+            float shi = 0.0f, slo = 0.0f;
+            u32x4 ph, pl;  // 8-bit pair order (x0,x2)(x1,x3)(x4,x6)(x5,x7)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t hb = f32_to_bf16_rne_bits(x[e]);
-                const float h = __uint_as_float(hb << 16);
-                const uint32_t lb = f32_to_bf16_rne_bits(x[e] - h);
-                const float l = __uint_as_float(lb << 16);
-                shi += h;
-                slo += l;
-                hi[e] = h * sc;
-                lo[e] = l * sc;
+            for (int q = 0; q < 4; ++q) {
+                const int e0 = (q & 1) + 4 * (q >> 1), e1 = e0 + 2;
+                const float a0 = x[e0] * sc, a1 = x[e1] * sc;
+                const uint32_t hb = bf16_pack(a0, a1);
+                const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xffff0000u);
+                const float l0 = a0 - h0, l1 = a1 - h1;
+                ph[q] = hb;
+                pl[q] = bf16_pack(l0, l1);
+                shi += h0 + h1;
+                slo += __uint_as_float(pl[q] << 16) + __uint_as_float(pl[q] & 0xffff0000u);
             }
-            // 8-bit pair order (x0,x2)(x1,x3)(x4,x6)(x5,x7)
-            u32x4 ph, pl;
-            ph[0] = perm(__float_as_uint(hi[2]), __float_as_uint(hi[0]), 0x07060302u);
-            ph[1] = perm(__float_as_uint(hi[3]), __float_as_uint(hi[1]), 0x07060302u);
-            ph[2] = perm(__float_as_uint(hi[6]), __float_as_uint(hi[4]), 0x07060302u);
-            ph[3] = perm(__float_as_uint(hi[7]), __float_as_uint(hi[5]), 0x07060302u);
-            pl[0] = perm(__float_as_uint(lo[2]), __float_as_uint(lo[0]), 0x07060302u);
-            pl[1] = perm(__float_as_uint(lo[3]), __float_as_uint(lo[1]), 0x07060302u);
-            pl[2] = perm(__float_as_uint(lo[6]), __float_as_uint(lo[4]), 0x07060302u);
-            pl[3] = perm(__float_as_uint(lo[7]), __float_as_uint(lo[5]), 0x07060302u);
+            shi *= 1.0f / sc;
+            slo *= 1.0f / sc;
             // the 4 chunks of a 32-value group sit in consecutive lanes
             shi += __shfl_xor(shi, 1, 64);
             shi += __shfl_xor(shi, 2, 64);
