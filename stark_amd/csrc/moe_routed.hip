@@ -71,50 +71,191 @@ RoutedLayout routed_layout(uint32_t rows, uint32_t model, uint32_t hidden, uint3
 // ---- 2. compaction: one workgroup of 1024 threads, one thread per expert id.
 // Routes are counting-sorted by expert, then every expert's routes are cut
 // into slots of at most 16 and each slot is written as a self-contained record
-// into the table of its route-count class.
-__global__ __launch_bounds__(1024) void moe_compact(const uint32_t* ids, uint32_t routes, uint32_t experts,
-                                                    uint32_t max_slots, uint32_t* sorted, uint32_t* table,
-                                                    uint32_t* header) {
-    __shared__ uint32_t cnt[1024], fill[1024], off[1024], wsum[16], ccount[kClasses];
+// into the table of its route-count class. `ids` may be in LDS or global.
+struct CompactLds {
+    uint32_t cnt[1024], fill[1024], off[1024], wsum[16], ccount[kClasses];
+};
+
+__device__ __forceinline__ void compact_routes(const uint32_t* ids, uint32_t routes, uint32_t experts,
+                                               uint32_t max_slots, uint32_t* sorted, uint32_t* table,
+                                               uint32_t* header, CompactLds& s) {
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    cnt[t] = 0;
-    fill[t] = 0;
-    if (t < kClasses) ccount[t] = 0;
+    s.cnt[t] = 0;
+    s.fill[t] = 0;
+    if (t < kClasses) s.ccount[t] = 0;
     __syncthreads();
     for (uint32_t r = t; r < routes; r += 1024) {
         uint32_t e = ids[r];
         e = e < experts ? e : 0;  // out-of-range ids read expert 0's rows (MoeGatherRows, moe.rs:87-107)
-        atomicAdd(&cnt[e], 1u);
+        atomicAdd(&s.cnt[e], 1u);
     }
     __syncthreads();
     // exclusive scan of the route counts over experts
-    const uint32_t c = cnt[t];
+    const uint32_t c = s.cnt[t];
     uint32_t ic = c;
     for (uint32_t d = 1; d < 64; d <<= 1) {
         const uint32_t u = __shfl_up(ic, d, 64);
         if (lane >= d) ic += u;
     }
-    if (lane == 63) wsum[wave] = ic;
+    if (lane == 63) s.wsum[wave] = ic;
     __syncthreads();
     uint32_t pc = 0;
-    for (uint32_t w = 0; w < wave; ++w) pc += wsum[w];
-    off[t] = pc + ic - c;
+    for (uint32_t w = 0; w < wave; ++w) pc += s.wsum[w];
+    s.off[t] = pc + ic - c;
     __syncthreads();
     for (uint32_t r = t; r < routes; r += 1024) {
         uint32_t e = ids[r];
         e = e < experts ? e : 0;
-        sorted[off[e] + atomicAdd(&fill[e], 1u)] = r;
+        sorted[s.off[e] + atomicAdd(&s.fill[e], 1u)] = r;
     }
     __syncthreads();  // sorted[] complete and visible to the workgroup
     for (uint32_t s0 = 0; s0 < c; s0 += kSlotRoutes) {
         const uint32_t n = min(kSlotRoutes, c - s0), cl = count_class(n);
-        uint32_t* rec = table + ((size_t)cl * max_slots + atomicAdd(&ccount[cl], 1u)) * kRecWords;
+        uint32_t* rec = table + ((size_t)cl * max_slots + atomicAdd(&s.ccount[cl], 1u)) * kRecWords;
         rec[0] = t;
         rec[1] = n;
-        for (uint32_t i = 0; i < n; ++i) rec[2 + i] = sorted[off[t] + s0 + i];
+        for (uint32_t i = 0; i < n; ++i) rec[2 + i] = sorted[s.off[t] + s0 + i];
     }
     __syncthreads();
-    if (t < kClasses) header[t] = ccount[t];
+    if (t < kClasses) header[t] = s.ccount[t];
+}
+
+__global__ __launch_bounds__(1024) void moe_compact(const uint32_t* ids, uint32_t routes, uint32_t experts,
+                                                    uint32_t max_slots, uint32_t* sorted, uint32_t* table,
+                                                    uint32_t* header) {
+    __shared__ CompactLds s;
+    compact_routes(ids, routes, experts, max_slots, sorted, table, header, s);
+}
+
+// ---- 1+2 fused for up to kFusedRoutes routes: route, adjust and compaction in
+// one workgroup, every phase spread over all 1024 threads (a single wave64
+// retires about one VALU instruction per 4 clocks, so no phase may leave the
+// work to a few waves):
+//   a. the logits of all rows into LDS (bf16-rounded if asked) as 64-bit keys
+//      (order-preserving value bits over the inverted expert id, -0 taken as
+//      +0), a per-row finite flag;
+//   b. per row (one wave each): max and den = sum exp(x - max) (a wave tree
+//      sum, the device expf);
+//   c. ranks: expert e of a row lands at rank
+//      #{e' : x[e'] > x[e] or (x[e'] == x[e] and e' < e)}, the order of the
+//      reference's repeated argmax in which a strictly greater value wins and
+//      ties go to the lower id (moe.rs:52-70), i.e. #{e' : key(e') > key(e)}.
+//      Eight consecutive lanes count one expert against interleaved eighths
+//      of the row (adjacent keys: no LDS bank conflicts) and add by shuffles;
+//   d. per row (one wave, lane = rank): score exp(x - max) / den, summed in
+//      rank order and renormalised (moe.rs:71-84); then the gains and the
+//      stable id sort of MoeAdjustRoutes (moe.rs:147-184), the sort as a rank
+//      count over the row's routes; ids and weights to the workspace and LDS;
+//   e. compaction.
+// Dynamic LDS: rows * E keys. The rank count costs rows * E^2 compares in one
+// CU, so larger cases take the multi-workgroup route kernel.
+constexpr uint32_t kFusedRoutes = 2048;
+constexpr uint32_t kFusedKeys = 4096;
+constexpr uint32_t kFusedRows = 512;
+constexpr uint64_t kFusedCompares = 65536;
+
+__device__ __forceinline__ uint64_t route_key(float x, uint32_t e) {
+    const uint32_t u = __float_as_uint(x + 0.0f);  // -0 -> +0: equal values tie
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (0xffffffffu - e);
+}
+
+__device__ __forceinline__ float route_key_value(uint64_t k) {
+    const uint32_t o = (uint32_t)(k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+__device__ __forceinline__ float route_round_bf16(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+__global__ __launch_bounds__(1024) void moe_route_compact(const float* logits, uint32_t rows, uint32_t experts,
+                                                          uint32_t active, uint32_t round_weights,
+                                                          uint32_t round_logits, const float* gains,
+                                                          uint32_t adjust, uint32_t sort_ids, uint32_t max_slots,
+                                                          uint32_t* ids, float* weights, uint32_t* sorted,
+                                                          uint32_t* table, uint32_t* header) {
+    __shared__ CompactLds s;
+    __shared__ uint32_t rid[kFusedRoutes];  // ids, then (after d) the compaction input
+    __shared__ float rmax[kFusedRows], rden[kFusedRows];
+    __shared__ uint32_t rbad[kFusedRows];
+    extern __shared__ uint64_t keys[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t E = experts, RE = rows * experts;
+    // a.
+    for (uint32_t r = tid; r < rows; r += 1024) rbad[r] = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < RE; i += 1024) {
+        float x = logits[i];
+        if (round_logits) x = route_round_bf16(x);
+        keys[i] = route_key(x, i % E);
+        if (!__builtin_isfinite(x)) rbad[i / E] = 1;
+    }
+    __syncthreads();
+    // b.
+    for (uint32_t row = wave; row < rows; row += 16) {
+        const uint64_t* kr = keys + (size_t)row * E;
+        float mx = -INFINITY;
+        for (uint32_t e = lane; e < E; e += 64) mx = fmaxf(mx, route_key_value(kr[e]));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float den = 0.0f;
+        for (uint32_t e = lane; e < E; e += 64) den += expf(route_key_value(kr[e]) - mx);
+        den = wave_sum(den);
+        if (lane == 0) {
+            rmax[row] = mx;
+            rden[row] = den;
+        }
+    }
+    // c.
+    for (uint32_t it = tid; it < RE * 8; it += 1024) {  // RE * 8 is a multiple of 8: lane groups stay whole
+        const uint32_t q = it & 7, re = it >> 3, row = re / E, e = re % E;
+        const uint64_t* kr = keys + (size_t)row * E;
+        const uint64_t k = kr[e];
+        uint32_t rank = 0;
+#pragma unroll 4
+        for (uint32_t f = q; f < E; f += 8) rank += kr[f] > k ? 1u : 0u;  // lanes of a group: adjacent keys
+        rank += __shfl_xor(rank, 1, 64);
+        rank += __shfl_xor(rank, 2, 64);
+        rank += __shfl_xor(rank, 4, 64);
+        if (q == 0 && rank < active) rid[row * active + rank] = e;
+    }
+    __syncthreads();
+    // d.
+    for (uint32_t row = wave; row < rows; row += 16) {
+        const bool valid = rbad[row] == 0;
+        const uint32_t my_id = lane < active ? rid[row * active + lane] : 0u;
+        // a row with a non-finite logit may leave ranks unfilled: its ids become 0
+        const float my_v = lane < active && my_id < E ? route_key_value(keys[(size_t)row * E + my_id]) : 0.0f;
+        const float score = lane < active ? expf(my_v - rmax[row]) / rden[row] : 0.0f;
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < active; ++r) sum += __shfl(score, r, 64);
+        float w = score / sum;
+        if (round_weights) w = route_round_bf16(w);
+        const uint32_t id = valid ? my_id : 0u;
+        w = valid ? w : __builtin_nanf("");
+        uint32_t pos = lane;
+        if (adjust) {
+            w = id < experts ? w * (gains ? gains[id] : 1.0f) : __builtin_nanf("");
+            if (sort_ids) {
+                pos = 0;
+                for (uint32_t r = 0; r < active; ++r) {
+                    const uint32_t o = __shfl(id, r, 64);
+                    pos += (o < id || (o == id && r < lane)) ? 1u : 0u;
+                }
+            }
+        }
+        // every lane has read its rank's id before any lane rewrites the row
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < active) {
+            ids[(size_t)row * active + pos] = id;
+            weights[(size_t)row * active + pos] = w;
+            rid[row * active + pos] = id;
+        }
+    }
+    __syncthreads();
+    // e.
+    compact_routes(rid, rows * active, experts, max_slots, sorted, table, header, s);
 }
 
 // Launch record of a grouped product, read through the kernarg segment.
@@ -337,18 +478,25 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
     uint16_t* act = (uint16_t*)(ws + Lw.act);
     uint16_t* proj = (uint16_t*)(ws + Lw.proj);
 
-    // 1. route (+ adjust), as routed.rs:188-209
-    st = stark_qmm_moe_route(a->router_logits, ids, weights, R, E, A, a->round_weights_bf16, a->round_logits_bf16,
-                             stream);
-    if (st != STARK_QMM_OK) return st;
-    if (a->expert_scales || a->sort_expert_ids)
-        st = launch_moe_adjust(ids, weights, a->expert_scales, R, E, A, a->expert_scales ? a->sort_expert_ids : 1,
-                               stream);
-    if (st != STARK_QMM_OK) return st;
-    // 2. compaction
-    hipLaunchKernelGGL(moe_compact, dim3(1), dim3(1024), 0, stream, ids, Lw.routes, E, Lw.max_slots, sorted, table,
-                       header);
-    QMM_HIP_CHECK(hipGetLastError());
+    // 1. route (+ adjust), as routed.rs:188-209, and 2. compaction
+    const bool adjust = a->expert_scales || a->sort_expert_ids;
+    const uint32_t sort = a->expert_scales ? a->sort_expert_ids : 1;
+    const uint64_t nkeys = (uint64_t)R * E;
+    if (Lw.routes <= kFusedRoutes && R <= kFusedRows && nkeys <= kFusedKeys && nkeys * E <= kFusedCompares) {
+        hipLaunchKernelGGL(moe_route_compact, dim3(1), dim3(1024), nkeys * 8, stream, a->router_logits, R, E, A,
+                           a->round_weights_bf16, a->round_logits_bf16, a->expert_scales, (uint32_t)adjust, sort,
+                           Lw.max_slots, ids, weights, sorted, table, header);
+        QMM_HIP_CHECK(hipGetLastError());
+    } else {
+        st = stark_qmm_moe_route(a->router_logits, ids, weights, R, E, A, a->round_weights_bf16,
+                                 a->round_logits_bf16, stream);
+        if (st != STARK_QMM_OK) return st;
+        if (adjust) st = launch_moe_adjust(ids, weights, a->expert_scales, R, E, A, sort, stream);
+        if (st != STARK_QMM_OK) return st;
+        hipLaunchKernelGGL(moe_compact, dim3(1), dim3(1024), 0, stream, ids, Lw.routes, E, Lw.max_slots, sorted,
+                           table, header);
+        QMM_HIP_CHECK(hipGetLastError());
+    }
     // 3./4. grouped products, one launch per route-count class in use
     const bool sg = a->up.signed_codes != 0;
     const int top = (int)count_class(max_count);

@@ -124,6 +124,17 @@ def test_routed_experts_options(qmm, oracle, biased, gains, flags):
     routed_check(qmm, oracle, c, **flags)
 
 
+@pytest.mark.parametrize("rows,experts,flags", [(16, 128, {}), (9, 96, dict(si=True, rw=True)), (4, 128, {}),
+                                                (5, 128, dict(rl=True))])
+def test_routed_experts_route_paths(qmm, oracle, rows, experts, flags):
+    """Both routing paths: the one-workgroup route + compaction (rows * E^2 up
+    to 65536 compares) and the per-row route kernel with a separate compaction
+    above it (16 x 128, 9 x 96, 5 x 128)."""
+    c = MC.case(oracle, 300 + rows + experts, rows, model=256, hidden=128, experts=experts, active=8,
+                gains=bool(flags.get("si")))
+    routed_check(qmm, oracle, c, **flags)
+
+
 def test_routed_experts_qwen3_moe_geometry(qmm, oracle):
     """Config-3 widths (H=2048, I=768, E=128, top-8) at one token."""
     c = MC.case(oracle, 9, 1, model=2048, hidden=768, experts=128, active=8)
