@@ -2,10 +2,11 @@
 // crates/stark-engine/src/encodable_block/mlp/routed.rs:154-257) as one device
 // pipeline with expert compaction:
 //
-//   1. route (moe.hip) and, when asked, adjust the routes;
+//   1. route (moe.hip) and, when asked, adjust the routes (fused with 2. in one
+//      workgroup for small token counts);
 //   2. compaction (one workgroup): a counting sort of the routes by expert,
 //      cut into slots of at most 16 routes of one expert, each slot filed in a
-//      list by its route count class (1, 2, 3-4, 5-8, 9-16). The counting-sort
+//      list by its route count class (1-2 or 3-16). The counting-sort
 //      idea follows vendor/lily-core/src/kernels/metal/moe.metal:905-1036;
 //   3. grouped up product per class: every slot streams its expert's
 //      [value | gate] rows once for all its routes (matrix-core tile with the
@@ -30,12 +31,18 @@ namespace {
 
 using namespace mfma;
 
-constexpr uint32_t kSlotRoutes = 16;
-constexpr int kClasses = 5;
+constexpr uint32_t kSlotRoutes = 16;  // routes per slot (record capacity)
 
-__device__ __host__ inline uint32_t count_class(uint32_t c) {
-    return c <= 1 ? 0 : c <= 2 ? 1 : c <= 4 ? 2 : c <= 8 ? 3 : 4;
-}
+// Routes per slot of a call: 4 up to 16 tokens (a slot of 3-4 routes takes the
+// 4-row tile; an expert with more routes streams its rows once per slot, rare
+// at these counts), else 16.
+__device__ __host__ inline uint32_t slot_routes(uint32_t rows) { return rows <= 16 ? 4u : kSlotRoutes; }
+// Two route-count classes, one launch each: small slots (1-2 routes) and
+// large slots (3-16 routes); each launch takes the narrowest tile shape that
+// fits the largest slot its class can hold in this call.
+constexpr int kClasses = 2;
+
+__device__ __host__ inline uint32_t count_class(uint32_t c) { return c <= 2 ? 0 : 1; }
 
 // Workspace carve-up (byte offsets, 256-aligned).
 struct RoutedLayout {
@@ -50,7 +57,8 @@ RoutedLayout routed_layout(uint32_t rows, uint32_t model, uint32_t hidden, uint3
     RoutedLayout L{};
     const uint64_t routes = (uint64_t)rows * active;
     L.routes = (uint32_t)routes;
-    L.max_slots = (uint32_t)(std::min<uint64_t>(experts, routes) + (routes + kSlotRoutes - 1) / kSlotRoutes);
+    const uint32_t sr = slot_routes(rows);
+    L.max_slots = (uint32_t)(std::min<uint64_t>(experts, routes) + (routes + sr - 1) / sr);
     uint64_t off = 0;
     auto take = [&](uint64_t bytes) {
         const uint64_t at = off;
@@ -77,7 +85,7 @@ struct CompactLds {
 };
 
 __device__ __forceinline__ void compact_routes(const uint32_t* ids, uint32_t routes, uint32_t experts,
-                                               uint32_t max_slots, uint32_t* sorted, uint32_t* table,
+                                               uint32_t max_slots, uint32_t slot, uint32_t* sorted, uint32_t* table,
                                                uint32_t* header, CompactLds& s) {
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     s.cnt[t] = 0;
@@ -109,8 +117,8 @@ __device__ __forceinline__ void compact_routes(const uint32_t* ids, uint32_t rou
         sorted[s.off[e] + atomicAdd(&s.fill[e], 1u)] = r;
     }
     __syncthreads();  // sorted[] complete and visible to the workgroup
-    for (uint32_t s0 = 0; s0 < c; s0 += kSlotRoutes) {
-        const uint32_t n = min(kSlotRoutes, c - s0), cl = count_class(n);
+    for (uint32_t s0 = 0; s0 < c; s0 += slot) {
+        const uint32_t n = min(slot, c - s0), cl = count_class(n);
         uint32_t* rec = table + ((size_t)cl * max_slots + atomicAdd(&s.ccount[cl], 1u)) * kRecWords;
         rec[0] = t;
         rec[1] = n;
@@ -121,10 +129,10 @@ __device__ __forceinline__ void compact_routes(const uint32_t* ids, uint32_t rou
 }
 
 __global__ __launch_bounds__(1024) void moe_compact(const uint32_t* ids, uint32_t routes, uint32_t experts,
-                                                    uint32_t max_slots, uint32_t* sorted, uint32_t* table,
-                                                    uint32_t* header) {
+                                                    uint32_t max_slots, uint32_t slot, uint32_t* sorted,
+                                                    uint32_t* table, uint32_t* header) {
     __shared__ CompactLds s;
-    compact_routes(ids, routes, experts, max_slots, sorted, table, header, s);
+    compact_routes(ids, routes, experts, max_slots, slot, sorted, table, header, s);
 }
 
 // ---- 1+2 fused for up to kFusedRoutes routes: route, adjust and compaction in
@@ -255,7 +263,7 @@ __global__ __launch_bounds__(1024) void moe_route_compact(const float* logits, u
     }
     __syncthreads();
     // e.
-    compact_routes(rid, rows * active, experts, max_slots, sorted, table, header, s);
+    compact_routes(rid, rows * active, experts, max_slots, slot_routes(rows), sorted, table, header, s);
 }
 
 // Launch record of a grouped product, read through the kernarg segment.
@@ -367,25 +375,27 @@ void* pick(uint32_t gs, bool sg) {
     return sg ? K<MP, MB, 128, true, P1>::fn() : K<MP, MB, 128, false, P1>::fn();
 }
 
-// Kernel for a route-count class; the one- and two-route classes take a pass
-// length matched to K so that all four waves of a tile get work.
+// Kernel for a route-count class, given the largest route count of any slot
+// in this call; the one- and two-route shapes take a pass length matched to K
+// so that all four waves of a tile get work.
 template <template <int, int, int, bool, int> class K>
-void* pick_class(int cls, uint32_t gs, bool sg, uint32_t k) {
+void* pick_class(int cls, uint32_t max_count, uint32_t gs, bool sg, uint32_t k) {
     const bool short_k = k <= 1024;
-    switch (cls) {
-    case 0: return short_k ? pick<K, 1, 1, 1024>(gs, sg) : pick<K, 1, 1, 2048>(gs, sg);
-    case 1: return short_k ? pick<K, 2, 1, 1024>(gs, sg) : pick<K, 2, 1, 2048>(gs, sg);
-    case 2: return pick<K, 4, 1, 2048>(gs, sg);
-    case 3: return pick<K, 8, 1, 2048>(gs, sg);
-    default: return pick<K, 8, 2, 2048>(gs, sg);
+    if (cls == 0) {
+        if (max_count <= 1) return short_k ? pick<K, 1, 1, 1024>(gs, sg) : pick<K, 1, 1, 2048>(gs, sg);
+        return short_k ? pick<K, 2, 1, 1024>(gs, sg) : pick<K, 2, 1, 2048>(gs, sg);
     }
+    if (max_count <= 4) return pick<K, 4, 1, 2048>(gs, sg);
+    if (max_count <= 8) return pick<K, 8, 1, 2048>(gs, sg);
+    return pick<K, 8, 2, 2048>(gs, sg);
 }
 
 // Largest number of slots a class can hold: an expert receives at most one
-// route per token, and a slot of class c holds at least lo(c) routes.
+// route per token, so it has at most one small slot (the remainder after full
+// slots of 16), and a large slot holds at least 3 routes.
 uint32_t class_slot_bound(int cls, uint32_t routes, uint32_t experts, uint32_t max_slots) {
-    static const uint32_t lo[kClasses] = {1, 2, 3, 5, 9};
-    return std::min<uint32_t>(std::min<uint32_t>(max_slots, routes / lo[cls]), cls == 4 ? max_slots : experts);
+    if (cls == 0) return std::min<uint32_t>(std::min<uint32_t>(max_slots, routes), experts);
+    return std::min<uint32_t>(max_slots, routes / 3);
 }
 
 AffineOp bank_op(const stark_qmm_b& b, uint32_t rows, uint32_t k, const void* x) {
@@ -460,7 +470,7 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
     if (((uintptr_t)a->input | (uintptr_t)a->workspace) & 15) return STARK_QMM_UNSUPPORTED;
     const RoutedLayout Lw = routed_layout(R, model, H, E, A);
     if (a->workspace_size < Lw.total) return STARK_QMM_WORKSPACE_TOO_SMALL;
-    const uint32_t max_count = std::min<uint32_t>(R, kSlotRoutes);
+    const uint32_t max_count = std::min<uint32_t>(R, slot_routes(R));
     stark_qmm_status st = check_bank(a->up, (uint64_t)E * 2 * H, model, max_count);
     if (st != STARK_QMM_OK) return st;
     st = check_bank(a->down, (uint64_t)E * model, H, max_count);
@@ -493,7 +503,8 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
         if (st != STARK_QMM_OK) return st;
         if (adjust) st = launch_moe_adjust(ids, weights, a->expert_scales, R, E, A, sort, stream);
         if (st != STARK_QMM_OK) return st;
-        hipLaunchKernelGGL(moe_compact, dim3(1), dim3(1024), 0, stream, ids, Lw.routes, E, Lw.max_slots, sorted,
+        hipLaunchKernelGGL(moe_compact, dim3(1), dim3(1024), 0, stream, ids, Lw.routes, E, Lw.max_slots,
+                           slot_routes(R), sorted,
                            table, header);
         QMM_HIP_CHECK(hipGetLastError());
     }
@@ -516,8 +527,8 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
             const uint64_t items = (uint64_t)class_slot_bound(c, Lw.routes, E, Lw.max_slots) * g.tiles;
             if (items == 0) continue;
             const uint32_t grid = (uint32_t)std::min<uint64_t>(items, 4096);
-            void* fn = up ? pick_class<moe_up_mfma_k>(c, g.op.group_size, sg, model)
-                          : pick_class<moe_down_mfma_k>(c, g.op.group_size, sg, H);
+            void* fn = up ? pick_class<moe_up_mfma_k>(c, max_count, g.op.group_size, sg, model)
+                          : pick_class<moe_down_mfma_k>(c, max_count, g.op.group_size, sg, H);
             if (!fn) return STARK_QMM_UNSUPPORTED_GROUP_SIZE;
             void* argv[] = {&g};
             QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(grid), dim3(kWg), argv, 0, stream));
