@@ -325,6 +325,43 @@ def test_decode_stream_kernel_layer_set_against_oracle(qmm, oracle, bits):
         check(got, H.load(oracle, want, H.BF16), mag=mag, label=f"op {i} bits {bits}")
 
 
+@pytest.mark.parametrize("bits", [4])
+def test_decode_stream_kernel_many_tiles_repeated(qmm, oracle, bits):
+    """More 32-row tiles than the streaming kernel has workgroups (several
+    tiles per workgroup list, ops of two K), three launches in a row, outputs
+    pre-filled with NaN so that a tile no workgroup takes shows; a ragged last
+    tile in every op."""
+    rng = np.random.default_rng(77)
+    shapes = [(20000 + 8, 4096, 1), (4000 + 24, 8192, 0), (1000 + 16, 4096, 1)]
+    kern = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    ops = []
+    for n, k, layout in shapes:
+        W = H.affine_weights(oracle, rng, n, k, bits, 64, layout=layout)
+        x = H.activations(oracle, rng, 1, k)
+        st, want = oracle.matmul(a=x, m=1, n=n, k=k, codes=W["codes"], scales=W["scales"], correction=1,
+                                 correction_data=W["corr"], layout=layout, row_count=n, group_count=k // 64,
+                                 bits=bits, group_size=64, output_dt=H.BF16, threads=8)
+        assert st == 0
+        mag = H.dequant_magnitude(oracle, W["codes"], W["scales"], W["corr"], n, k, bits, 64, layout, 1, H.BF16,
+                                  x, H.BF16, 1, out_n=n)
+        ops.append((n, k, layout, W, x, want, mag))
+    for rep in range(3):
+        args = []
+        for n, k, layout, W, x, _, _ in ops:
+            d = torch_empty(n, H.BF16)
+            d.fill_(0x7FC0)  # bf16 NaN bits
+            args.append(qmm.MatmulArguments(
+                a=H.to_dev(x), m=1, n=n, k=k, d=d,
+                b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                                 params=qmm.QuantParams(layout, n, k // 64), mode=qmm.MODE_U4,
+                                 correction_data=H.to_dev(W["corr"]))))
+        kern.encode_many(args)
+        torch.cuda.synchronize()
+        for i, (a, (n, k, layout, W, x, want, mag)) in enumerate(zip(args, ops)):
+            got = H.load(oracle, H.from_dev(a.d, np.uint16), H.BF16)
+            check(got, H.load(oracle, want, H.BF16), mag=mag, label=f"launch {rep} op {i}")
+
+
 @pytest.mark.parametrize("n,k,gs", [(80, 4160, 32), (64, 8192 + 512, 64), (1040, 12288, 128), (3072, 1024, 64),
                                     (96, 96, 32)])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16])
