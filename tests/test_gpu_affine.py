@@ -415,7 +415,7 @@ def bf16_effective_reference(O, W, x, m, n, k, bits, gs, layout, correction, w_d
     return xf @ w.T, np.abs(xf) @ np.abs(w).T
 
 
-@pytest.mark.parametrize("m,n,k", [(17, 96, 512), (64, 256, 1024), (200, 300, 4096), (2048, 128, 256),
+@pytest.mark.parametrize("m,n,k", [(17, 96, 512), (64, 256, 1024), (200, 300, 4096), (2048, 128, 256), (520, 136, 320),
                                    (130, 1000, 192)])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_prefill_gemm_shapes(qmm, oracle, m, n, k, bits):
