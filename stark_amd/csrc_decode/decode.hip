@@ -392,7 +392,22 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint3
     const uint32_t t = threadIdx.x;
     float best = -INFINITY;
     uint32_t idx = 0xffffffffu;
-    for (uint32_t i = t; i < n; i += 1024) {
+    // 16-byte loads, eight in flight per thread; a thread sees its indices in
+    // increasing order, so the strict > keeps the lowest index of a tie
+    const uint32_t n4 = n / 4;
+    const float4* l4 = (const float4*)logits;
+#pragma unroll 8
+    for (uint32_t c = t; c < n4; c += 1024) {
+        const float4 v = l4[c];
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (e[q] > best) {
+                best = e[q];
+                idx = 4 * c + q;
+            }
+    }
+    for (uint32_t i = 4 * n4 + t; i < n; i += 1024) {
         const float v = logits[i];
         if (v > best) {
             best = v;

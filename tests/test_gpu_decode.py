@@ -182,6 +182,19 @@ def test_argmax_and_embed(D):
     pos.fill_(8)
     assert D.lib().stark_decode_argmax(_p(logits), n, _p(tok), _p(pos), _p(hist), 8, _s()) == 0
     assert pos.item() == 8
+    # ties inside one 16-byte chunk and across one thread's chunks, the last
+    # element; then a count with a tail past the last whole chunk (1027 values)
+    logits[777] = 0.0
+    logits[90000] = 0.0
+    for m, where in [(61.0, (4101, 4102)), (62.0, (8, 8 + 4096 * 4)), (63.0, (n - 1,))]:
+        for w in where:
+            logits[w] = m
+        assert D.lib().stark_decode_argmax(_p(logits), n, _p(tok), _p(pos), _p(hist), 8, _s()) == 0
+        assert tok.item() == where[0]
+    odd = torch.randn(1027, device="cuda")
+    odd[1026] = 99.0
+    assert D.lib().stark_decode_argmax(_p(odd), 1027, _p(tok), _p(pos), _p(hist), 8, _s()) == 0
+    assert tok.item() == 1026
     # all NaN: the token stays in range
     logits.fill_(float("nan"))
     assert D.lib().stark_decode_argmax(_p(logits), n, _p(tok), _p(pos), _p(hist), 8, _s()) == 0
