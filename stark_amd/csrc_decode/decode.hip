@@ -49,9 +49,11 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
     __shared__ float part[4];
     const uint32_t t = threadIdx.x, nv = n / 8;
     const uint4* xv = (const uint4*)x;
-    uint4 keep[kKeep];
+    uint4 keep[kKeep], wkeep[kKeep];  // the weights are loaded with x: one memory round trip
 #pragma unroll
     for (int j = 0; j < kKeep; ++j) keep[j] = t + j * 256 < nv ? xv[t + j * 256] : uint4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) wkeep[j] = t + j * 256 < nv ? ((const uint4*)w)[t + j * 256] : uint4{0, 0, 0, 0};
     float ss = 0.0f;
     const auto sq = [&](const uint4& u) {
         const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
@@ -68,8 +70,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
     if ((t & 63) == 0) part[t >> 6] = ss;
     __syncthreads();
     const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)n + eps);
-    const auto emit = [&](uint32_t i, const uint4& u) {
-        const uint4 wv = ((const uint4*)w)[i];
+    const auto emit = [&](uint32_t i, const uint4& u, const uint4& wv) {
         const uint32_t xd[4] = {u.x, u.y, u.z, u.w}, wd[4] = {wv.x, wv.y, wv.z, wv.w};
         uint32_t od[4];
 #pragma unroll
@@ -83,8 +84,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
     };
 #pragma unroll
     for (int j = 0; j < kKeep; ++j)
-        if (t + j * 256 < nv) emit(t + j * 256, keep[j]);
-    for (uint32_t i = t + kKeep * 256; i < nv; i += 256) emit(i, xv[i]);
+        if (t + j * 256 < nv) emit(t + j * 256, keep[j], wkeep[j]);
+    for (uint32_t i = t + kKeep * 256; i < nv; i += 256) emit(i, xv[i], ((const uint4*)w)[i]);
 }
 
 // Per-head RMSNorm of q and k, rotate-half RoPE at *pos, and the k/v write
@@ -213,6 +214,14 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
     __shared__ float fs[kMaxChunks];
     __shared__ float red[2];
     const uint32_t h = blockIdx.x, d = threadIdx.x;
+    // The first kPre chunks' partial outputs are loaded at once, before the
+    // position is known (chunks past it are loaded and not used): one memory
+    // round trip for contexts up to kPre * kChunk.
+    constexpr uint32_t kPre = 80;
+    const float* col = po + (size_t)h * nchunks * kHd + d;
+    float pre[kPre];
+#pragma unroll
+    for (uint32_t j = 0; j < kPre; ++j) pre[j] = j < nchunks ? col[(size_t)j * kHd] : 0.0f;
     const uint32_t len = min((uint32_t)*pos_ptr + 1, cap);
     const uint32_t nc = min(nchunks, (len + kChunk - 1) / kChunk);
     const float2* ml = (const float2*)pml + (size_t)h * nchunks;
@@ -234,9 +243,11 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
     if ((d & 63) == 0) red[d >> 6] = l;
     __syncthreads();
     l = red[0] + red[1];
-    const float* col = po + (size_t)h * nchunks * kHd + d;
     float o = 0.0f;
-    uint32_t c = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kPre; ++j)
+        if (j < nc) o = fmaf(pre[j], fs[j], o);
+    uint32_t c = kPre;
     for (; c + 8 <= nc; c += 8) {
         float v[8];
 #pragma unroll
