@@ -262,6 +262,11 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
 // Per-head RMSNorm + rotate-half RoPE of one head (128 values, lane owns dims
 // i and i + 64), the arithmetic of qk_norm_rope_kernel: returns the rotated
 // pair rounded to bf16.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 __device__ __forceinline__ void norm_rope_pair(float a, float b, const uint16_t* w, uint32_t i, int32_t pos,
                                                float theta, float eps, uint16_t& ra, uint16_t& rb) {
     const float inv = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)kHd + eps);
@@ -293,9 +298,9 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
                                                             uint32_t nchunks, float scale, float theta, float eps) {
     constexpr int kRowK = kHd / 2 + 4;
     constexpr int kVec = kChunk * kHd / 8;
-    __shared__ uint32_t ks[kChunk * kRowK];
+    __shared__ __attribute__((aligned(16))) uint32_t ks[kChunk * kRowK];
     __shared__ uint32_t vs[kChunk * kHd / 2];
-    __shared__ float qs[G][kHd];
+    __shared__ __attribute__((aligned(16))) uint16_t qs[G][kHd];  // the rotated query, bf16
     __shared__ float ws[G][kChunk];
     const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63, h = t >> 6;
     const int32_t pos = *pos_ptr;
@@ -321,8 +326,8 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
             const uint16_t* src = q + (size_t)(g * G + h) * kHd;
             uint16_t ra, rb;
             norm_rope_pair(bf(src[lane]), bf(src[lane + 64]), qw, lane, pos, theta, eps, ra, rb);
-            qs[h][lane] = bf(ra);
-            qs[h][lane + 64] = bf(rb);
+            qs[h][lane] = ra;
+            qs[h][lane + 64] = rb;
         }
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
@@ -353,19 +358,32 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
         }
     }
     __syncthreads();
+    // scores: lane = position, wave = head; bf16 pairs of K and of the query
+    // (bf16 values) on v_dot2_f32_bf16, f32 accumulation
     float s = -INFINITY;
-    if (lane < np) {
-        const uint32_t* kr = &ks[lane * kRowK];
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int d2 = 0; d2 < kHd / 2; d2 += 2) {
-            const uint2 u = *(const uint2*)&kr[d2];
-            acc = fmaf(qs[h][2 * d2], __uint_as_float(u.x << 16), acc);
-            acc = fmaf(qs[h][2 * d2 + 1], __uint_as_float(u.x & 0xffff0000u), acc);
-            acc = fmaf(qs[h][2 * d2 + 2], __uint_as_float(u.y << 16), acc);
-            acc = fmaf(qs[h][2 * d2 + 3], __uint_as_float(u.y & 0xffff0000u), acc);
+    {
+        uint32_t qp[kHd / 2];
+#pragma unroll
+        for (int i = 0; i < kHd / 8; ++i) {
+            const uint4 u = ((const uint4*)qs[h])[i];
+            qp[4 * i] = u.x;
+            qp[4 * i + 1] = u.y;
+            qp[4 * i + 2] = u.z;
+            qp[4 * i + 3] = u.w;
         }
-        s = acc * scale;
+        if (lane < np) {
+            const uint4* kr = (const uint4*)&ks[lane * kRowK];
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kHd / 8; ++i) {
+                const uint4 u = kr[i];
+                acc = dot2_bf16(u.x, qp[4 * i], acc);
+                acc = dot2_bf16(u.y, qp[4 * i + 1], acc);
+                acc = dot2_bf16(u.z, qp[4 * i + 2], acc);
+                acc = dot2_bf16(u.w, qp[4 * i + 3], acc);
+            }
+            s = acc * scale;
+        }
     }
     const float m = wave_max(s);
     const float e = lane < np ? __expf(s - m) : 0.0f;
