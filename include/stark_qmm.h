@@ -237,7 +237,11 @@ stark_qmm_status stark_qmm_moe_accumulate(const void* input, const float* weight
  * matvec with SiLU gating -> grouped down matvec -> weighted accumulation.
  * Banks flatten [experts, rows, cols] (routed.rs:1-5): up [E*2*hidden, model]
  * with rows [value(hidden) | gate(hidden)] per expert, down [E*model, hidden].
- * Both banks are 4- or 8-bit affine with BF16 scale/bias planes. */
+ * Both banks are 4-bit affine (group size 32, 64 or 128) with BF16 scale
+ * and bias planes, or symmetric; other banks return STARK_QMM_UNSUPPORTED or
+ * STARK_QMM_UNSUPPORTED_GROUP_SIZE. The workspace holds the routes, the
+ * compaction tables and the intermediate activations; its contents do not
+ * survive the call. */
 typedef struct stark_qmm_routed_args {
     uint32_t struct_size;
     const void* input;          /* [rows, model] bf16 */
