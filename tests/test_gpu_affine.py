@@ -218,6 +218,39 @@ def test_error_paths(qmm, oracle):
     assert e.value.status == qmm.UNSUPPORTED_DATA_TYPE
 
 
+def test_empty_products_are_no_ops(qmm, oracle):
+    """m = 0 or n = 0: the reference's loops run zero times and return Ok
+    (kernel.rs:168-285); nothing is written (the output keeps its bits), alone
+    and inside a batch with a real product."""
+    rng = np.random.default_rng(3)
+    W = H.affine_weights(oracle, rng, 64, 256)
+    x = H.to_dev(H.activations(oracle, rng, 2, 256))
+    k = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+
+    def args(m, n, d):
+        return qmm.MatmulArguments(
+            a=x, m=m, n=n, k=256, d=d,
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(0, 64, 4), correction_data=H.to_dev(W["corr"])))
+    for m, n in [(0, 64), (1, 0), (0, 0), (2, 0)]:
+        d = torch_empty(128, H.BF16)
+        d.fill_(0x1234)
+        k.encode(args(m, n, d))
+        torch.cuda.synchronize()
+        assert bool((d == 0x1234).all()), (m, n)
+    d0, d1 = torch_empty(64, H.BF16), torch_empty(64, H.BF16)
+    d0.fill_(0x1234)
+    k.encode_many([args(0, 64, d0), args(1, 64, d1)])
+    torch.cuda.synchronize()
+    assert bool((d0 == 0x1234).all())
+    st, want = oracle.matmul(a=H.from_dev(x, np.uint16)[:256], m=1, n=64, k=256, codes=W["codes"],
+                             scales=W["scales"], correction=1, correction_data=W["corr"], layout=0, row_count=64,
+                             group_count=4, bits=4, group_size=64, output_dt=H.BF16, threads=1)
+    assert st == 0
+    assert np.array_equal(H.from_dev(d1, np.uint16), want) or np.allclose(
+        H.load(oracle, H.from_dev(d1, np.uint16), H.BF16), H.load(oracle, want, H.BF16), rtol=2 ** -7, atol=1e-3)
+
+
 def test_encode_many_matches_single(qmm, oracle):
     """stark_qmm_encode_many: one launch for several independent products
     (the config-1 layer set at reduced N) equals one encode per product."""

@@ -73,6 +73,22 @@ def test_packed_q8_0_short_rows(qmm, oracle):
     _run_packed(qmm, oracle, 8, 33, 96, 2, seed=3)
 
 
+def test_empty_mapped_operations_are_rejected(qmm, oracle):
+    """parameters_for_input rejects zero rows or columns as invalid dimensions
+    (weight_metal.rs:456-466): INVALID_ARGUMENT, also next to a valid op."""
+    rng = np.random.default_rng(13)
+    blocks = _packed(oracle, rng, 8, 32, 256)
+    x = torch.from_numpy(rng.normal(0, 1, 256).astype(np.float32)).cuda()
+
+    def op(rows, columns):
+        return qmm.MappedOperation(matrices=[qmm.MappedMatrix(codes=H.to_dev(blocks.ravel()))], inputs=x,
+                                   rows=rows, columns=columns, format=("packed", 8))
+    for bad in (op(0, 256), op(32, 0)):
+        with pytest.raises(qmm.MatmulError) as e:
+            qmm.mapped_many([bad, op(32, 256)])
+        assert e.value.status == qmm.INVALID_ARGUMENT
+
+
 def test_packed_wide_range_inputs(qmm, oracle):
     """f32 activations far from bf16: the result must still hold the bar."""
     rng = np.random.default_rng(11)
