@@ -121,18 +121,13 @@ def test_mapped_many_validation_without_device():
     op[0].scale_dtype, op[0].bits, op[0].group = qmm.BF16, 4, 64
     outs = (C.c_void_p * 1)(0x5000)
 
-    def st(**kw):
-        saved = {k: getattr(op[0], k) for k in kw}
-        for k, v in kw.items():
-            setattr(op[0], k, v)
-        r = lib.stark_qmm_mapped_many_async(op, 1, outs, C.c_void_p(0x6000), None) if False else None
-        for k, v in saved.items():
-            setattr(op[0], k, v)
-        return r
-
-    # validation is reached before any launch only for invalid descriptors:
+    # validation is reached before any launch only for invalid descriptors;
+    # the size bounds are parameters_for_input's (weight_metal.rs:456-466)
+    big = 8_000_001
     for kw in ({"input_length": 63}, {"group": 16}, {"bits": 5}, {"scale_dtype": 9}, {"rows": 0},
-               {"columns": 0}, {"rows_per_batch": 3}, {"format": 7}):
+               {"columns": 0}, {"rows_per_batch": 3}, {"format": 7}, {"rows": big},
+               {"columns": big, "input_length": big}, {"input_length": big},
+               {"rows": 4_000_004, "matrix_count": 2, "input_length": 128}):
         saved = {k: getattr(op[0], k) for k in kw}
         for k, v in kw.items():
             setattr(op[0], k, v)
