@@ -3,6 +3,7 @@
 // mfma::TileEngine (mfma_tile.h). Reference semantics: MatmulCpuKernel::encode,
 // crates/stark-engine/src/backends/cpu/kernel/matmul/kernel.rs:168-285 (sum,
 // then ab_scale, accumulate, bias, soft-cap, output rounding).
+#include <algorithm>
 #include <map>
 #include <mutex>
 
@@ -161,6 +162,23 @@ bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* 
                 if (load[x + 8 * w] < load[x + 8 * best]) best = w;
             lists[x + 8 * best].push_back(et.first);
             load[x + 8 * best] += et.second;
+        }
+    }
+    // Streaming kernel (32-row tiles): within each XCD the lists with the most
+    // tiles go to the workgroups dispatched first. Workgroups dispatched late
+    // queue behind everyone's first loads; a list of one long tile (no tile
+    // switches) absorbs that best (measured: launch median 25.6 -> 24.3 us on
+    // the Qwen3-8B layer set).
+    if (rows == 32) {
+        for (uint32_t x = 0; x < 8; ++x) {
+            std::vector<uint32_t> idx(per_xcd);
+            for (uint32_t w = 0; w < per_xcd; ++w) idx[w] = w;
+            std::stable_sort(idx.begin(), idx.end(), [&](uint32_t a, uint32_t b) {
+                return lists[x + 8 * a].size() > lists[x + 8 * b].size();
+            });
+            std::vector<std::vector<uint32_t>> sorted_lists(per_xcd);
+            for (uint32_t w = 0; w < per_xcd; ++w) sorted_lists[w] = std::move(lists[x + 8 * idx[w]]);
+            for (uint32_t w = 0; w < per_xcd; ++w) lists[x + 8 * w] = std::move(sorted_lists[w]);
         }
     }
     std::vector<uint32_t> host(grid + 1);
