@@ -283,6 +283,44 @@ def config1(args, torch, Q):
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+    if args.verify:
+        verify_lines(args, torch, Q, gen, kern, layers, stream)
+
+
+def verify_lines(args, torch, Q, gen, kern, layers, stream):
+    """Config 1 at M = 2, 4, 8, 16 (speculative verify): the same layer set and
+    rotating copies, M activation rows per product (q/k/v and gate/up share
+    theirs), one line each (opt-in: the default run prints the M = 1 line only)."""
+    for m in (2, 4, 8, 16):
+        xs = {}
+        for name, n, k in SHAPES:
+            key = {"k_proj": "q_proj", "v_proj": "q_proj", "up_proj": "gate_proj"}.get(name, name)
+            if key not in xs:
+                xs[key] = torch.randn(m * k, generator=gen, device="cuda").to(torch.bfloat16)
+            xs[name] = xs[key]
+        outs = [torch.empty(m * n, dtype=torch.int16, device="cuda") for _, n, _ in SHAPES]
+        all_args = [kern.prepare_many([Q.MatmulArguments(
+            a=xs[name].view(torch.int16), m=m, n=mat["n"], k=mat["k"], d=out,
+            b=Q.QuantizedB(codes=mat["codes"], scales=mat["scales"],
+                           params=Q.QuantParams(Q.GROUP_OUTPUT, mat["n"], mat["k"] // GROUP),
+                           correction_data=mat["biases"]))
+            for (name, _, _), mat, out in zip(SHAPES, layer, outs)]) for layer in layers]
+        ms = timed(torch, lambda i: kern.encode_prepared(all_args[i % args.copies], stream), args.steps,
+                   args.warmup, stream)
+        nbytes = algorithmic_bytes(m)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": f"q4 matvec HBM GB/s at M={m} (speculative verify)", "value": round(gbs, 1),
+                          "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+                          "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic: the config-1 layer set, bf16 N(0,1) activations",
+                          "config": {"workload": f"config 1 verify: Qwen3-8B layer matvec set at M={m}, "
+                                                 f"{args.copies} rotating layer copies, one launch per step",
+                                     "bytes_per_step": nbytes,
+                                     "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+                                     "tokens_per_s": round(m * 1000.0 / ms, 1)},
+                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                       "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
 
 
 def timed(torch, step, steps, warmup, stream):
@@ -520,6 +558,8 @@ def main():
     ap.add_argument("--decode-tokens", type=int, default=256,
                     help="config 4: greedy tokens generated after the 4096-token context (0 skips the decode line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--verify", action="store_true",
+                    help="config 1: also print the M = 2, 4, 8, 16 (speculative verify) lines")
     ap.add_argument("--copies", type=int, default=LAYERS,
                     help="config 1: distinct layer-weight copies the steps rotate through (36 = one Qwen3-8B)")
     ap.add_argument("--calibrate-copy", action="store_true",
