@@ -1,0 +1,223 @@
+// Dense small-M form of the 4-bit MLX-affine product (speculative verify:
+// M = 9 .. 16 activation rows, group size 64, bf16 activations).
+//
+// Same arithmetic as the tile engine (mfma_tile.h): codes enter
+// v_mfma_f32_16x16x32_bf16 as raw bf16 bit patterns (p < 256 is p * 2^-133),
+// activations are staged as bf16 x * 2^64 (x * 2^60 where the code is the
+// high nibble, i.e. 16 q), and each group's scale and bias are applied once,
+// in f32: acc += s * 2^69 * C + bias_term * sum(x) (kernel.rs:219-265 per
+// element, regrouped). The layout differs: every MFMA takes all 16 activation
+// rows (A row = activation row, no group slots), covers 32 k of one group and
+// accumulates the group's two halves before its flush, and a workgroup runs
+// two 16-row weight tiles per pass under one activation stage (the A operand
+// serves both tiles). The slot form instead needs one MFMA per 8 activation
+// rows and re-stages the activations for every tile. At 8 rows or fewer the
+// slot form is faster (the dense form leaves half its A rows empty): measured
+// on the Qwen3-8B layer set, M = 16 1.0 -> 1.48 TB/s, M = 8 1.69 -> 1.53 TB/s.
+#include "mfma_tile.h"
+
+namespace qmm {
+
+namespace {
+
+using namespace mfma;
+
+constexpr int kSmPass = 1024;            // k per pass: 4 waves x 256
+constexpr int kSmQ = kSmPass / 4;        // k per wave per pass (4 groups)
+constexpr int kSmTiles = 2;              // 16-row tiles per workgroup pass
+constexpr int kSmRowB = kSmQ / 2 + 16;   // padded LDS row of a wave's codes (bytes)
+constexpr int kSmGroups = kSmPass / 64;  // groups per pass
+
+struct SmLds {
+    union {
+        u32x4 stage[kSmTiles][4][kRows * kSmRowB / 16];  // codes [tile][wave][row][kSmRowB bytes]
+        float red[kSmTiles][4][16][kRows];               // per-wave partial outputs, after the last pass
+    };
+    float2 pl[kSmTiles][kSmGroups][kRows];  // (scale * 2^69, bias term) [tile][group][row]
+    u32x4 xp[16][kSmPass / 8];              // activation rows, MFMA pair order, scaled
+    float xs[16][kSmGroups];                // per-group activation sums
+};
+
+template <bool SIGNED>
+__global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void qmv_small_m(AffineBatch batch) {
+    (void)batch;
+    __shared__ SmLds lds;
+    const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t oi = 0;
+    for (uint32_t i = 1; i < kb->count; ++i)
+        if (blockIdx.x >= kb->op[i].block_begin) oi = i;
+    const AffineOp& op = kb->op[oi];
+    const uint32_t N = op.n, K = op.k, M = op.m;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t j = lane & 15, kq = lane >> 4;
+    // tile tt covers rows n0[tt] .. +15 and writes those from t0 + 16 tt on; a
+    // tile past N moves back to end at N, so every row is written once
+    const uint32_t t0 = (blockIdx.x - op.block_begin) * kRows * kSmTiles;
+    uint32_t n0[kSmTiles];
+#pragma unroll
+    for (int tt = 0; tt < kSmTiles; ++tt) n0[tt] = min(t0 + kRows * tt, N - kRows);
+    const size_t row_bytes = K / 2;
+    const bool bf = op.w_dt == STARK_QMM_BF16, biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
+    const uint16_t* X = (const uint16_t*)op.x;
+
+    u32x4 wc[kSmTiles][2];  // codes: piece p = tid + 256 i of a tile's [16 rows][512 bytes]
+    u32x4 xv[8];            // activations: vector v = tid + 256 i is row v / 128, values 8 (v % 128)
+    uint32_t ps[kSmTiles], pb[kSmTiles];  // raw plane values of (group tid / 16, row tid % 16)
+    const auto load = [&](uint32_t kbase) {
+#pragma unroll
+        for (int tt = 0; tt < kSmTiles; ++tt) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t p = tid + 256 * i, r = p / 32, c = p % 32;
+                wc[tt][i] = __builtin_nontemporal_load(
+                    (const u32x4*)(op.codes + (size_t)(n0[tt] + r) * row_bytes + kbase / 2 + 16 * c));
+            }
+            const uint32_t g = tid / 16, r = tid % 16;
+            const size_t pi = (size_t)(n0[tt] + r) * op.os + (size_t)(kbase / 64 + g) * op.gs;
+            ps[tt] = ((const uint16_t*)op.scales)[pi];
+            pb[tt] = biased ? ((const uint16_t*)op.corr)[pi] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
+            xv[i] = m < M ? *(const u32x4*)(X + (size_t)m * K + kbase + 8 * c) : u32x4{0, 0, 0, 0};
+        }
+    };
+    const auto stage = [&]() {
+#pragma unroll
+        for (int tt = 0; tt < kSmTiles; ++tt) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t p = tid + 256 * i, r = p / 32, c = p % 32;
+                *(u32x4*)((uint8_t*)lds.stage[tt][c / 8] + r * kSmRowB + 16 * (c % 8)) = wc[tt][i];
+            }
+            const float sc = plane_f32(ps[tt], bf);
+            lds.pl[tt][tid / 16][tid % 16] = float2{sc * 0x1p69f, biased ? plane_f32(pb[tt], bf) : -8.0f * sc};
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
+            const u32x4 t = xv[i];
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f[2 * e] = __uint_as_float(t[e] << 16) * 0x1p64f;           // even values meet q
+                f[2 * e + 1] = __uint_as_float(t[e] & 0xffff0000u) * 0x1p60f;  // odd values meet 16 q
+            }
+            u32x4 pq;  // (x0,x4)(x1,x5)(x2,x6)(x3,x7), as the codes unpack
+            pq[0] = perm(__float_as_uint(f[4]), __float_as_uint(f[0]), 0x07060302u);
+            pq[1] = perm(__float_as_uint(f[5]), __float_as_uint(f[1]), 0x07060302u);
+            pq[2] = perm(__float_as_uint(f[6]), __float_as_uint(f[2]), 0x07060302u);
+            pq[3] = perm(__float_as_uint(f[7]), __float_as_uint(f[3]), 0x07060302u);
+            lds.xp[m][c] = pq;
+            float sm = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sm = dot2_bf16(t[e], 0x3F803F80u, sm);
+            sm += __shfl_xor(sm, 1, 64);  // the 8 vectors of a group sit in consecutive lanes
+            sm += __shfl_xor(sm, 2, 64);
+            sm += __shfl_xor(sm, 4, 64);
+            if ((c & 7) == 0) lds.xs[m][c / 8] = sm;
+        }
+    };
+
+    f32x4 acc[kSmTiles];
+#pragma unroll
+    for (int tt = 0; tt < kSmTiles; ++tt) acc[tt] = f32x4{0, 0, 0, 0};
+    // the wave's 256 k of a pass: 8 chunks of 32, two per group
+    const auto compute = [&]() {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 C[kSmTiles];
+#pragma unroll
+            for (int tt = 0; tt < kSmTiles; ++tt) C[tt] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int cc = 2 * g + h;
+                const u32x4 a = lds.xp[j][wave * 32 + 4 * cc + kq];  // A row j = activation row j
+#pragma unroll
+                for (int tt = 0; tt < kSmTiles; ++tt) {
+                    uint32_t u = *(const uint32_t*)((const uint8_t*)lds.stage[tt][wave] + j * kSmRowB + 16 * cc +
+                                                    4 * kq);
+                    if (SIGNED) u ^= 0x88888888u;
+                    const uint32_t u8 = u >> 8;
+                    const u32x4 bq{u & 0x000F000Fu, u & 0x00F000F0u, u8 & 0x000F000Fu, u8 & 0x00F000F0u};
+                    C[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                                  __builtin_bit_cast(bf16x8, bq), C[tt], 0, 0, 0);
+                }
+            }
+            // flush: lane (j, kq) holds activation rows 4kq .. 4kq+3 of tile row j
+            const uint32_t gp = wave * 4 + g;  // group within the pass
+            const f32x4 x4 = f32x4{lds.xs[4 * kq][gp], lds.xs[4 * kq + 1][gp], lds.xs[4 * kq + 2][gp],
+                                   lds.xs[4 * kq + 3][gp]};
+#pragma unroll
+            for (int tt = 0; tt < kSmTiles; ++tt) {
+                const float2 p = lds.pl[tt][gp][j];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[tt][q] = fmaf(p.x, C[tt][q], fmaf(p.y, x4[q], acc[tt][q]));
+            }
+        }
+    };
+
+    load(0);
+    for (uint32_t kbase = 0; kbase < K; kbase += kSmPass) {
+        if (kbase) __syncthreads();  // every wave finished the previous pass's LDS
+        stage();
+        __syncthreads();
+        if (kbase + kSmPass < K) load(kbase + kSmPass);
+        compute();
+    }
+    __syncthreads();  // the results overwrite the code stage
+#pragma unroll
+    for (int tt = 0; tt < kSmTiles; ++tt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds.red[tt][wave][4 * kq + q][j] = acc[tt][q];
+    __syncthreads();
+    for (uint32_t t = tid; t < (uint32_t)(kSmTiles * 16 * kRows); t += kWg) {
+        const uint32_t tt = t / (16 * kRows), m = (t / kRows) % 16, r = t % kRows;
+        const uint32_t n = n0[tt] + r;
+        if (m >= M || n < t0 + kRows * tt) continue;
+        const size_t o = (size_t)m * N + n;
+        float v = op.ab_scale * ((lds.red[tt][0][m][r] + lds.red[tt][1][m][r]) +
+                                 (lds.red[tt][2][m][r] + lds.red[tt][3][m][r]));
+        if (op.flags & FLAG_ACCUMULATE) v += load_as_f32(op.d, op.d_dt, o);
+        if (op.bias) v += load_as_f32(op.bias, op.w_dt, n);
+        if (op.flags & FLAG_SOFT_CAP) v = op.soft_cap * tanhf(v / op.soft_cap);
+        store_from_f32(op.d, op.d_dt, o, v);
+    }
+}
+
+}  // namespace
+
+bool small_m_eligible(const AffineOp* ops, uint32_t count) {
+    for (uint32_t i = 0; i < count; ++i) {
+        const AffineOp& o = ops[i];
+        if (o.m < 9 || o.m > 16 || o.group_size != 64 || o.k % kSmPass || o.n < (uint32_t)kRows || o.gather)
+            return false;
+        if (o.x_dt != STARK_QMM_BF16 || !(o.w_dt == STARK_QMM_BF16 || o.w_dt == STARK_QMM_F16)) return false;
+        if (!(o.corr_kind == STARK_QMM_CORRECTION_BIASES || o.corr_kind == STARK_QMM_CORRECTION_SYMMETRIC))
+            return false;
+        if (((uintptr_t)o.codes | (uintptr_t)o.x) & 15) return false;
+    }
+    return count > 0;
+}
+
+stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream) {
+    AffineBatch batch{};
+    uint32_t blocks = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        batch.op[i] = ops[i];
+        batch.op[i].block_begin = blocks;
+        blocks += (ops[i].n + kRows * kSmTiles - 1) / (kRows * kSmTiles);
+    }
+    batch.count = count;
+    if (blocks == 0) return STARK_QMM_OK;
+    if (signed_codes)
+        hipLaunchKernelGGL(qmv_small_m<true>, dim3(blocks), dim3(kWg), 0, stream, batch);
+    else
+        hipLaunchKernelGGL(qmv_small_m<false>, dim3(blocks), dim3(kWg), 0, stream, batch);
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
+
+}  // namespace qmm

@@ -406,6 +406,54 @@ def test_matrix_core_kernel_shapes(qmm, oracle, n, k, gs, m, layout):
     run_case(qmm, oracle, m=m, n=n, k=k, gs=gs, layout=layout, seed=n + k + m + 7 * layout)
 
 
+@pytest.mark.parametrize("n,k", [(16, 1024), (40, 4096), (1000, 2048), (96, 12288)])
+@pytest.mark.parametrize("m", [9, 12, 16])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_small_m_dense_kernel_shapes(qmm, oracle, n, k, m, layout):
+    """M = 9 .. 16, 4-bit, group 64, K % 1024 == 0 takes the dense small-M
+    kernel (all 16 activation rows per MFMA, two 16-row tiles per pass): one
+    tile, a pair with a shifted second tile, ragged N, long K."""
+    run_case(qmm, oracle, m=m, n=n, k=k, gs=64, layout=layout, seed=n + k + 3 * m + layout)
+
+
+@pytest.mark.parametrize("correction,signed,w_dt", [(0, False, H.BF16), (1, True, H.F16), (0, True, H.F16)])
+def test_small_m_dense_kernel_corrections(qmm, oracle, correction, signed, w_dt):
+    run_case(qmm, oracle, m=11, n=72, k=2048, gs=64, correction=correction, signed=signed, w_dt=w_dt,
+             seed=17 + correction + 2 * signed)
+
+
+def test_small_m_dense_kernel_d_ops(qmm, oracle):
+    run_case(qmm, oracle, m=16, n=40, k=1024, gs=64, ab_scale=0.75, accumulate=True, with_bias=True,
+             soft_cap=30.0, seed=5)
+
+
+def test_small_m_dense_kernel_batch_matches_single(qmm, oracle):
+    """Three dense-eligible ops (N = 48, 17, 64) in one launch give the bits
+    of three single launches (the op search by first block)."""
+    rng = np.random.default_rng(31)
+    k = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    specs = [(12, 48, 1024), (12, 17, 1024), (12, 64, 2048)]
+    made = []
+    for m, n, kk in specs:
+        W = H.affine_weights(oracle, rng, n, kk, 4, 64, layout=1)
+        x = H.to_dev(H.activations(oracle, rng, m, kk))
+        made.append((m, n, kk, W, x))
+
+    def args(m, n, kk, W, x):
+        return qmm.MatmulArguments(
+            a=x, m=m, n=n, k=kk, d=torch_empty(m * n, H.BF16),
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(1, n, kk // 64), correction_data=H.to_dev(W["corr"])))
+    many = [args(*t) for t in made]
+    k.encode_many(many)
+    single = [args(*t) for t in made]
+    for a in single:
+        k.encode(a)
+    torch.cuda.synchronize()
+    for a, b in zip(many, single):
+        assert torch.equal(a.d, b.d)
+
+
 @pytest.mark.parametrize("correction,signed", [(0, False), (1, True), (0, True)])
 @pytest.mark.parametrize("m", [1, 4, 16])
 def test_matrix_core_kernel_corrections(qmm, oracle, correction, signed, m):
