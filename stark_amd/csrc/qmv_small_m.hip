@@ -14,6 +14,10 @@
 // rows and re-stages the activations for every tile. At 8 rows or fewer the
 // slot form is faster (the dense form leaves half its A rows empty): measured
 // on the Qwen3-8B layer set, M = 16 1.0 -> 1.48 TB/s, M = 8 1.69 -> 1.53 TB/s.
+#include <algorithm>
+#include <type_traits>
+#include <vector>
+
 #include "mfma_tile.h"
 
 namespace qmm {
@@ -61,44 +65,48 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const bool bf = op.w_dt == STARK_QMM_BF16, biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     const uint16_t* X = (const uint16_t*)op.x;
 
-    u32x4 wc[kSmTiles][2];  // codes: piece p = tid + 256 i of a tile's [16 rows][512 bytes]
-    u32x4 xv[8];            // activations: vector v = tid + 256 i is row v / 128, values 8 (v % 128)
-    uint32_t ps[kSmTiles], pb[kSmTiles];  // raw plane values of (group tid / 16, row tid % 16)
-    const auto load = [&](uint32_t kbase) {
+    // two register buffers: a pass's loads are issued two passes before it is
+    // staged (the passes alternate between the buffers)
+    u32x4 wc[2][kSmTiles][2];  // codes: piece p = tid + 256 i of a tile's [16 rows][512 bytes]
+    u32x4 xv[2][8];            // activations: vector v = tid + 256 i is row v / 128, values 8 (v % 128)
+    uint32_t ps[2][kSmTiles], pb[2][kSmTiles];  // raw plane values of (group tid / 16, row tid % 16)
+    const auto load = [&](auto buf, uint32_t kbase) {
+        constexpr int B = decltype(buf)::value;
 #pragma unroll
         for (int tt = 0; tt < kSmTiles; ++tt) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const uint32_t p = tid + 256 * i, r = p / 32, c = p % 32;
-                wc[tt][i] = __builtin_nontemporal_load(
+                wc[B][tt][i] = __builtin_nontemporal_load(
                     (const u32x4*)(op.codes + (size_t)(n0[tt] + r) * row_bytes + kbase / 2 + 16 * c));
             }
             const uint32_t g = tid / 16, r = tid % 16;
             const size_t pi = (size_t)(n0[tt] + r) * op.os + (size_t)(kbase / 64 + g) * op.gs;
-            ps[tt] = ((const uint16_t*)op.scales)[pi];
-            pb[tt] = biased ? ((const uint16_t*)op.corr)[pi] : 0u;
+            ps[B][tt] = ((const uint16_t*)op.scales)[pi];
+            pb[B][tt] = biased ? ((const uint16_t*)op.corr)[pi] : 0u;
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
-            xv[i] = m < M ? *(const u32x4*)(X + (size_t)m * K + kbase + 8 * c) : u32x4{0, 0, 0, 0};
+            xv[B][i] = m < M ? *(const u32x4*)(X + (size_t)m * K + kbase + 8 * c) : u32x4{0, 0, 0, 0};
         }
     };
-    const auto stage = [&]() {
+    const auto stage = [&](auto buf) {
+        constexpr int B = decltype(buf)::value;
 #pragma unroll
         for (int tt = 0; tt < kSmTiles; ++tt) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const uint32_t p = tid + 256 * i, r = p / 32, c = p % 32;
-                *(u32x4*)((uint8_t*)lds.stage[tt][c / 8] + r * kSmRowB + 16 * (c % 8)) = wc[tt][i];
+                *(u32x4*)((uint8_t*)lds.stage[tt][c / 8] + r * kSmRowB + 16 * (c % 8)) = wc[B][tt][i];
             }
-            const float sc = plane_f32(ps[tt], bf);
-            lds.pl[tt][tid / 16][tid % 16] = float2{sc * 0x1p69f, biased ? plane_f32(pb[tt], bf) : -8.0f * sc};
+            const float sc = plane_f32(ps[B][tt], bf);
+            lds.pl[tt][tid / 16][tid % 16] = float2{sc * 0x1p69f, biased ? plane_f32(pb[B][tt], bf) : -8.0f * sc};
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
-            const u32x4 t = xv[i];
+            const u32x4 t = xv[B][i];
             float f[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -159,13 +167,20 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         }
     };
 
-    load(0);
-    for (uint32_t kbase = 0; kbase < K; kbase += kSmPass) {
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    const auto pass = [&](auto buf, uint32_t kbase) {
         if (kbase) __syncthreads();  // every wave finished the previous pass's LDS
-        stage();
+        stage(buf);
         __syncthreads();
-        if (kbase + kSmPass < K) load(kbase + kSmPass);
+        if (kbase + 2 * kSmPass < K) load(buf, kbase + 2 * kSmPass);
         compute();
+    };
+    load(B0{}, 0);
+    if (kSmPass < K) load(B1{}, kSmPass);
+    for (uint32_t kbase = 0; kbase < K; kbase += 2 * kSmPass) {
+        pass(B0{}, kbase);
+        if (kbase + kSmPass < K) pass(B1{}, kbase + kSmPass);
     }
     __syncthreads();  // the results overwrite the code stage
 #pragma unroll
@@ -203,12 +218,16 @@ bool small_m_eligible(const AffineOp* ops, uint32_t count) {
 }
 
 stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream) {
+    // longest K first: the workgroups with the most passes are dispatched first
+    // instead of forming the tail of the launch
+    std::vector<AffineOp> sorted(ops, ops + count);
+    std::stable_sort(sorted.begin(), sorted.end(), [](const AffineOp& a, const AffineOp& b) { return a.k > b.k; });
     AffineBatch batch{};
     uint32_t blocks = 0;
     for (uint32_t i = 0; i < count; ++i) {
-        batch.op[i] = ops[i];
+        batch.op[i] = sorted[i];
         batch.op[i].block_begin = blocks;
-        blocks += (ops[i].n + kRows * kSmTiles - 1) / (kRows * kSmTiles);
+        blocks += (sorted[i].n + kRows * kSmTiles - 1) / (kRows * kSmTiles);
     }
     batch.count = count;
     if (blocks == 0) return STARK_QMM_OK;
