@@ -1,5 +1,5 @@
 // Dense small-M form of the 4-bit MLX-affine product (speculative verify:
-// M = 9 .. 16 activation rows, group size 64, bf16 activations).
+// M = 5 .. 16 activation rows, group size 64, bf16 activations).
 //
 // Same arithmetic as the tile engine (mfma_tile.h): codes enter
 // v_mfma_f32_16x16x32_bf16 as raw bf16 bit patterns (p < 256 is p * 2^-133),
@@ -11,9 +11,9 @@
 // accumulates the group's two halves before its flush, and a workgroup runs
 // two 16-row weight tiles per pass under one activation stage (the A operand
 // serves both tiles). The slot form instead needs one MFMA per 8 activation
-// rows and re-stages the activations for every tile. At 8 rows or fewer the
-// slot form is faster (the dense form leaves half its A rows empty): measured
-// on the Qwen3-8B layer set, M = 16 1.0 -> 1.48 TB/s, M = 8 1.69 -> 1.53 TB/s.
+// rows and re-stages the activations for every tile. Measured on the Qwen3-8B
+// layer set against the slot form: M = 16 1.0 -> 1.94 TB/s, M = 8 1.69 ->
+// 2.02 TB/s (at 8 rows half the A rows are empty and it still wins).
 #include <algorithm>
 #include <type_traits>
 #include <vector>
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
 bool small_m_eligible(const AffineOp* ops, uint32_t count) {
     for (uint32_t i = 0; i < count; ++i) {
         const AffineOp& o = ops[i];
-        if (o.m < 9 || o.m > 16 || o.group_size != 64 || o.k % kSmPass || o.n < (uint32_t)kRows || o.gather)
+        if (o.m < 5 || o.m > 16 || o.group_size != 64 || o.k % kSmPass || o.n < (uint32_t)kRows || o.gather)
             return false;
         if (o.x_dt != STARK_QMM_BF16 || !(o.w_dt == STARK_QMM_BF16 || o.w_dt == STARK_QMM_F16)) return false;
         if (!(o.corr_kind == STARK_QMM_CORRECTION_BIASES || o.corr_kind == STARK_QMM_CORRECTION_SYMMETRIC))
