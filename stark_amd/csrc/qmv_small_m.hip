@@ -106,6 +106,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
+            if (m >= M) continue;  // rows past M stay zero (cleared once); a row's 8-lane groups agree
             const u32x4 t = xv[B][i];
             float f[8];
 #pragma unroll
@@ -178,6 +179,13 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     };
     load(B0{}, 0);
     if (kSmPass < K) load(B1{}, kSmPass);
+    // activation rows past M: zero once (their products and sums are zero)
+    for (uint32_t v = tid; v < 16 * (kSmPass / 8); v += kWg) {
+        const uint32_t m = v / (kSmPass / 8);
+        if (m >= M) lds.xp[m][v % (kSmPass / 8)] = u32x4{0, 0, 0, 0};
+    }
+    for (uint32_t v = tid; v < 16 * kSmGroups; v += kWg)
+        if (v / kSmGroups >= M) lds.xs[v / kSmGroups][v % kSmGroups] = 0.0f;
     for (uint32_t kbase = 0; kbase < K; kbase += 2 * kSmPass) {
         pass(B0{}, kbase);
         if (kbase + kSmPass < K) pass(B1{}, kbase + kSmPass);
