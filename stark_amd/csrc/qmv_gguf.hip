@@ -30,6 +30,7 @@
 // realigned with v_alignbyte). Block headers are decoded to per-group f32
 // scale and bias in LDS once per pass. The next pass's loads are issued as
 // soon as the current pass sits in LDS.
+#include <algorithm>
 #include "mfma_tile.h"
 
 namespace qmm {
@@ -538,13 +539,16 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(MB >= 4 ? 2
 
 template <int KIND, int MP, int MB>
 stark_qmm_status launch_mfma(const GgufOp* ops, uint32_t count, uint32_t* status, hipStream_t stream) {
+    // longest K first: the workgroups with the most passes are dispatched first
+    std::vector<GgufOp> sorted(ops, ops + count);
+    std::stable_sort(sorted.begin(), sorted.end(), [](const GgufOp& a, const GgufOp& b) { return a.k > b.k; });
     GgufBatch batch{};
     batch.status = status;
     uint32_t blocks = 0;
     for (uint32_t i = 0; i < count; ++i) {
-        batch.op[i] = ops[i];
+        batch.op[i] = sorted[i];
         batch.op[i].block_begin = blocks;
-        blocks += (ops[i].n + kRows * GGeo<KIND, MP, MB>::TPW - 1) / (kRows * GGeo<KIND, MP, MB>::TPW);
+        blocks += (sorted[i].n + kRows * GGeo<KIND, MP, MB>::TPW - 1) / (kRows * GGeo<KIND, MP, MB>::TPW);
     }
     batch.count = count;
     if (blocks) hipLaunchKernelGGL((gguf_mfma<KIND, MP, MB>), dim3(blocks), dim3(kWg), 0, stream, batch);

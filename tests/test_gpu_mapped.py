@@ -64,6 +64,29 @@ def test_packed_small_m_ragged(qmm, oracle, kind, n, k, m):
 
 
 @pytest.mark.parametrize("kind", [8, 12])
+def test_packed_batch_of_mixed_k(qmm, oracle, kind):
+    """One mapped_many call with products of different K and M (the launch
+    orders them longest K first; every output goes to its own operation)."""
+    rng = np.random.default_rng(41 + kind)
+    specs = [(96, 1024, 1), (64, 4096, 1), (48, 2048, 6), (80, 4096, 6)]
+    ops, wants = [], []
+    for n, k, m in specs:
+        blocks = _packed(oracle, rng, kind, n, k)
+        x = rng.normal(0, 1, (m, k)).astype(np.float32)
+        ops.append(qmm.MappedOperation(matrices=[qmm.MappedMatrix(codes=H.to_dev(blocks.ravel()))] * m,
+                                       inputs=torch.from_numpy(x.ravel()).cuda(), rows=n, columns=k,
+                                       format=("packed", kind)))
+        dec = oracle.decode_rows(kind, blocks, n, k)
+        wants.append([(oracle.hybrid_packed_matvec(kind, blocks, n, k, x[i]), np.abs(dec) @ np.abs(x[i]))
+                      for i in range(m)])
+    outs = qmm.mapped_many(ops)
+    for (n, k, m), out, want in zip(specs, outs, wants):
+        got = out.cpu().numpy().reshape(m, n)
+        for i in range(m):
+            check(got[i], want[i][0], mag=want[i][1], label=f"n{n} k{k} m{m} row{i}")
+
+
+@pytest.mark.parametrize("kind", [8, 12])
 def test_packed_bf16_exact_inputs(qmm, oracle, kind):
     _run_packed(qmm, oracle, kind, 256, 4096, 1, seed=5 + kind, xkind="bf16")
 
