@@ -539,6 +539,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(MB >= 4 ? 2
 
 template <int KIND, int MP, int MB>
 stark_qmm_status launch_mfma(const GgufOp* ops, uint32_t count, uint32_t* status, hipStream_t stream) {
+    if (count > (uint32_t)kMaxBatchOps) return STARK_QMM_INVALID_ARGUMENT;  // the batch holds kMaxBatchOps
     // longest K first: the workgroups with the most passes are dispatched first
     std::vector<GgufOp> sorted(ops, ops + count);
     std::stable_sort(sorted.begin(), sorted.end(), [](const GgufOp& a, const GgufOp& b) { return a.k > b.k; });

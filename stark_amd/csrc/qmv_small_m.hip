@@ -226,6 +226,7 @@ bool small_m_eligible(const AffineOp* ops, uint32_t count) {
 }
 
 stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream) {
+    if (count > (uint32_t)kMaxBatchOps) return STARK_QMM_INVALID_ARGUMENT;  // the batch holds kMaxBatchOps
     // longest K first: the workgroups with the most passes are dispatched first
     // instead of forming the tail of the launch
     std::vector<AffineOp> sorted(ops, ops + count);
