@@ -117,7 +117,9 @@ struct GGeo {
     static constexpr int GPS = kStep / GS;             // 4 groups per step
     static_assert(S >= GPS, "slots");
     static constexpr int PERIOD = S / GPS;
-    static constexpr int PASS = MR <= 4 ? 2048 : 1024;  // k values per pass
+    // k values per pass; Q8_0 at M = 1 takes 1024 (four passes at K = 4096,
+    // so less of the last pass's compute trails the loads: +5%; Q4_K lost 10%)
+    static constexpr int PASS = (MR <= 2 && KIND == 8) ? 1024 : MR <= 4 ? 2048 : 1024;
     static constexpr int Q = PASS / 4;                  // per wave
     static constexpr int BPW = Q / BE;                  // blocks per wave per pass
     static constexpr int SEGB = BPW * BB;               // bytes of a row per wave per pass
