@@ -12,7 +12,15 @@
  * borrowed for the duration of the (stream-ordered) call. The library never
  * frees caller memory. `stream` is a hipStream_t passed as void* (NULL = the
  * default stream). Work is asynchronous on that stream unless an entry point
- * says otherwise.
+ * says otherwise. No entry point allocates device memory or waits for the
+ * device on its stream-ordered path, with these documented exceptions:
+ * stark_qmm_mapped_many (synchronous, as the reference; one 256-byte status
+ * word per device on first use), and the matvec schedule store: the first
+ * call on a new shape set enqueues small upload launches on the caller's
+ * stream into a fixed 4 MiB device array per GPU (no allocation); when that
+ * array is full, an eager call synchronizes the device once and drops the
+ * schedules no captured graph references (a capturing call returns
+ * STARK_QMM_OUT_OF_MEMORY instead). Calls are capture-safe (hipStreamBeginCapture).
  *
  * Threading: a handle is not reentrant (the reference keeps each kernel object
  * behind a Mutex, src/encodable_block/linear/matmul.rs:42); distinct handles
@@ -29,6 +37,13 @@ extern "C" {
 #endif
 
 #define STARK_QMM_ABI_VERSION 1u
+
+/* The library is built with hidden visibility; only these entry points are exported. */
+#if defined(__GNUC__)
+#define STARK_QMM_API __attribute__((visibility("default")))
+#else
+#define STARK_QMM_API
+#endif
 
 typedef uint32_t stark_qmm_status;
 enum {
@@ -129,31 +144,31 @@ typedef struct stark_qmm_args {
 
 /* Replaces MatmulKernel::new (kernel.rs:18-23; CPU twin
  * src/backends/cpu/kernel/matmul/kernel.rs:31-56): F32/F16/BF16 only. */
-stark_qmm_status stark_qmm_create(uint32_t weights_dtype, uint32_t input_dtype, uint32_t output_dtype,
+STARK_QMM_API stark_qmm_status stark_qmm_create(uint32_t weights_dtype, uint32_t input_dtype, uint32_t output_dtype,
                                   stark_qmm_kernel** out);
 
 /* Replaces MatmulKernel::encode (kernel.rs:51-62; Metal dispatch
  * src/backends/metal/kernel/matmul/mod.rs:551-613). Chooses the GEMV/verify
  * path for M <= 16 and the MFMA dequant-GEMM for larger M. */
-stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kernel, const stark_qmm_args* args, void* stream);
+STARK_QMM_API stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kernel, const stark_qmm_args* args, void* stream);
 
 /* Independent products with one submission, in the manner of the hybrid
  * engine's Weights::matvec_many (src/engine/hybrid/weights.rs:1323-1388): every
  * args[i] is validated as stark_qmm_encode would, then all eligible GEMV
  * products share one launch per (bits, M class). Outputs must not alias inputs
  * of other entries. */
-stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kernel, const stark_qmm_args* args, uint32_t count,
+STARK_QMM_API stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kernel, const stark_qmm_args* args, uint32_t count,
                                        void* stream);
 
 /* Replaces MatmulKernel::set_reference_accumulation (kernel.rs:34-37): when
  * enabled, every M uses the GEMV/verify kernels (f32 dequant semantics). */
-stark_qmm_status stark_qmm_set_reference_accumulation(stark_qmm_kernel* kernel, uint32_t enabled);
+STARK_QMM_API stark_qmm_status stark_qmm_set_reference_accumulation(stark_qmm_kernel* kernel, uint32_t enabled);
 
-void stark_qmm_destroy(stark_qmm_kernel* kernel);
+STARK_QMM_API void stark_qmm_destroy(stark_qmm_kernel* kernel);
 
-uint32_t stark_qmm_abi_version(void);
+STARK_QMM_API uint32_t stark_qmm_abi_version(void);
 /* Text for a status code; never NULL. */
-const char* stark_qmm_status_string(stark_qmm_status status);
+STARK_QMM_API const char* stark_qmm_status_string(stark_qmm_status status);
 
 /* ------------------------------------------------------------------ */
 /* Hybrid engine operator: weight_metal::mapped_many                   */
@@ -188,20 +203,21 @@ typedef struct stark_qmm_mapped_op {
     uint32_t group;         /* affine: 32, 64 or 128 */
 } stark_qmm_mapped_op;
 
-/* Replaces mapped_many (weight_metal.rs:539-545): validates every operation as
+/* Replaces mapped_many (weight_metal.rs:539-545). Thread-safe: concurrent calls on one
+ * device serialize on that device's status word. Validates every operation as
  * parameters_for_input does (weight_metal.rs:442-537; at most 64 ops), runs all
  * of them in one launch per format, and -- like the reference -- returns only
  * after the work completes. A non-finite input makes the call return
  * STARK_QMM_INVALID_ARGUMENT (weight_metal.rs:435-440); outputs are then
  * unspecified. outputs[i] is a device pointer with room for
  * matrix_count * rows floats. */
-stark_qmm_status stark_qmm_mapped_many(const stark_qmm_mapped_op* ops, uint32_t op_count, float* const* outputs,
+STARK_QMM_API stark_qmm_status stark_qmm_mapped_many(const stark_qmm_mapped_op* ops, uint32_t op_count, float* const* outputs,
                                        void* stream);
 
 /* Asynchronous form of stark_qmm_mapped_many: no host wait. The finite check
  * ORs 1 into *status_word (device u32, caller-zeroed) when any input is not
  * finite. */
-stark_qmm_status stark_qmm_mapped_many_async(const stark_qmm_mapped_op* ops, uint32_t op_count,
+STARK_QMM_API stark_qmm_status stark_qmm_mapped_many_async(const stark_qmm_mapped_op* ops, uint32_t op_count,
                                              float* const* outputs, uint32_t* status_word, void* stream);
 
 /* ------------------------------------------------------------------ */
@@ -211,21 +227,21 @@ stark_qmm_status stark_qmm_mapped_many_async(const stark_qmm_mapped_op* ops, uin
 
 /* MoeRoute (moe.rs:23-85, moe.metal:13-50): softmax over experts, repeated
  * argmax top-k (ties to the lowest id), renormalised weights. */
-stark_qmm_status stark_qmm_moe_route(const float* logits, uint32_t* ids, float* weights, uint32_t rows,
+STARK_QMM_API stark_qmm_status stark_qmm_moe_route(const float* logits, uint32_t* ids, float* weights, uint32_t rows,
                                      uint32_t experts, uint32_t active, uint32_t round_weights,
                                      uint32_t round_logits, void* stream);
 
 /* MoeAdjustRoutes (moe.rs:147-184, moe.metal:88-104). */
-stark_qmm_status stark_qmm_moe_adjust_routes(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
+STARK_QMM_API stark_qmm_status stark_qmm_moe_adjust_routes(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
                                              uint32_t experts, uint32_t active, uint32_t sort_ids, void* stream);
 
 /* MoeGatherRows (moe.rs:87-107, moe.metal:52-63). */
-stark_qmm_status stark_qmm_moe_gather_rows(const uint32_t* ids, uint32_t* indices, uint32_t route_offset,
+STARK_QMM_API stark_qmm_status stark_qmm_moe_gather_rows(const uint32_t* ids, uint32_t* indices, uint32_t route_offset,
                                            uint32_t rows_per_expert, uint32_t experts, uint32_t length,
                                            void* stream);
 
 /* MoeAccumulate (moe.rs:109-145, moe.metal:65-86). input/output are bf16. */
-stark_qmm_status stark_qmm_moe_accumulate(const void* input, const float* weights, float* accumulator,
+STARK_QMM_API stark_qmm_status stark_qmm_moe_accumulate(const void* input, const float* weights, float* accumulator,
                                           void* output, uint32_t length, uint32_t weight_offset,
                                           uint32_t output_offset, uint32_t initialize, uint32_t finalize,
                                           uint32_t round_product, uint32_t round_accumulator, void* stream);
@@ -256,9 +272,9 @@ typedef struct stark_qmm_routed_args {
     uint64_t workspace_size;
 } stark_qmm_routed_args;
 
-uint64_t stark_qmm_routed_experts_workspace_size(uint32_t rows, uint32_t model, uint32_t hidden, uint32_t experts,
+STARK_QMM_API uint64_t stark_qmm_routed_experts_workspace_size(uint32_t rows, uint32_t model, uint32_t hidden, uint32_t experts,
                                                  uint32_t active);
-stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* args, void* stream);
+STARK_QMM_API stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -29,16 +29,18 @@ FLAGS = [
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    # the drop-in library exports only the entry points its header marks STARK_QMM_API
+    extra = ["-fvisibility=hidden", "-fvisibility-inlines-hidden"] if os.path.dirname(src) == CSRC else []
+    cmd = [HIPCC, *FLAGS, *extra, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
     return obj
 
 
-def _link(objs, lib):
+def _link(objs, lib, extra=()):
     tmp = lib + ".tmp"
-    r = subprocess.run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp],
+    r = subprocess.run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, *extra, "-o", tmp],
                        capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
@@ -53,7 +55,7 @@ def build(jobs: int = 8) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(jobs, len(sources) + len(decode_sources))) as ex:
         objs = list(ex.map(_compile, sources + decode_sources))
     _link(objs[len(sources):], DECODE_LIB)
-    return _link(objs[:len(sources)], LIB)
+    return _link(objs[:len(sources)], LIB, [f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}"])
 
 
 if __name__ == "__main__":

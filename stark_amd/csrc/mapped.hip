@@ -173,18 +173,17 @@ void expand(const stark_qmm_mapped_op& op, float* out, std::vector<AffineOp>* af
     }
 }
 
-uint32_t* status_word_device() {
-    static std::mutex mu;
-    static uint32_t* words[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> g(mu);
-    if (!words[dev]) {
-        void* p = nullptr;
-        if (hipMalloc(&p, 256) != hipSuccess) return nullptr;
-        words[dev] = (uint32_t*)p;
-    }
-    return words[dev];
+// Status word of the synchronous form, one per device. The whole synchronous
+// call (zero, launches, wait, read) holds the device's lock, so concurrent
+// callers on different streams never share a word in flight.
+struct SyncWord {
+    std::mutex mu;
+    uint32_t* word = nullptr;
+};
+
+SyncWord* sync_word(int dev) {
+    static SyncWord words[64];
+    return dev >= 0 && dev < 64 ? &words[dev] : nullptr;
 }
 
 stark_qmm_status run(const stark_qmm_mapped_op* ops, uint32_t count, float* const* outputs, uint32_t* status,
@@ -245,8 +244,17 @@ stark_qmm_status stark_qmm_mapped_many_async(const stark_qmm_mapped_op* ops, uin
 stark_qmm_status stark_qmm_mapped_many(const stark_qmm_mapped_op* ops, uint32_t count, float* const* outputs,
                                        void* stream_ptr) {
     hipStream_t stream = (hipStream_t)stream_ptr;
-    uint32_t* word = status_word_device();
-    if (!word) return STARK_QMM_DEVICE_FAILURE;
+    int dev = 0;
+    QMM_HIP_CHECK(hipGetDevice(&dev));
+    SyncWord* sw = sync_word(dev);
+    if (!sw) return STARK_QMM_DEVICE_FAILURE;
+    std::lock_guard<std::mutex> hold(sw->mu);
+    if (!sw->word) {
+        void* p = nullptr;
+        QMM_HIP_CHECK(hipMalloc(&p, 256));
+        sw->word = (uint32_t*)p;
+    }
+    uint32_t* word = sw->word;
     hipLaunchKernelGGL(zero_word_kernel, dim3(1), dim3(1), 0, stream, word);
     QMM_HIP_CHECK(hipGetLastError());
     stark_qmm_status st = run(ops, count, outputs, word, stream);

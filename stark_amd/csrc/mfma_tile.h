@@ -9,9 +9,10 @@
 // bit patterns: a pattern p < 256 (exponent field 0 or 1) is exactly
 // p * 2^-133, so a code needs only a mask to become an operand (4-bit: the odd
 // nibble is left at bit 4, i.e. 16q, and its activation is scaled by 2^-4).
-// The activations are staged as bf16 x * 2^64 (exact), which puts the products
-// x*q*2^-69 in f32's normal range; the flush multiplies by s * 2^69. Products
-// are exact and accumulate in f32.
+// The activations are staged as bf16 x * 2^E (exact) with a per-group exponent
+// E (group_shift, qmm_common.h), which puts the products x*q*2^(E-133) in f32's
+// normal range for every finite x; the flush brings a group's sum back with
+// ldexp by 133 - E and multiplies by s. Products are exact and accumulate in f32.
 //
 // MFMA roles: B columns are the 16 weight rows of the tile; A rows are
 // (activation row, group slot) pairs -- A holds x where the k position's group
@@ -39,6 +40,7 @@ namespace mfma {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWg = 256;
 constexpr int kRows = 16;   // tile rows (MFMA B columns)
@@ -97,6 +99,7 @@ struct MfmaLds {
     uint16_t bi[G::GPP + G::S][kRows];        // raw bias plane
     u32x4 xp[G::MR][G::XK / 8];               // activation pairs per 8 values, in MFMA k order
     float xs[G::MR][G::XK / GS + G::S];       // activation sum per group
+    alignas(16) int xe[G::MR][G::XK / GS + G::S];  // 133 - E per group (activations staged as x * 2^E)
     float red[4][G::MR][kRows];               // per-wave partial outputs
     u32x4 zero[4];
 };
@@ -228,11 +231,17 @@ struct TileEngine {
             for (int i = 0; i < XI; ++i) {
                 const uint32_t v = tid + i * kWg, m = v / (XK / 8), vi = v % (XK / 8);
                 const u32x4 t = xv[i];
+                // the group's exponent: its GS/8 vectors sit in consecutive lanes
+                uint32_t fx = bf16x8_exp_max(t);
+#pragma unroll
+                for (int o = 1; o < GS / 8; o <<= 1) fx = max(fx, (uint32_t)__shfl_xor((int)fx, o, 64));
+                const int E = group_shift(fx);
+                const float se = pow2i(E), so = BITS == 4 ? pow2i(E - 4) : se;
                 float f[8];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    f[2 * e] = __uint_as_float(t[e] << 16) * 0x1p64f;
-                    f[2 * e + 1] = __uint_as_float(t[e] & 0xffff0000u) * (BITS == 4 ? 0x1p60f : 0x1p64f);
+                    f[2 * e] = __uint_as_float(t[e] << 16) * se;
+                    f[2 * e + 1] = __uint_as_float(t[e] & 0xffff0000u) * so;
                 }
                 // 4-bit pairs (x0,x4)(x1,x5)(x2,x6)(x3,x7); 8-bit pairs (x0,x2)(x1,x3)(x4,x6)(x5,x7)
                 constexpr int p0 = 0, p1 = BITS == 4 ? 4 : 2, p2 = 1, p3 = BITS == 4 ? 5 : 3;
@@ -249,7 +258,10 @@ struct TileEngine {
                 // the GS/8 vectors of a group sit in consecutive lanes
 #pragma unroll
                 for (int o = 1; o < GS / 8; o <<= 1) sm += __shfl_xor(sm, o, 64);
-                if (v < (uint32_t)XV && (vi & (GS / 8 - 1)) == 0) lds.xs[m][(vi * 8) >> GSH] = sm;
+                if (v < (uint32_t)XV && (vi & (GS / 8 - 1)) == 0) {
+                    lds.xs[m][(vi * 8) >> GSH] = sm;
+                    lds.xe[m][(vi * 8) >> GSH] = 133 - E;
+                }
             }
         }
         if (pf & PLANE_GROUP_OUT) {
@@ -324,7 +336,7 @@ struct TileEngine {
     }
 
     // Fold one period's accumulator rows into acc: C row i = (m, slot) holds
-    // wave-pass group gbase + slot; acc += s * 2^69 * C + bias_term * xsum.
+    // wave-pass group gbase + slot; acc += s * ldexp(C, 133 - E) + bias_term * xsum.
     // Groups at or past glim (past the wave's quarter or the K tail) are not
     // this wave's and are skipped.
     __device__ __forceinline__ void flush(uint32_t pf, uint32_t gbase, uint32_t glim, uint32_t xg0, f32x4 (&C0)[MB],
@@ -335,14 +347,17 @@ struct TileEngine {
             const f32x4 c = C0[b] + C1[b];
             uint32_t g[4];
             float xsum[4];
+            int xn[4];
             if (S >= 4) {
                 const uint32_t g4 = gbase + (4 * kq) % S;
                 const uint32_t m = b * MP + (4 * kq) / S;
                 const f32x4 x4 = *(const f32x4*)&lds.xs[m][xg0 + g4];
+                const i32x4 e4 = *(const i32x4*)&lds.xe[m][xg0 + g4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     g[q] = g4 + q;
                     xsum[q] = x4[q];
+                    xn[q] = e4[q];
                 }
             } else {  // S == 2: rows (2kq, gbase), (2kq, gbase+1), (2kq+1, gbase), (2kq+1, gbase+1)
                 const uint32_t m = b * MP + 2 * kq;
@@ -350,13 +365,14 @@ struct TileEngine {
                 for (int q = 0; q < 4; ++q) {
                     g[q] = gbase + (q & 1);
                     xsum[q] = lds.xs[m + (q >> 1)][xg0 + g[q]];
+                    xn[q] = lds.xe[m + (q >> 1)][xg0 + g[q]];
                 }
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float sc = plane_f32(lds.sc[g[q]][j], bf);
                 const float bias = biased ? plane_f32(lds.bi[g[q]][j], bf) : -(float)(1 << (BITS - 1)) * sc;
-                const float nv = fmaf(sc * 0x1p69f, c[q], fmaf(bias, xsum[q], acc[b][q]));
+                const float nv = fmaf(sc, ldexp_f32(c[q], xn[q]), fmaf(bias, xsum[q], acc[b][q]));
                 acc[b][q] = g[q] < glim ? nv : acc[b][q];
             }
             C0[b] = C1[b] = f32x4{0, 0, 0, 0};

@@ -86,6 +86,42 @@ QMM_DEVICE float wave_sum8(const float (&v)[8], int lane) {
     return c;
 }
 
+// ---- Per-group activation exponent of the matrix-core kernels. Their codes
+// enter the MFMA as raw bf16 bit patterns (a pattern p < 256 is exactly
+// p * 2^-133), so each group's activations are staged as x * 2^E with
+// E = min(189 - f, 127), f the largest exponent field in the group: the
+// group's largest |x| lands in [2^62, 2^64), every product x * 2^E * q * 2^-133
+// is exact and in f32's normal range (for |x| >= 2^-120 or so), and the group's
+// accumulated sum is brought back with one v_ldexp_f32 by 133 - E. This holds
+// for every finite activation (E = -66 for Inf/NaN keeps them as they are).
+
+// Largest exponent field among the 8 bf16 values of a 16-byte vector.
+QMM_DEVICE uint32_t bf16x8_exp_max(const u32x4& t) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        m = max(m, max(__builtin_amdgcn_ubfe(t[e], 7, 8), __builtin_amdgcn_ubfe(t[e], 23, 8)));
+    return m;
+}
+
+// Largest f32 exponent field among 8 f32 values (two 16-byte vectors).
+QMM_DEVICE uint32_t f32x8_exp_max(const u32x4& a, const u32x4& b) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        m = max(m, max(__builtin_amdgcn_ubfe(a[e], 23, 8), __builtin_amdgcn_ubfe(b[e], 23, 8)));
+    return m;
+}
+
+// Staging exponent E of a group whose largest exponent field is f.
+QMM_DEVICE int group_shift(uint32_t f) { return min(189 - (int)f, 127); }
+
+// 2^e as f32 for e in [-126, 127].
+QMM_DEVICE float pow2i(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+// c * 2^n, exact unless the result leaves f32's range.
+QMM_DEVICE float ldexp_f32(float c, int n) { return __builtin_amdgcn_ldexpf(c, n); }
+
 // D = a.lo*b.lo + a.hi*b.hi + c (products exact for bf16, f32 accumulate).
 QMM_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,

@@ -1,7 +1,7 @@
 // Decode-shaped 4-bit affine matvec (M <= 2, bf16 activations) on gfx950.
 //
 // Arithmetic: per group g of a weight row,
-//   s*sum(x*q) + b*sum(x) = 16s * sum x*(1 + q/16) + (b - 16s) * sum x
+//   s*sum(x*q) + b*sum(x) = (16s * sum x*(1 + q/16) - 16s * sum x) + b * sum x
 // where (1 + q/16) is a bf16 built from a code nibble by one shift and one
 // v_and_or_b32, and the sums run on v_dot2_f32_bf16 (exact bf16 products, f32
 // accumulation). This reassociates only additions of the reference's per-element
@@ -50,7 +50,7 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 }
 
 
-// LDS per workgroup: folded (16s, b - 16s) per (tile row, group of the pass),
+// LDS per workgroup: (16s, bias term) per (tile row, group of the pass),
 // activation pairs stored [d][chunk] (16-byte units) so that a wave reading
 // vector d of chunks L, L+64 touches consecutive addresses, and chunk sums.
 template <int MT>
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(kWgThreads) void qmv_w4_decode(AffineBatch batch) {
                     const float s16 = 16.0f * sc;
                     const float b = BIASED ? h2f<BF_PLANES>((bv[e >> 1] >> (16 * (e & 1))) & 0xffffu)
                                            : -8.0f * sc;  // symmetric: -s * 2^(bits-1)
-                    lds.meta[r8 + e][g] = make_float2(s16, b - s16);
+                    lds.meta[r8 + e][g] = make_float2(s16, b);
                 }
             }
             // activations: MT * 512 vectors over all threads
@@ -194,7 +194,10 @@ __global__ __launch_bounds__(kWgThreads) void qmv_w4_decode(AffineBatch batch) {
                         d0 = dot2_bf16(pr[2][q], xr[m][8 + q], d0);
                         d1 = dot2_bf16(pr[3][q], xr[m][12 + q], d1);
                     }
-                    acc[r][m] = fmaf(e.x, d0 + d1, fmaf(e.y, xs[m], acc[r][m]));
+                    // (16s * sum x(1 + q/16) - 16s * sum x) is s * sum x*q exactly for
+                    // a single term, so a one-hot row yields s*q + b with one
+                    // rounding, the reference's dequantised weight
+                    acc[r][m] = fmaf(e.y, xs[m], fmaf(e.x, d0 + d1, fmaf(-e.x, xs[m], acc[r][m])));
                 }
             }
         }

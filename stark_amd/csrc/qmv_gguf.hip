@@ -17,9 +17,11 @@
 // p * 2^-133; Q8_0 codes enter as q + 128, the -128 folded into the bias
 // term; Q4_K high nibbles enter as 16 q with their activations scaled by
 // 2^-4), B columns = the 16 weight rows of a tile, A rows = (activation part,
-// group slot). The activations are f32: each row enters as two bf16 rows,
-// hi = bf16(x) and lo = bf16(x - hi), so |x - hi - lo| <= 2^-18 |x| and the
-// products stay exact; the two parts' sums meet in the reduction. Groups are
+// group slot). The activations are f32, staged per group as x * 2^E (a
+// per-group exponent, group_shift in qmm_common.h): each row enters as two
+// bf16 rows, hi = bf16(x 2^E) and lo = bf16(x 2^E - hi), so
+// |x 2^E - hi - lo| <= 2^-18 |x 2^E| and the products stay exact; the two
+// parts' sums meet in the reduction, brought back by ldexp(., 133 - E). Groups are
 // the 32-value (sub-)blocks; per-group scale and bias are applied once in f32
 // when a period of steps ends.
 //
@@ -145,6 +147,7 @@ struct GLds {
     float bi[G::TPW][G::GX][kRows];  // per (group, row) bias term
     u32x4 xp[G::MR][G::PASS / 8];    // activation rows (hi, lo per real row), 8-bit pair order
     float xs[G::MR][G::GX];          // per-group activation sums
+    alignas(16) int xe[G::MR][G::GX];  // per-group 133 - E (activations staged as x * 2^E)
     u32x4 zero[4];
 };
 
@@ -233,8 +236,15 @@ struct GEngine {
                 x[e] = __uint_as_float(xa[i][e]);
                 x[4 + e] = __uint_as_float(xb[i][e]);
             }
-            // Q4_K: values 32..63 of every 64 meet the high nibbles (16 q)
-            const float sc = (KIND == 12 && ((c * 8) & 32)) ? 0x1p60f : 0x1p64f;
+            // per-group exponent E (group_shift): the 4 chunks of a 32-value
+            // group sit in consecutive lanes; Q4_K values 32..63 of every 64
+            // meet the high nibbles (16 q) and are staged at x * 2^(E-4)
+            uint32_t fx = f32x8_exp_max(xa[i], xb[i]);
+            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 1, 64));
+            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 2, 64));
+            const int E = group_shift(fx);
+            const int Es = (KIND == 12 && ((c * 8) & 32)) ? E - 4 : E;
+            const float sc = pow2i(Es);
             if (v < (uint32_t)XV && r < M && c * 8 < kvals) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(x[e]);
@@ -256,8 +266,8 @@ struct GEngine {
                 shi += h0 + h1;
                 slo += __uint_as_float(pl[q] << 16) + __uint_as_float(pl[q] & 0xffff0000u);
             }
-            shi *= 1.0f / sc;
-            slo *= 1.0f / sc;
+            shi = ldexp_f32(shi, -Es);
+            slo = ldexp_f32(slo, -Es);
             // the 4 chunks of a 32-value group sit in consecutive lanes
             shi += __shfl_xor(shi, 1, 64);
             shi += __shfl_xor(shi, 2, 64);
@@ -269,6 +279,8 @@ struct GEngine {
                 if ((c & 3) == 0) {
                     lds.xs[2 * r][c >> 2] = shi;
                     lds.xs[2 * r + 1][c >> 2] = slo;
+                    lds.xe[2 * r][c >> 2] = 133 - E;
+                    lds.xe[2 * r + 1][c >> 2] = 133 - E;
                 }
             }
         }
@@ -353,10 +365,11 @@ struct GEngine {
             const uint32_t g4 = gbase + (4 * kq) % S;
             const uint32_t a = b * MP + (4 * kq) / S;
             const f32x4 x4 = *(const f32x4*)&lds.xs[a][g4];
+            const mfma::i32x4 e4 = *(const mfma::i32x4*)&lds.xe[a][g4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float nv =
-                    fmaf(lds.sc[0][g4 + q][j] * 0x1p69f, c[q], fmaf(lds.bi[0][g4 + q][j], x4[q], acc[b][q]));
+                const float nv = fmaf(lds.sc[0][g4 + q][j], ldexp_f32(c[q], e4[q]),
+                                      fmaf(lds.bi[0][g4 + q][j], x4[q], acc[b][q]));
                 acc[b][q] = g4 + q < glim ? nv : acc[b][q];
             }
             C0[b] = C1[b] = f32x4{0, 0, 0, 0};
@@ -419,11 +432,12 @@ struct GEngine {
                 for (int t = 0; t < 4; ++t) {
                     const uint32_t g = gw + 4 * s + t;
                     if (TAIL && g >= glim) continue;
-                    const float sc = lds.sc[tt][g][j] * 0x1p69f, bi = lds.bi[tt][g][j];
+                    const float sc = lds.sc[tt][g][j], bi = lds.bi[tt][g][j];
                     const float x0 = lds.xs[2 * m0][g] + lds.xs[2 * m0 + 1][g];
                     const float x1 = lds.xs[2 * m1][g] + lds.xs[2 * m1 + 1][g];
-                    acc[tt][0] = fmaf(sc, c[t][0] + c[t][1], fmaf(bi, x0, acc[tt][0]));
-                    acc[tt][1] = fmaf(sc, c[t][2] + c[t][3], fmaf(bi, x1, acc[tt][1]));
+                    const int n0 = lds.xe[2 * m0][g], n1 = lds.xe[2 * m1][g];
+                    acc[tt][0] = fmaf(sc, ldexp_f32(c[t][0] + c[t][1], n0), fmaf(bi, x0, acc[tt][0]));
+                    acc[tt][1] = fmaf(sc, ldexp_f32(c[t][2] + c[t][3], n1), fmaf(bi, x1, acc[tt][1]));
                 }
             }
         }

@@ -120,27 +120,63 @@ uint32_t persistent_grid(Kern kern) {
     return grid;
 }
 
-// Device copy of the schedule of a shape set (ops in launch order: tile
-// count and K each) for `grid` workgroups and tiles of `rows` rows, built on
-// first use and kept for the life of the process (a few KiB per distinct
-// shape set and device). The tiles that share the 128-byte lines of the
-// group-output planes (64 rows) go to one XCD.
-bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* out, uint32_t rows = kRows) {
-    static std::mutex mu;
-    static std::map<std::vector<uint32_t>, Schedule> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    std::vector<uint32_t> key{(uint32_t)dev, grid, rows};
-    for (uint32_t i = 0; i < count; ++i) {
-        key.push_back((ops[i].n + rows - 1) / rows);
-        key.push_back(ops[i].k);
+// ---- Schedule store. The host-built schedules live in a file-scope device
+// array (one copy per GPU, no allocation on any call) and are written by a
+// stream-ordered upload kernel whose payload travels in its kernel arguments,
+// so a first call on a new shape set neither allocates nor waits for the
+// device: it enqueues one or more small upload launches ahead of the product
+// on the caller's stream. Entries are immutable once written.
+//  - Another stream that uses an entry before its upload has completed waits
+//    for it on the device (hipStreamWaitEvent), never on the host.
+//  - Under stream capture the upload becomes part of the graph (every replay
+//    rewrites the same words); such an entry is pinned for the life of the
+//    process, and the next eager call uploads it once more for eager use.
+//  - When the store is full, an eager call synchronizes the device once and
+//    drops every unpinned entry (the only blocking case; a capturing call
+//    gets STARK_QMM_OUT_OF_MEMORY instead).
+constexpr uint32_t kStoreWords = 1u << 20;   // 4 MiB per device
+constexpr uint32_t kUploadWords = 960;       // payload words per upload launch (3.8 KB of arguments)
+__device__ __align__(256) uint32_t sched_store[kStoreWords];
+
+struct UploadChunk {
+    uint32_t offset, count;
+    uint32_t w[kUploadWords];
+};
+
+__global__ __launch_bounds__(256) void sched_upload(uint32_t* store, UploadChunk c) {
+    for (uint32_t i = threadIdx.x; i < c.count; i += 256) store[c.offset + i] = c.w[i];
+}
+
+struct StoreEntry {
+    std::vector<uint32_t> host;  // begin[grid + 1] then the tile lists
+    uint32_t offset = 0;
+    hipEvent_t done = nullptr;   // recorded after the eager upload
+    bool eager = false;          // uploaded outside capture
+    bool pinned = false;         // referenced by a captured graph
+};
+
+struct DeviceStore {
+    uint32_t* base = nullptr;
+    uint32_t used = 0;
+    std::map<std::vector<uint32_t>, StoreEntry> entries;
+};
+
+stark_qmm_status upload(uint32_t* base, const StoreEntry& e, hipStream_t stream) {
+    UploadChunk c;
+    for (size_t s = 0; s < e.host.size(); s += kUploadWords) {
+        c.offset = e.offset + (uint32_t)s;
+        c.count = (uint32_t)std::min<size_t>(kUploadWords, e.host.size() - s);
+        std::copy(e.host.begin() + s, e.host.begin() + s + c.count, c.w);
+        hipLaunchKernelGGL(sched_upload, dim3(1), dim3(256), 0, stream, base, c);
+        QMM_HIP_CHECK(hipGetLastError());
     }
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(key);
-    if (it != cache.end()) {
-        *out = it->second;
-        return true;
-    }
+    return STARK_QMM_OK;
+}
+
+// Tile lists of a shape set (ops in launch order: tile count and K each) for
+// `grid` workgroups and tiles of `rows` rows. The tiles that share the
+// 128-byte lines of the group-output planes (64 rows) go to one XCD.
+std::vector<uint32_t> build_schedule(const AffineOp* ops, uint32_t count, uint32_t grid, uint32_t rows) {
     const uint32_t per_xcd = grid / 8;
     std::vector<std::vector<uint32_t>> lists(grid);
     std::vector<uint64_t> load(grid, 0);
@@ -189,16 +225,74 @@ bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* 
     }
     host[grid] = total;
     for (uint32_t b = 0; b < grid; ++b) host.insert(host.end(), lists[b].begin(), lists[b].end());
-    void* d = nullptr;
-    if (hipMalloc(&d, host.size() * sizeof(uint32_t)) != hipSuccess) return false;
-    if (hipMemcpy(d, host.data(), host.size() * sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess) {
-        (void)hipFree(d);
-        return false;
+    return host;
+}
+
+// Device schedule of a shape set, uploaded on `stream` on first use (see the
+// store above).
+stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* out, hipStream_t stream,
+                              uint32_t rows = kRows) {
+    static std::mutex mu;
+    static std::map<int, DeviceStore> stores;
+    int dev = 0;
+    QMM_HIP_CHECK(hipGetDevice(&dev));
+    std::vector<uint32_t> key{grid, rows};
+    for (uint32_t i = 0; i < count; ++i) {
+        key.push_back((ops[i].n + rows - 1) / rows);
+        key.push_back(ops[i].k);
     }
-    Schedule s{(const uint32_t*)d, (const uint32_t*)d + grid + 1};
-    cache.emplace(std::move(key), s);
-    *out = s;
-    return true;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    QMM_HIP_CHECK(hipStreamIsCapturing(stream, &cap));
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(mu);
+    DeviceStore& ds = stores[dev];
+    if (!ds.base) QMM_HIP_CHECK(hipGetSymbolAddress((void**)&ds.base, HIP_SYMBOL(sched_store)));
+    auto it = ds.entries.find(key);
+    if (it == ds.entries.end()) {
+        StoreEntry e;
+        e.host = build_schedule(ops, count, grid, rows);
+        const uint32_t words = ((uint32_t)e.host.size() + 63) / 64 * 64;
+        if (words > kStoreWords) return STARK_QMM_OUT_OF_MEMORY;
+        if (ds.used + words > kStoreWords) {
+            if (capturing) return STARK_QMM_OUT_OF_MEMORY;
+            QMM_HIP_CHECK(hipDeviceSynchronize());
+            uint32_t end = 0;
+            for (auto jt = ds.entries.begin(); jt != ds.entries.end();) {
+                if (jt->second.pinned) {
+                    end = std::max(end, jt->second.offset + ((uint32_t)jt->second.host.size() + 63) / 64 * 64);
+                    ++jt;
+                } else {
+                    if (jt->second.done) (void)hipEventDestroy(jt->second.done);
+                    jt = ds.entries.erase(jt);
+                }
+            }
+            ds.used = end;
+            if (ds.used + words > kStoreWords) return STARK_QMM_OUT_OF_MEMORY;
+        }
+        e.offset = ds.used;
+        ds.used += words;
+        it = ds.entries.emplace(std::move(key), std::move(e)).first;
+    }
+    StoreEntry& e = it->second;
+    if (capturing) {
+        // the graph carries its own upload, ordered before the product
+        if (e.eager && hipEventQuery(e.done) == hipErrorNotReady) QMM_HIP_CHECK(hipEventSynchronize(e.done));
+        if (!e.eager) {
+            const stark_qmm_status st = upload(ds.base, e, stream);
+            if (st != STARK_QMM_OK) return st;
+        }
+        e.pinned = true;
+    } else if (!e.eager) {
+        const stark_qmm_status st = upload(ds.base, e, stream);
+        if (st != STARK_QMM_OK) return st;
+        if (!e.done) QMM_HIP_CHECK(hipEventCreateWithFlags(&e.done, hipEventDisableTiming));
+        QMM_HIP_CHECK(hipEventRecord(e.done, stream));
+        e.eager = true;
+    } else if (hipEventQuery(e.done) == hipErrorNotReady) {
+        QMM_HIP_CHECK(hipStreamWaitEvent(stream, e.done, 0));
+    }
+    *out = Schedule{ds.base + e.offset, ds.base + e.offset + grid + 1};
+    return STARK_QMM_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -224,7 +318,8 @@ bool schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* 
 //  - Loads in flight. A ring of 8 step registers, refilled 8 steps ahead
 //    across unit, tile and barrier boundaries (8 KiB per wave in flight). Two
 //    workgroups per CU: more bytes in flight only lengthen the queues.
-//  - Activations are staged per wave (no barrier) into one of kXR regions
+//  - Activations are staged per wave (no barrier) into one of kXR regions,
+//    as x * 2^E with a per-group exponent E (group_shift in qmm_common.h),
 //    tagged (op, chunk), so consecutive tiles of an op reuse them; the plane
 //    vectors of a unit are loaded with the unit and pass through a
 //    wave-private LDS block at the flush.
@@ -234,9 +329,10 @@ constexpr int kUnitK = 1024;   // k values per unit (16 groups of 64)
 constexpr int kListLds = kWg;  // schedule entries staged in LDS at kernel start (one per thread)
 
 struct StreamLds {
-    u32x4 xp[4][kXR][kUnitK / 8];  // activation pairs (x0,x4)(x1,x5).. per 8 values; x*2^64, odd values x*2^60
+    u32x4 xp[4][kXR][kUnitK / 8];  // activation pairs (x0,x4)(x1,x5).. per 8 values; x*2^E, odd values x*2^(E-4)
     float xs[4][kXR][kUnitK / 64];  // activation sum per group
-    f32x4 pl[4][kTR * 8];          // (scale * 2^69, bias term) of [row][group] of the wave's unit
+    int xe[4][kXR][kUnitK / 64];    // 133 - E per group: the flush's ldexp (activations staged as x * 2^E)
+    f32x4 pl[4][kTR * 8];          // (scale, bias term) of [row][group] of the wave's unit
     float red[2][4][kTR];           // per-wave row sums, double-buffered by tile parity
     u32x4 zero[4][4];
     uint32_t list[kListLds];        // the workgroup's first kListLds schedule entries
@@ -335,15 +431,23 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         const uint32_t tag = ((e >> 24) << 16) | c;
         u32x4* xpw = lds.xp[wave][rg];
         float* xsw = lds.xs[wave][rg];
+        int* xew = lds.xe[wave][rg];
         if (tag_of(rg) != tag) {  // stage this unit's activations (loaded with the unit)
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
                 const u32x4 t = xv[m];
+                // the group's exponent: its 8 vectors sit in 8 consecutive lanes
+                uint32_t fx = bf16x8_exp_max(t);
+                fx = max(fx, (uint32_t)__shfl_xor((int)fx, 1, 64));
+                fx = max(fx, (uint32_t)__shfl_xor((int)fx, 2, 64));
+                fx = max(fx, (uint32_t)__shfl_xor((int)fx, 4, 64));
+                const int E = group_shift(fx);
+                const float se = pow2i(E), so = pow2i(E - 4);
                 float f[8];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    f[2 * q] = __uint_as_float(t[q] << 16) * 0x1p64f;
-                    f[2 * q + 1] = __uint_as_float(t[q] & 0xffff0000u) * 0x1p60f;
+                    f[2 * q] = __uint_as_float(t[q] << 16) * se;
+                    f[2 * q + 1] = __uint_as_float(t[q] & 0xffff0000u) * so;
                 }
                 u32x4 pq;  // (x0,x4)(x1,x5)(x2,x6)(x3,x7), as the codes unpack
                 pq[0] = perm(__float_as_uint(f[4]), __float_as_uint(f[0]), 0x07060302u);
@@ -357,13 +461,16 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 sm += __shfl_xor(sm, 1, 64);
                 sm += __shfl_xor(sm, 2, 64);
                 sm += __shfl_xor(sm, 4, 64);
-                if ((lane & 7) == 0) xsw[8 * m + (lane >> 3)] = sm;
+                if ((lane & 7) == 0) {
+                    xsw[8 * m + (lane >> 3)] = sm;
+                    xew[8 * m + (lane >> 3)] = 133 - E;
+                }
             }
             tg0 = rg == 0 ? tag : tg0;
             tg1 = rg == 1 ? tag : tg1;
             tg2 = rg == 2 ? tag : tg2;
         }
-        {  // plane vectors -> f32 (scale * 2^69, bias term) pairs at [row][group]
+        {  // plane vectors -> f32 (scale, bias term) pairs at [row][group]
             const bool bf = op.w_dt == STARK_QMM_BF16, biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
             float sv[8], bv[8];
 #pragma unroll
@@ -371,7 +478,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 const uint32_t hs = (pls[q >> 1] >> (16 * (q & 1))) & 0xffffu;
                 const uint32_t hb = (plb[q >> 1] >> (16 * (q & 1))) & 0xffffu;
                 const float sc = plane_f32(hs, bf);
-                sv[q] = sc * 0x1p69f;
+                sv[q] = sc;
                 bv[q] = biased ? plane_f32(hb, bf) : -8.0f * sc;
             }
             float2* pw = (float2*)lds.pl[wave];
@@ -452,6 +559,9 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             const float2 xa = *(const float2*)&xsw[gb];
             const float2 xb = *(const float2*)&xsw[gb + 4];
             const float xq[4] = {xa.x, xa.y, xb.x, xb.y};
+            const int2 ea = *(const int2*)&xew[gb];
+            const int2 eb = *(const int2*)&xew[gb + 4];
+            const int nq[4] = {ea.x, ea.y, eb.x, eb.y};
             const f32x4* pw = lds.pl[wave];
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
@@ -460,7 +570,8 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 const f32x4 pa = pw[(row * 16 + gb) / 2], pb = pw[(row * 16 + gb + 4) / 2];  // (s, b) of 2 groups each
                 const float sq[4] = {pa[0], pa[2], pb[0], pb[2]}, bq[4] = {pa[1], pa[3], pb[1], pb[3]};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[st][q] = fmaf(sq[q], cs[q], fmaf(bq[q], xq[q], acc[st][q]));
+                for (int q = 0; q < 4; ++q)
+                    acc[st][q] = fmaf(sq[q], ldexp_f32(cs[q], nq[q]), fmaf(bq[q], xq[q], acc[st][q]));
             }
         }
 
@@ -527,8 +638,10 @@ stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t 
     // two workgroups (eight waves) per CU, a multiple of the 8 XCDs
     const uint32_t grid = std::min(std::min(persistent_grid(kern), (uint32_t)std::max(8, cus * 2 / 8 * 8)),
                                    (tiles + 7) / 8 * 8);
+    if (grid == 0) return STARK_QMM_DEVICE_FAILURE;
     Schedule sched;
-    if (grid == 0 || !schedule_for(sorted.data(), count, grid, &sched, kTR)) return STARK_QMM_DEVICE_FAILURE;
+    const stark_qmm_status st = schedule_for(sorted.data(), count, grid, &sched, stream, kTR);
+    if (st != STARK_QMM_OK) return st;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(kWg), 0, stream, batch, sched);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
@@ -550,8 +663,10 @@ stark_qmm_status launch_one(const AffineOp* ops, uint32_t count, hipStream_t str
     if (tiles == 0) return STARK_QMM_OK;
     auto kern = qmv_mfma<MP, MB, GS, BITS, SIGNED>;
     const uint32_t grid = std::min(persistent_grid(kern), (tiles + 7) / 8 * 8);
+    if (grid == 0) return STARK_QMM_DEVICE_FAILURE;
     Schedule sched;
-    if (grid == 0 || !schedule_for(sorted.data(), count, grid, &sched)) return STARK_QMM_DEVICE_FAILURE;
+    const stark_qmm_status st = schedule_for(sorted.data(), count, grid, &sched, stream);
+    if (st != STARK_QMM_OK) return st;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(kWg), 0, stream, batch, sched);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;

@@ -3,9 +3,10 @@
 //
 // Same arithmetic as the tile engine (mfma_tile.h): codes enter
 // v_mfma_f32_16x16x32_bf16 as raw bf16 bit patterns (p < 256 is p * 2^-133),
-// activations are staged as bf16 x * 2^64 (x * 2^60 where the code is the
-// high nibble, i.e. 16 q), and each group's scale and bias are applied once,
-// in f32: acc += s * 2^69 * C + bias_term * sum(x) (kernel.rs:219-265 per
+// activations are staged as bf16 x * 2^E with a per-group exponent E
+// (x * 2^(E-4) where the code is the high nibble, i.e. 16 q), and each group's
+// scale and bias are applied once, in f32:
+// acc += s * ldexp(C, 133 - E) + bias_term * sum(x) (kernel.rs:219-265 per
 // element, regrouped). The layout differs: every MFMA takes all 16 activation
 // rows (A row = activation row, no group slots), covers 32 k of one group and
 // accumulates the group's two halves before its flush, and a workgroup runs
@@ -37,9 +38,10 @@ struct SmLds {
         u32x4 stage[kSmTiles][4][kRows * kSmRowB / 16];  // codes [tile][wave][row][kSmRowB bytes]
         float red[kSmTiles][4][16][kRows];               // per-wave partial outputs, after the last pass
     };
-    float2 pl[kSmTiles][kSmGroups][kRows];  // (scale * 2^69, bias term) [tile][group][row]
+    float2 pl[kSmTiles][kSmGroups][kRows];  // (scale, bias term) [tile][group][row]
     u32x4 xp[16][kSmPass / 8];              // activation rows, MFMA pair order, scaled
     float xs[16][kSmGroups];                // per-group activation sums
+    int xe[16][kSmGroups];                  // per-group 133 - E (activations staged as x * 2^E)
 };
 
 template <bool SIGNED>
@@ -101,18 +103,25 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 *(u32x4*)((uint8_t*)lds.stage[tt][c / 8] + r * kSmRowB + 16 * (c % 8)) = wc[B][tt][i];
             }
             const float sc = plane_f32(ps[B][tt], bf);
-            lds.pl[tt][tid / 16][tid % 16] = float2{sc * 0x1p69f, biased ? plane_f32(pb[B][tt], bf) : -8.0f * sc};
+            lds.pl[tt][tid / 16][tid % 16] = float2{sc, biased ? plane_f32(pb[B][tt], bf) : -8.0f * sc};
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
             if (m >= M) continue;  // rows past M stay zero (cleared once); a row's 8-lane groups agree
             const u32x4 t = xv[B][i];
+            // the group's exponent: its 8 vectors sit in 8 consecutive lanes
+            uint32_t fx = bf16x8_exp_max(t);
+            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 1, 64));
+            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 2, 64));
+            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 4, 64));
+            const int E = group_shift(fx);
+            const float se = pow2i(E), so = pow2i(E - 4);
             float f[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                f[2 * e] = __uint_as_float(t[e] << 16) * 0x1p64f;           // even values meet q
-                f[2 * e + 1] = __uint_as_float(t[e] & 0xffff0000u) * 0x1p60f;  // odd values meet 16 q
+                f[2 * e] = __uint_as_float(t[e] << 16) * se;           // even values meet q
+                f[2 * e + 1] = __uint_as_float(t[e] & 0xffff0000u) * so;  // odd values meet 16 q
             }
             u32x4 pq;  // (x0,x4)(x1,x5)(x2,x6)(x3,x7), as the codes unpack
             pq[0] = perm(__float_as_uint(f[4]), __float_as_uint(f[0]), 0x07060302u);
@@ -126,7 +135,10 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             sm += __shfl_xor(sm, 1, 64);  // the 8 vectors of a group sit in consecutive lanes
             sm += __shfl_xor(sm, 2, 64);
             sm += __shfl_xor(sm, 4, 64);
-            if ((c & 7) == 0) lds.xs[m][c / 8] = sm;
+            if ((c & 7) == 0) {
+                lds.xs[m][c / 8] = sm;
+                lds.xe[m][c / 8] = 133 - E;
+            }
         }
     };
 
@@ -159,11 +171,14 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             const uint32_t gp = wave * 4 + g;  // group within the pass
             const f32x4 x4 = f32x4{lds.xs[4 * kq][gp], lds.xs[4 * kq + 1][gp], lds.xs[4 * kq + 2][gp],
                                    lds.xs[4 * kq + 3][gp]};
+            const int e4[4] = {lds.xe[4 * kq][gp], lds.xe[4 * kq + 1][gp], lds.xe[4 * kq + 2][gp],
+                               lds.xe[4 * kq + 3][gp]};
 #pragma unroll
             for (int tt = 0; tt < kSmTiles; ++tt) {
                 const float2 p = lds.pl[tt][gp][j];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[tt][q] = fmaf(p.x, C[tt][q], fmaf(p.y, x4[q], acc[tt][q]));
+                for (int q = 0; q < 4; ++q)
+                    acc[tt][q] = fmaf(p.x, ldexp_f32(C[tt][q], e4[q]), fmaf(p.y, x4[q], acc[tt][q]));
             }
         }
     };
@@ -185,7 +200,10 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         if (m >= M) lds.xp[m][v % (kSmPass / 8)] = u32x4{0, 0, 0, 0};
     }
     for (uint32_t v = tid; v < 16 * kSmGroups; v += kWg)
-        if (v / kSmGroups >= M) lds.xs[v / kSmGroups][v % kSmGroups] = 0.0f;
+        if (v / kSmGroups >= M) {
+            lds.xs[v / kSmGroups][v % kSmGroups] = 0.0f;
+            lds.xe[v / kSmGroups][v % kSmGroups] = 0;
+        }
     for (uint32_t kbase = 0; kbase < K; kbase += 2 * kSmPass) {
         pass(B0{}, kbase);
         if (kbase + kSmPass < K) pass(B1{}, kbase + kSmPass);

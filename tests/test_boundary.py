@@ -32,6 +32,20 @@ def test_library_exports_every_declared_symbol():
     assert set(declared_symbols()) == set(qmm.SIGNATURES), "python mirror out of sync with header"
 
 
+def test_library_exports_only_the_c_abi():
+    """Hidden visibility plus a version script: internal C++ symbols (kernel
+    launchers, eligibility checks, std:: instantiations) stay local."""
+    import subprocess
+    from stark_amd import qmm
+    qmm.lib()
+    out = subprocess.run(["nm", "-D", "--defined-only", qmm.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    names = [ln.split()[-1] for ln in out.splitlines() if ln.strip()]
+    extra = [n for n in names if not n.startswith("stark_qmm_") and not n.startswith("__hip_cuid_")]
+    assert not extra, extra[:10]
+    assert set(n for n in names if n.startswith("stark_qmm_")) == set(declared_symbols())
+
+
 def test_abi_version_and_status_strings():
     from stark_amd import qmm
     assert qmm.lib().stark_qmm_abi_version() == 1
