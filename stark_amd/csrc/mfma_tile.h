@@ -232,10 +232,7 @@ struct TileEngine {
                 const uint32_t v = tid + i * kWg, m = v / (XK / 8), vi = v % (XK / 8);
                 const u32x4 t = xv[i];
                 // the group's exponent: its GS/8 vectors sit in consecutive lanes
-                uint32_t fx = bf16x8_exp_max(t);
-#pragma unroll
-                for (int o = 1; o < GS / 8; o <<= 1) fx = max(fx, (uint32_t)__shfl_xor((int)fx, o, 64));
-                const int E = group_shift(fx);
+                const int E = group_shift(group_max<GS / 8>(bf16x8_exp_max(t)));
                 const float se = pow2i(E), so = BITS == 4 ? pow2i(E - 4) : se;
                 float f[8];
 #pragma unroll
@@ -256,8 +253,7 @@ struct TileEngine {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) sm = dot2_bf16(t[e], 0x3F803F80u, sm);
                 // the GS/8 vectors of a group sit in consecutive lanes
-#pragma unroll
-                for (int o = 1; o < GS / 8; o <<= 1) sm += __shfl_xor(sm, o, 64);
+                sm = group_sum<GS / 8>(sm);
                 if (v < (uint32_t)XV && (vi & (GS / 8 - 1)) == 0) {
                     lds.xs[m][(vi * 8) >> GSH] = sm;
                     lds.xe[m][(vi * 8) >> GSH] = 133 - E;

@@ -86,6 +86,37 @@ QMM_DEVICE float wave_sum8(const float (&v)[8], int lane) {
     return c;
 }
 
+// ---- Lane exchanges inside a row of 16 lanes through DPP (no LDS traffic,
+// unlike __shfl_xor's ds_bpermute). Every lane receives the result.
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+
+template <int CTRL>
+QMM_DEVICE uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+QMM_DEVICE float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum / max over aligned groups of L consecutive lanes (L = 1, 2, 4, 8, 16).
+template <int L>
+QMM_DEVICE float group_sum(float v) {
+    if (L >= 2) v += dpp_f32<DPP_XOR1>(v);
+    if (L >= 4) v += dpp_f32<DPP_XOR2>(v);
+    if (L >= 8) v += dpp_f32<DPP_HALF_MIRROR>(v);
+    if (L >= 16) v += dpp_f32<DPP_MIRROR>(v);
+    return v;
+}
+template <int L>
+QMM_DEVICE uint32_t group_max(uint32_t v) {
+    if (L >= 2) v = max(v, dpp_u32<DPP_XOR1>(v));
+    if (L >= 4) v = max(v, dpp_u32<DPP_XOR2>(v));
+    if (L >= 8) v = max(v, dpp_u32<DPP_HALF_MIRROR>(v));
+    if (L >= 16) v = max(v, dpp_u32<DPP_MIRROR>(v));
+    return v;
+}
+
 // ---- Per-group activation exponent of the matrix-core kernels. Their codes
 // enter the MFMA as raw bf16 bit patterns (a pattern p < 256 is exactly
 // p * 2^-133), so each group's activations are staged as x * 2^E with
@@ -97,20 +128,19 @@ QMM_DEVICE float wave_sum8(const float (&v)[8], int lane) {
 
 // Largest exponent field among the 8 bf16 values of a 16-byte vector.
 QMM_DEVICE uint32_t bf16x8_exp_max(const u32x4& t) {
-    uint32_t m = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-        m = max(m, max(__builtin_amdgcn_ubfe(t[e], 7, 8), __builtin_amdgcn_ubfe(t[e], 23, 8)));
-    return m;
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const auto h = [](uint32_t w) { return __builtin_bit_cast(u16x2, w & 0x7f807f80u); };
+    const u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(h(t[0]), h(t[1])),
+                                              __builtin_elementwise_max(h(t[2]), h(t[3])));
+    return (uint32_t)max(m[0], m[1]) >> 7;
 }
 
 // Largest f32 exponent field among 8 f32 values (two 16-byte vectors).
 QMM_DEVICE uint32_t f32x8_exp_max(const u32x4& a, const u32x4& b) {
     uint32_t m = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-        m = max(m, max(__builtin_amdgcn_ubfe(a[e], 23, 8), __builtin_amdgcn_ubfe(b[e], 23, 8)));
-    return m;
+    for (int e = 0; e < 4; ++e) m = max(m, max(a[e] & 0x7f800000u, b[e] & 0x7f800000u));
+    return m >> 23;
 }
 
 // Staging exponent E of a group whose largest exponent field is f.

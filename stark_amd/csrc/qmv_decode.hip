@@ -144,8 +144,7 @@ __global__ __launch_bounds__(kWgThreads) void qmv_w4_decode(AffineBatch batch) {
                 float sm = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) sm = dot2_bf16(t[e], 0x3F803F80u, sm);
-                sm += __shfl_xor(sm, 1, 64);  // the 4 vectors of a chunk are 4 consecutive lanes
-                sm += __shfl_xor(sm, 2, 64);
+                sm = group_sum<4>(sm);  // the 4 vectors of a chunk are 4 consecutive lanes
                 if ((vi & 3) == 0) lds.xs[m][vi >> 2] = sm;
             }
         }

@@ -146,8 +146,11 @@ struct GLds {
     float sc[G::TPW][G::GX][kRows];  // per (group, row) scale
     float bi[G::TPW][G::GX][kRows];  // per (group, row) bias term
     u32x4 xp[G::MR][G::PASS / 8];    // activation rows (hi, lo per real row), 8-bit pair order
-    float xs[G::MR][G::GX];          // per-group activation sums
-    alignas(16) int xe[G::MR][G::GX];  // per-group 133 - E (activations staged as x * 2^E)
+    // per-group activation sums and 133 - E (activations staged as x * 2^E):
+    // per A row in the slot form; per real row (hi + lo) in the dense form,
+    // whose flush adds the two parts anyway (this keeps two workgroups per CU)
+    float xs[G::DENSE ? G::RR : G::MR][G::GX];
+    alignas(16) int xe[G::DENSE ? G::RR : G::MR][G::GX];
     u32x4 zero[4];
 };
 
@@ -239,10 +242,7 @@ struct GEngine {
             // per-group exponent E (group_shift): the 4 chunks of a 32-value
             // group sit in consecutive lanes; Q4_K values 32..63 of every 64
             // meet the high nibbles (16 q) and are staged at x * 2^(E-4)
-            uint32_t fx = f32x8_exp_max(xa[i], xb[i]);
-            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 1, 64));
-            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 2, 64));
-            const int E = group_shift(fx);
+            const int E = group_shift(group_max<4>(f32x8_exp_max(xa[i], xb[i])));
             const int Es = (KIND == 12 && ((c * 8) & 32)) ? E - 4 : E;
             const float sc = pow2i(Es);
             if (v < (uint32_t)XV && r < M && c * 8 < kvals) {
@@ -269,18 +269,21 @@ struct GEngine {
             shi = ldexp_f32(shi, -Es);
             slo = ldexp_f32(slo, -Es);
             // the 4 chunks of a 32-value group sit in consecutive lanes
-            shi += __shfl_xor(shi, 1, 64);
-            shi += __shfl_xor(shi, 2, 64);
-            slo += __shfl_xor(slo, 1, 64);
-            slo += __shfl_xor(slo, 2, 64);
+            shi = group_sum<4>(shi);
+            slo = group_sum<4>(slo);
             if (v < (uint32_t)XV) {
                 lds.xp[2 * r][c] = ph;
                 lds.xp[2 * r + 1][c] = pl;
                 if ((c & 3) == 0) {
-                    lds.xs[2 * r][c >> 2] = shi;
-                    lds.xs[2 * r + 1][c >> 2] = slo;
-                    lds.xe[2 * r][c >> 2] = 133 - E;
-                    lds.xe[2 * r + 1][c >> 2] = 133 - E;
+                    if constexpr (G::DENSE) {
+                        lds.xs[r][c >> 2] = shi + slo;
+                        lds.xe[r][c >> 2] = 133 - E;
+                    } else {
+                        lds.xs[2 * r][c >> 2] = shi;
+                        lds.xs[2 * r + 1][c >> 2] = slo;
+                        lds.xe[2 * r][c >> 2] = 133 - E;
+                        lds.xe[2 * r + 1][c >> 2] = 133 - E;
+                    }
                 }
             }
         }
@@ -433,9 +436,8 @@ struct GEngine {
                     const uint32_t g = gw + 4 * s + t;
                     if (TAIL && g >= glim) continue;
                     const float sc = lds.sc[tt][g][j], bi = lds.bi[tt][g][j];
-                    const float x0 = lds.xs[2 * m0][g] + lds.xs[2 * m0 + 1][g];
-                    const float x1 = lds.xs[2 * m1][g] + lds.xs[2 * m1 + 1][g];
-                    const int n0 = lds.xe[2 * m0][g], n1 = lds.xe[2 * m1][g];
+                    const float x0 = lds.xs[m0][g], x1 = lds.xs[m1][g];
+                    const int n0 = lds.xe[m0][g], n1 = lds.xe[m1][g];
                     acc[tt][0] = fmaf(sc, ldexp_f32(c[t][0] + c[t][1], n0), fmaf(bi, x0, acc[tt][0]));
                     acc[tt][1] = fmaf(sc, ldexp_f32(c[t][2] + c[t][3], n1), fmaf(bi, x1, acc[tt][1]));
                 }

@@ -152,6 +152,7 @@ struct StoreEntry {
     uint32_t offset = 0;
     hipEvent_t done = nullptr;   // recorded after the eager upload
     bool eager = false;          // uploaded outside capture
+    bool landed = false;         // the eager upload has been seen complete
     bool pinned = false;         // referenced by a captured graph
 };
 
@@ -276,7 +277,8 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
     StoreEntry& e = it->second;
     if (capturing) {
         // the graph carries its own upload, ordered before the product
-        if (e.eager && hipEventQuery(e.done) == hipErrorNotReady) QMM_HIP_CHECK(hipEventSynchronize(e.done));
+        if (e.eager && !e.landed) QMM_HIP_CHECK(hipEventSynchronize(e.done));
+        e.landed = e.eager;
         if (!e.eager) {
             const stark_qmm_status st = upload(ds.base, e, stream);
             if (st != STARK_QMM_OK) return st;
@@ -288,8 +290,14 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
         if (!e.done) QMM_HIP_CHECK(hipEventCreateWithFlags(&e.done, hipEventDisableTiming));
         QMM_HIP_CHECK(hipEventRecord(e.done, stream));
         e.eager = true;
-    } else if (hipEventQuery(e.done) == hipErrorNotReady) {
-        QMM_HIP_CHECK(hipStreamWaitEvent(stream, e.done, 0));
+    } else if (!e.landed) {
+        const hipError_t q = hipEventQuery(e.done);
+        if (q == hipSuccess)
+            e.landed = true;
+        else if (q == hipErrorNotReady)
+            QMM_HIP_CHECK(hipStreamWaitEvent(stream, e.done, 0));
+        else
+            return STARK_QMM_DEVICE_FAILURE;
     }
     *out = Schedule{ds.base + e.offset, ds.base + e.offset + grid + 1};
     return STARK_QMM_OK;
@@ -437,11 +445,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             for (int m = 0; m < 2; ++m) {
                 const u32x4 t = xv[m];
                 // the group's exponent: its 8 vectors sit in 8 consecutive lanes
-                uint32_t fx = bf16x8_exp_max(t);
-                fx = max(fx, (uint32_t)__shfl_xor((int)fx, 1, 64));
-                fx = max(fx, (uint32_t)__shfl_xor((int)fx, 2, 64));
-                fx = max(fx, (uint32_t)__shfl_xor((int)fx, 4, 64));
-                const int E = group_shift(fx);
+                const int E = group_shift(group_max<8>(bf16x8_exp_max(t)));
                 const float se = pow2i(E), so = pow2i(E - 4);
                 float f[8];
 #pragma unroll
@@ -458,9 +462,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 float sm = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) sm = dot2_bf16(t[q], 0x3F803F80u, sm);
-                sm += __shfl_xor(sm, 1, 64);
-                sm += __shfl_xor(sm, 2, 64);
-                sm += __shfl_xor(sm, 4, 64);
+                sm = group_sum<8>(sm);
                 if ((lane & 7) == 0) {
                     xsw[8 * m + (lane >> 3)] = sm;
                     xew[8 * m + (lane >> 3)] = 133 - E;

@@ -111,11 +111,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             if (m >= M) continue;  // rows past M stay zero (cleared once); a row's 8-lane groups agree
             const u32x4 t = xv[B][i];
             // the group's exponent: its 8 vectors sit in 8 consecutive lanes
-            uint32_t fx = bf16x8_exp_max(t);
-            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 1, 64));
-            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 2, 64));
-            fx = max(fx, (uint32_t)__shfl_xor((int)fx, 4, 64));
-            const int E = group_shift(fx);
+            const int E = group_shift(group_max<8>(bf16x8_exp_max(t)));
             const float se = pow2i(E), so = pow2i(E - 4);
             float f[8];
 #pragma unroll
@@ -132,9 +128,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             float sm = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) sm = dot2_bf16(t[e], 0x3F803F80u, sm);
-            sm += __shfl_xor(sm, 1, 64);  // the 8 vectors of a group sit in consecutive lanes
-            sm += __shfl_xor(sm, 2, 64);
-            sm += __shfl_xor(sm, 4, 64);
+            sm = group_sum<8>(sm);  // the 8 vectors of a group sit in consecutive lanes
             if ((c & 7) == 0) {
                 lds.xs[m][c / 8] = sm;
                 lds.xe[m][c / 8] = 133 - E;
