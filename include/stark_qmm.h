@@ -276,6 +276,18 @@ STARK_QMM_API uint64_t stark_qmm_routed_experts_workspace_size(uint32_t rows, ui
                                                  uint32_t active);
 STARK_QMM_API stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* args, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): stark_qmm_routed_experts with the workspace taken from a
+ * fixed device array inside the library (one per GPU, held until the process
+ * ends); args->workspace and args->workspace_size are ignored. Calls whose
+ * stark_qmm_routed_experts_workspace_size() exceeds
+ * STARK_QMM_ROUTED_STATIC_SCRATCH_BYTES return STARK_QMM_WORKSPACE_TOO_SMALL.
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (different streams, or threads) race; serialize them. Allocates nothing. */
+#define STARK_QMM_ROUTED_STATIC_SCRATCH_BYTES (8ull << 20)
+STARK_QMM_API stark_qmm_status stark_qmm_routed_experts_static(const stark_qmm_routed_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,7 @@
 // a route; each output value of the matrix-core tile depends on its own
 // activation row alone.
 #include <cmath>
+#include <mutex>
 
 #include "mfma_tile.h"
 
@@ -458,18 +459,23 @@ uint64_t stark_qmm_routed_experts_workspace_size(uint32_t rows, uint32_t model, 
     return routed_layout(rows, model, hidden, experts, active).total;
 }
 
-stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* stream_ptr) {
+}  // extern "C"
+
+namespace {
+
+// The routed pipeline on a workspace of ws_size bytes at ws (device memory).
+stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_t ws_size, void* stream_ptr) {
     if (!a || a->struct_size != sizeof(stark_qmm_routed_args)) return STARK_QMM_ABI_MISMATCH;
     const uint32_t R = a->rows, model = a->model, H = a->hidden, E = a->experts, A = a->active;
     // geometry accepted by RoutedExperts::new / encode_scaled (routed.rs:62-73, 162-170)
     if (R == 0 || R > 1024 || E == 0 || E > 1024 || A == 0 || A > 32 || A > E || model == 0 || model > 16384 ||
         H == 0 || H > 131072)
         return STARK_QMM_INVALID_ARGUMENT;
-    if (!a->input || !a->router_logits || !a->output || !a->workspace) return STARK_QMM_INVALID_ARGUMENT;
+    if (!a->input || !a->router_logits || !a->output || !ws) return STARK_QMM_INVALID_ARGUMENT;
     if (model % 64 || H % 64) return STARK_QMM_UNSUPPORTED_LAYOUT;  // K of both products, 16-row tiles
-    if (((uintptr_t)a->input | (uintptr_t)a->workspace) & 15) return STARK_QMM_UNSUPPORTED;
+    if (((uintptr_t)a->input | (uintptr_t)ws) & 15) return STARK_QMM_UNSUPPORTED;
     const RoutedLayout Lw = routed_layout(R, model, H, E, A);
-    if (a->workspace_size < Lw.total) return STARK_QMM_WORKSPACE_TOO_SMALL;
+    if (ws_size < Lw.total) return STARK_QMM_WORKSPACE_TOO_SMALL;
     const uint32_t max_count = std::min<uint32_t>(R, slot_routes(R));
     stark_qmm_status st = check_bank(a->up, (uint64_t)E * 2 * H, model, max_count);
     if (st != STARK_QMM_OK) return st;
@@ -479,7 +485,6 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
         return STARK_QMM_UNSUPPORTED;
 
     hipStream_t stream = (hipStream_t)stream_ptr;
-    uint8_t* ws = (uint8_t*)a->workspace;
     uint32_t* ids = (uint32_t*)(ws + Lw.ids);
     float* weights = (float*)(ws + Lw.weights);
     uint32_t* sorted = (uint32_t*)(ws + Lw.sorted);
@@ -539,6 +544,49 @@ stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* 
                        (uint16_t*)a->output, model, A, a->round_products_bf16, a->round_accumulator_bf16);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
+}
+
+// ---- Allocation-free variant: the workspace is a file-scope device array,
+// one copy per GPU, held from module load until the process ends. In host
+// code `scratch` only names the symbol; its device address comes from
+// hipGetSymbolAddress once per device (on the entry point's first call there)
+// and is the only form ever passed to a kernel. Nothing in the workspace has
+// to start at zero: every route, table and intermediate is written before it
+// is read within one call.
+constexpr uint64_t kScratchBytes = STARK_QMM_ROUTED_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+uint8_t* scratch_ptr() {
+    static std::mutex mu;
+    static uint8_t* ptrs[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> g(mu);
+    if (!ptrs[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        ptrs[dev] = (uint8_t*)p;
+    }
+    return ptrs[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_args* a, void* stream_ptr) {
+    if (!a || a->struct_size != sizeof(stark_qmm_routed_args)) return STARK_QMM_ABI_MISMATCH;
+    return routed_run(a, (uint8_t*)a->workspace, a->workspace_size, stream_ptr);
+}
+
+stark_qmm_status stark_qmm_routed_experts_static(const stark_qmm_routed_args* a, void* stream_ptr) {
+    if (!a || a->struct_size != sizeof(stark_qmm_routed_args)) return STARK_QMM_ABI_MISMATCH;
+    if (stark_qmm_routed_experts_workspace_size(a->rows, a->model, a->hidden, a->experts, a->active) >
+        kScratchBytes)
+        return STARK_QMM_WORKSPACE_TOO_SMALL;
+    uint8_t* ws = scratch_ptr();
+    if (!ws) return STARK_QMM_DEVICE_FAILURE;
+    return routed_run(a, ws, kScratchBytes, stream_ptr);
 }
 
 }  // extern "C"

@@ -128,6 +128,7 @@ SIGNATURES = {
                                               C.c_uint32, C.c_void_p]),
     "stark_qmm_routed_experts_workspace_size": (C.c_uint64, [C.c_uint32] * 5),
     "stark_qmm_routed_experts": (C.c_uint32, [C.POINTER(_RoutedArgs), C.c_void_p]),
+    "stark_qmm_routed_experts_static": (C.c_uint32, [C.POINTER(_RoutedArgs), C.c_void_p]),
 }
 
 _lib = None
@@ -434,6 +435,9 @@ def mapped_many_async(prepared, status_word: torch.Tensor, stream=None) -> None:
     _check(lib().stark_qmm_mapped_many_async(ops, n, ptrs, _ptr(status_word), _stream(stream)), "mapped_many_async")
 
 
+_NO_WORKSPACE = object()  # routed_experts_static: the library supplies the workspace
+
+
 def routed_experts(input: torch.Tensor, router_logits: torch.Tensor, up: QuantizedB, down: QuantizedB, rows: int,
                    model: int, hidden: int, experts: int, active: int, expert_scales=None, round_logits=False,
                    round_weights=False, round_products=False, round_accumulator=False, sort_expert_ids=False,
@@ -441,7 +445,9 @@ def routed_experts(input: torch.Tensor, router_logits: torch.Tensor, up: Quantiz
                    prepare_only: bool = False):
     """RoutedExperts::encode_scaled (routed.rs:154-257) as one device pipeline."""
     need = routed_experts_workspace_size(rows, model, hidden, experts, active)
-    if workspace is None:
+    if workspace is _NO_WORKSPACE:
+        workspace = None
+    elif workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=input.device)
     if output is None:
         output = torch.empty(rows * model, dtype=torch.bfloat16, device=input.device)
@@ -458,10 +464,30 @@ def routed_experts(input: torch.Tensor, router_logits: torch.Tensor, up: Quantiz
     s.round_products_bf16, s.round_accumulator_bf16 = int(round_products), int(round_accumulator)
     s.sort_expert_ids = int(sort_expert_ids)
     s.workspace = _ptr(workspace)
-    s.workspace_size = _nbytes(workspace)
+    s.workspace_size = 0 if workspace is None else _nbytes(workspace)
     if prepare_only:
         return s, (input, router_logits, expert_scales, up, down, workspace, output)
     _check(lib().stark_qmm_routed_experts(C.byref(s), _stream(stream)), "routed_experts")
+    return output
+
+
+ROUTED_STATIC_SCRATCH_BYTES = 8 << 20
+
+
+def routed_experts_static(input: torch.Tensor, router_logits: torch.Tensor, up: QuantizedB, down: QuantizedB,
+                          rows: int, model: int, hidden: int, experts: int, active: int, output: torch.Tensor,
+                          expert_scales=None, round_logits=False, round_weights=False, round_products=False,
+                          round_accumulator=False, sort_expert_ids=False, stream=None) -> torch.Tensor:
+    """stark_qmm_routed_experts_static: routed_experts with the library's fixed
+    per-GPU scratch as its workspace (no device allocation; `output` is the
+    caller's). Calls that overlap on one GPU race on that scratch."""
+    s, keep = routed_experts(input, router_logits, up, down, rows, model, hidden, experts, active,
+                             expert_scales=expert_scales, round_logits=round_logits, round_weights=round_weights,
+                             round_products=round_products, round_accumulator=round_accumulator,
+                             sort_expert_ids=sort_expert_ids, workspace=_NO_WORKSPACE, output=output,
+                             prepare_only=True)
+    _check(lib().stark_qmm_routed_experts_static(C.byref(s), _stream(stream)), "routed_experts_static")
+    del keep
     return output
 
 
