@@ -92,19 +92,77 @@ def routed_check(qmm, O, c, **flags):
                              sort_expert_ids=flags.get("si", False))
     torch.cuda.synchronize()
     got = O.bf16_to_f32(H.from_dev(out.view(torch.int16), np.uint16))
-    # Each (token, rank) passes through bf16 roundings of the up product, the
-    # gate and the down product; a sum that lands on the other side of a bf16
-    # rounding boundary moves one ulp and propagates. Bound: 2 bf16 ulp of the
-    # value + 1e-2 relative + 5e-3 of the row's largest output.
-    want2, got2 = want.reshape(R, M), got.reshape(R, M)
-    scale = np.abs(want2).max(axis=1, keepdims=True)
-    tol = 2 * np.abs(want2) * 2.0 ** -8 + 1e-2 * np.abs(want2) + 5e-3 * scale + 1e-6
-    bad = np.abs(got2 - want2) > tol
-    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance; worst {np.abs(got2 - want2).max()}"
-    # and the bulk is exact or one ulp off
-    close = np.abs(got2 - want2) <= np.abs(want2) * 2.0 ** -7 + 1e-30
-    assert close.mean() > 0.9
+    check_routed(O, c, got, want, flags)
     return got, want
+
+
+def _dequant4(O, bank, r0, rows, cols, total_rows, layout, group):
+    """s*q + b (float64) of bank rows r0 .. r0+rows (4-bit, bf16 planes)."""
+    codes = np.asarray(bank["codes"], np.uint8).reshape(total_rows, cols // 2)[r0:r0 + rows]
+    q = np.empty((rows, cols), np.float64)
+    q[:, 0::2] = codes & 15
+    q[:, 1::2] = codes >> 4
+    G = cols // group
+    os_, gs_ = O.quant_strides(layout, total_rows, G, 1)
+    idx = (r0 + np.arange(rows))[:, None] * os_ + (np.arange(cols) // group)[None, :] * gs_
+    s = O.bf16_to_f32(np.asarray(bank["scales"], np.uint16)).astype(np.float64)[idx]
+    if bank["biases"] is None:
+        return s * q - 8.0 * s
+    return s * q + O.bf16_to_f32(np.asarray(bank["biases"], np.uint16)).astype(np.float64)[idx]
+
+
+def routed_magnitude(O, c, flags):
+    """Per output, sum over its routes of p_r * sum_i |w_down[n, i] * act_r[i]|,
+    with act_r the oracle's gated activation of route r (its up product
+    through MatmulCpuKernel and the gated SiLU, both restated in the oracle)."""
+    R, M, Hd, E, A = c["rows"], c["model"], c["hidden"], c["experts"], c["active"]
+    ids, w = O.moe_route(c["logits"], R, E, A, flags.get("rw", False), flags.get("rl", False))
+    if c["scales"] is not None:
+        O.moe_adjust_routes(ids, w, c["scales"], R, E, A, flags.get("si", False))
+    corr = 1 if c["up"]["biases"] is not None else 0
+    mag = np.zeros((R, M))
+    for r in range(R):
+        for k in range(A):
+            e = int(ids[r * A + k]) % E
+            up = c["up"]
+            rows = np.arange(e * 2 * Hd, (e + 1) * 2 * Hd, dtype=np.uint32)
+            st, proj = O.matmul(a=c["x"][r * M:(r + 1) * M], m=1, n=2 * Hd, k=M, codes=up["codes"],
+                                scales=up["scales"], correction=corr, correction_data=up["biases"],
+                                layout=c["layout"], row_count=E * 2 * Hd, group_count=M // c["group"], bits=4,
+                                group_size=c["group"], gather=rows, output_dt=H.BF16)
+            assert st == 0
+            act = np.abs(O.bf16_to_f32(O.gated_silu_bf16(proj, Hd, 1))).astype(np.float64)
+            wd = _dequant4(O, c["down"], e * M, M, Hd, E * M, c["layout"], c["group"])
+            mag[r] += abs(float(w[r * A + k])) * (np.abs(wd) @ act)
+    return mag
+
+
+def check_routed(O, c, got, want, flags):
+    """Parity bar of the routed pipeline. Each (token, rank) passes through the
+    reference's bf16 rounding points (value and gate rows of the up product,
+    the gated activation, the down product; routed.rs:208-239 writes bf16 at
+    each). The GPU's f32 sums differ from the oracle's sequential ones only in
+    summation order, but a sum that lands on the other side of a bf16 rounding
+    boundary moves that intermediate by one bf16 ulp (<= 2^-7 relative); a
+    flipped value or gate moves the activation by at most about 4 * 2^-7 of
+    itself. So every output is held to
+        max(1e-2 |want|, 2 bf16 ulps, 2^-5 * sum_r p_r sum_i |w_down act_r,i|)
+    the last term bounding what one-ulp flips of the bf16 intermediates can
+    move an output (it only exceeds the others where the down product
+    cancels), and at least 99% of the outputs must meet the north-star bar
+    max(1e-2 |want|, 2 bf16 ulps) outright."""
+    from tests.tolerances import bf16_ulp
+    R, M = c["rows"], c["model"]
+    want2, got2 = want.reshape(R, M).astype(np.float64), got.reshape(R, M).astype(np.float64)
+    base = np.maximum(1e-2 * np.abs(want2), 2 * bf16_ulp(want2))
+    mag = routed_magnitude(O, c, flags)
+    tol = np.maximum(base, 2.0 ** -5 * mag)
+    err = np.abs(got2 - want2)
+    bad = err > tol
+    assert not bad.any(), (f"{int(bad.sum())} of {bad.size} outside the bound; worst excess "
+                           f"{float((err - tol).max())}")
+    strict = float((err <= base).mean())
+    assert strict >= 0.99, f"only {strict:.4f} of outputs within 1e-2 rel / 2 bf16 ulp"
 
 
 @pytest.mark.parametrize("rows", [1, 3, 16, 40])
@@ -135,9 +193,11 @@ def test_routed_experts_route_paths(qmm, oracle, rows, experts, flags):
     routed_check(qmm, oracle, c, **flags)
 
 
-def test_routed_experts_qwen3_moe_geometry(qmm, oracle):
-    """Config-3 widths (H=2048, I=768, E=128, top-8) at one token."""
-    c = MC.case(oracle, 9, 1, model=2048, hidden=768, experts=128, active=8)
+@pytest.mark.parametrize("rows", [1, 4, 16])
+def test_routed_experts_qwen3_moe_geometry(qmm, oracle, rows):
+    """Config-3 widths (H=2048, I=768, E=128, top-8) at 1, 4 and 16 tokens:
+    the K=2048 grouped up kernels of every route-count class run."""
+    c = MC.case(oracle, 9 + rows, rows, model=2048, hidden=768, experts=128, active=8)
     routed_check(qmm, oracle, c)
 
 
