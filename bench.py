@@ -137,9 +137,24 @@ def build_layer_set(torch, Q, gen):
     return mats
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, layer, xs, budget_s=12.0):
-    """Single-thread oracle (MatmulCpuKernel restated) over whole layer-set
-    passes until ~budget_s of CPU time; returns GB/s of algorithmic bytes."""
+    """The oracle (MatmulCpuKernel::encode restated) on the host over whole
+    layer-set passes, for about budget_s of wall time per mode:
+      A: one thread, the reference CPU backend's single worker
+         (crates/stark-engine/src/backends/cpu/context.rs:26-30);
+      B: OpenMP over the output rows on every host core this process may use
+         (per-output arithmetic order unchanged, so bit-identical to A).
+    Returns GB/s of algorithmic bytes; mode B is the reported value."""
     import numpy as np
     from oracle import oracle as O
     O.lib()
@@ -148,21 +163,39 @@ def cpu_baseline(torch, layer, xs, budget_s=12.0):
         host.append(dict(n=mat["n"], k=mat["k"], codes=mat["codes"].cpu().numpy(),
                          s=mat["scales"].cpu().numpy().view(np.uint16), b=mat["biases"].cpu().numpy().view(np.uint16),
                          x=x.view(torch.int16).cpu().numpy().view(np.uint16)))
-    passes, bytes_done, t0 = 0, 0, time.perf_counter()
-    while True:
-        for h in host:
-            st, _ = O.matmul(a=h["x"], m=1, n=h["n"], k=h["k"], codes=h["codes"], scales=h["s"],
-                             correction_data=h["b"], layout=O.GROUP_OUTPUT, bits=4, group_size=GROUP,
-                             output_dt=O.BF16)
-            assert st == 0
-        passes += 1
-        bytes_done += algorithmic_bytes(1)
-        el = time.perf_counter() - t0
-        if el >= budget_s or passes >= 50:
-            break
-    return dict(value=bytes_done / el / 1e9, unit="GB/s", cores=1, kind="port",
-                sample=f"{passes} full passes over one Qwen3-8B W4 layer matvec set (M=1), single thread, "
-                       f"oracle restatement of MatmulCpuKernel::encode, {el:.1f} s")
+
+    def run(threads):
+        passes, bytes_done, t0 = 0, 0, time.perf_counter()
+        outs = []
+        while True:
+            outs = []
+            for h in host:
+                st, y = O.matmul(a=h["x"], m=1, n=h["n"], k=h["k"], codes=h["codes"], scales=h["s"],
+                                 correction_data=h["b"], layout=O.GROUP_OUTPUT, bits=4, group_size=GROUP,
+                                 output_dt=O.BF16, threads=threads)
+                assert st == 0
+                outs.append(np.asarray(y).copy())
+            passes += 1
+            bytes_done += algorithmic_bytes(1)
+            el = time.perf_counter() - t0
+            if el >= budget_s or passes >= 400:
+                return bytes_done / el / 1e9, passes, el, outs
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    a_gbs, a_passes, a_el, a_out = run(0)
+    b_gbs, b_passes, b_el, b_out = run(cores)
+    assert all(np.array_equal(u, v) for u, v in zip(a_out, b_out)), "mode B must be bit-identical to mode A"
+    return dict(value=round(b_gbs, 4), unit="GB/s", cores=cores, kind="port",
+                cpu_model=_cpu_model(),
+                single_thread=dict(value=round(a_gbs, 4), cores=1,
+                                   sample=f"{a_passes} passes, {a_el:.1f} s"),
+                sample=f"mode B: {b_passes} full passes over one Qwen3-8B W4 layer matvec set (M=1) with OpenMP "
+                       f"over output rows on {cores} threads, {b_el:.1f} s; oracle restatement of "
+                       f"MatmulCpuKernel::encode, bit-identical to the single-thread mode A")
 
 
 def copy_calibration(torch, mib=256):
@@ -210,6 +243,19 @@ def config1(args, torch, Q):
     if args.calibrate_copy:
         copy_calibration(torch)
 
+    # setup, outside the timed region: one pass over every copy (first touch of
+    # all 3.9 GB), checking the property that copies of the same weights give
+    # bit-identical outputs
+    ref = None
+    for i in range(args.copies):
+        kern.encode_prepared(all_args[i], stream)
+        got = torch.cat([o.clone() for o in outs])
+        if ref is None:
+            ref = got
+        elif not torch.equal(got, ref):
+            raise SystemExit(f"bench: layer copy {i} gave different outputs from copy 0")
+    torch.cuda.synchronize()
+
     for i in range(args.warmup):
         kern.encode_prepared(all_args[i % args.copies], stream)
     torch.cuda.synchronize()
@@ -246,6 +292,10 @@ def config1(args, torch, Q):
         hit = re.search(r"hbm_bytes_per_launch\s*=\s*(\d+)", open(tfile).read())
         traffic = int(hit.group(1)) if hit else None
 
+    decode = None
+    if args.decode_tokens:
+        decode = decode_measure(args, torch)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(torch, layer0, x_list)
@@ -268,7 +318,7 @@ def config1(args, torch, Q):
                         f"{args.copies} rotating layer copies; one stark_qmm_encode_many launch per step",
             "bytes_per_step": bytes_step,
             "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
-            "matvec_decode_tokens_per_s_36_layers": round(1000.0 / (ms_step * LAYERS), 1),
+            "matvec_only_layer_sets_per_s_over_36": round(1000.0 / (ms_step * LAYERS), 1),
             "launch_ms_median": round(launch_ms[len(launch_ms) // 2], 5),
         },
         "roofline": {
@@ -282,6 +332,9 @@ def config1(args, torch, Q):
         },
         "cpu_baseline": cpu,
     }
+    if decode is not None:
+        line["config"]["decode_tokens_per_s"] = decode["tokens_per_s"]
+        line["config"]["decode"] = decode
     print(json.dumps(line))
     if args.verify:
         verify_lines(args, torch, Q, gen, kern, layers, stream)
@@ -497,12 +550,12 @@ def config4(args, torch, Q):
         decode_line(args, torch)
 
 
-def decode_line(args, torch):
+def decode_measure(args, torch):
     """Config 4 (decode part): random-init Qwen3-8B architecture (36 layers,
     32/8 heads of 128, intermediate 12288, vocab 151936; W4 g64 projections,
     W8 g64 lm_head, bf16 KV cache), a 4096-token context whose KV rows are
     synthetic N(0,1), then greedy tokens generated one HIP-graph replay each.
-    Value: generated tokens per second over the timed tokens."""
+    Returns generated tokens per second over the timed tokens and the bytes."""
     from stark_amd import decode as DEC
     cfg = DEC.Qwen3Config()
     ctx, gen_tokens = 4096, args.decode_tokens
@@ -526,23 +579,34 @@ def decode_line(args, torch):
     ms = a.elapsed_time(b) / timed_tokens
     assert int(m.pos.item()) == ctx + gen_tokens, "device position did not advance once per token"
     tps = 1000.0 / ms
-    H, I, hd = cfg.hidden, cfg.intermediate, cfg.head_dim
+    H, hd = cfg.hidden, cfg.head_dim
     layer_bytes = algorithmic_bytes()
     lm_bytes = cfg.vocab * H * (1 + 4 / GROUP) + H * 2 + cfg.vocab * 4
     mid = ctx + gen_tokens // 2
     kv_bytes = cfg.layers * 2 * cfg.kv_heads * mid * hd * 2
     per_token = cfg.layers * layer_bytes + lm_bytes + kv_bytes + H * 2
     gbs = per_token * tps / 1e9
-    print(json.dumps({"metric": "Qwen3-8B W4 end-to-end greedy decode tokens/s", "value": round(tps, 1),
-                      "unit": "tokens/s", "n_gpus": 1, "steps": timed_tokens, "warmup": warm + 1,
-                      "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-                      "dtype": "bf16",
+    del graph, m
+    torch.cuda.empty_cache()
+    return dict(tokens_per_s=round(tps, 1), ms_per_token=round(ms, 5), timed_tokens=timed_tokens,
+                workload=f"config 4 decode: {gen_tokens} greedy tokens after a {ctx}-token context, 36 layers, "
+                         "vocab 151936 (W8 lm_head), one HIP graph replay per token",
+                hbm_bytes_per_token_algorithmic=per_token, achieved_gbs=round(gbs, 1),
+                frac_of_hbm_peak=round(gbs / PEAK_HBM_GBS, 4))
+
+
+def decode_line(args, torch):
+    d = decode_measure(args, torch)
+    gbs = d["achieved_gbs"]
+    print(json.dumps({"metric": "Qwen3-8B W4 end-to-end greedy decode tokens/s", "value": d["tokens_per_s"],
+                      "unit": "tokens/s", "n_gpus": 1, "steps": d["timed_tokens"], "warmup": 4,
+                      "ms_per_step": d["ms_per_token"], "higher_is_better": True, "scaling": "weak",
+                      "vs_baseline": None, "dtype": "bf16",
                       "data": "synthetic: random-init weights (W4 g64, W8 g64 lm_head), KV of a 4096-token context "
                               "filled N(0,1), uniform random prompt token",
-                      "config": {"workload": f"config 4 decode: {gen_tokens} greedy tokens after a {ctx}-token "
-                                             "context, one HIP graph replay per token",
-                                 "hbm_bytes_per_token_algorithmic": per_token},
-                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                      "config": {"workload": d["workload"],
+                                 "hbm_bytes_per_token_algorithmic": d["hbm_bytes_per_token_algorithmic"]},
+                      "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
 
 
@@ -556,7 +620,8 @@ def main():
                          "4: prefill dequant-GEMM at M=2048")
     ap.add_argument("--tokens", type=int, nargs="+", default=[1, 4, 16], help="config 3 tokens per step")
     ap.add_argument("--decode-tokens", type=int, default=256,
-                    help="config 4: greedy tokens generated after the 4096-token context (0 skips the decode line)")
+                    help="configs 1 and 4: greedy tokens generated after the 4096-token context in the end-to-end "
+                         "decode measurement (0 skips it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verify", action="store_true",
                     help="config 1: also print the M = 2, 4, 8, 16 (speculative verify) lines")

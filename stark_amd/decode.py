@@ -174,29 +174,43 @@ class Qwen3Decoder:
         self.pos.fill_(length)
         self.token.fill_(int(torch.randint(0, self.cfg.vocab, (1,), generator=gen, device=self.x.device).item()))
 
-    def step(self, stream=None):
+    def step(self, stream=None, trace=None):
         """One greedy token: embed the current token, run every layer at the
-        current position, lm_head, argmax; advances the device position."""
+        current position, lm_head, argmax; advances the device position.
+        trace(layer, stage), when given, is called after each launch (eager
+        use only: tests snapshot the activations there)."""
+        t = trace if trace is not None else (lambda layer, stage: None)
         cfg, D = self.cfg, lib()
         s = stream if stream is not None else torch.cuda.current_stream()
         sp = C.c_void_p(s.cuda_stream)
         H, I = cfg.hidden, cfg.intermediate
         p = lambda t: C.c_void_p(t.data_ptr())
         _ok(D.stark_decode_embed(p(self.embed), p(self.token), p(self.x), H, cfg.vocab, sp), "embed")
-        for L, B in zip(self.layers, self.batches):
+        t(-1, "embed")
+        for i, (L, B) in enumerate(zip(self.layers, self.batches)):
             _ok(D.stark_decode_rms_norm(p(self.x), p(L["attn_norm"]), p(self.h), H, cfg.eps, sp), "attn_norm")
+            t(i, "attn_norm")
             self.kern4.encode_prepared(B["qkv"], s)
+            t(i, "qkv")
             # q/k norm + RoPE, KV write and attention partials in one launch, then the chunk reduction
             _ok(D.stark_decode_attention_fused(p(self.q), p(self.k), p(self.v), p(L["q_norm"]), p(L["k_norm"]),
                                                p(L["kcache"]), p(L["vcache"]), p(self.po), p(self.pml), p(self.attn), p(self.pos), cfg.q_heads, cfg.kv_heads, self.cap,
                                                cfg.rope_theta, cfg.eps, sp), "attention")
+            t(i, "attention")
             self.kern4.encode_prepared(B["o"], s)
+            t(i, "o")
             _ok(D.stark_decode_rms_norm(p(self.x), p(L["mlp_norm"]), p(self.h), H, cfg.eps, sp), "mlp_norm")
+            t(i, "mlp_norm")
             self.kern4.encode_prepared(B["gu"], s)
+            t(i, "gate_up")
             _ok(D.stark_decode_silu_mul(p(self.g), p(self.u), p(self.a), I, sp), "silu_mul")
+            t(i, "silu_mul")
             self.kern4.encode_prepared(B["down"], s)
+            t(i, "down")
         _ok(D.stark_decode_rms_norm(p(self.x), p(self.final_norm), p(self.h), H, cfg.eps, sp), "final_norm")
+        t(-1, "final_norm")
         self.kern_lm.encode_prepared(self.lm_batch, s)
+        t(-1, "lm_head")
         _ok(D.stark_decode_argmax(p(self.logits), cfg.vocab, p(self.token), p(self.pos), p(self.history),
                              self.history.numel(), sp),
             "argmax")
