@@ -361,7 +361,9 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <bool SIGNED>
+// BF: bf16 planes (else f16); BIASED: bias plane (else symmetric). Both are
+// compile-time so that the per-unit plane conversion is straight-line code.
+template <bool SIGNED, bool BF, bool BIASED>
 __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void qmv_stream(AffineBatch batch, Schedule sched) {
     (void)batch;
     constexpr uint32_t UB = kUnitK / 2;    // bytes of a row per unit
@@ -403,8 +405,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         const size_t off = op.os == 1 ? (size_t)(c * 16 + ((lane >> 2) & 15)) * op.gs + n0 + 8 * (lane & 3)
                                       : (size_t)(n0 + ((lane >> 1) & 31)) * op.os + c * 16 + 8 * (lane & 1);
         pls = buf_load(rsrc(op.scales, PLANE), (uint32_t)off * 2);
-        plb = buf_load(rsrc(op.corr, PLANE),
-                       op.corr_kind == STARK_QMM_CORRECTION_BIASES ? (uint32_t)off * 2 : OOB);
+        plb = buf_load(rsrc(op.corr, PLANE), BIASED ? (uint32_t)off * 2 : OOB);
     };
     const auto code_rsrc = [&](const AffineOp& op, uint32_t n0) {
         return rsrc(op.codes + (size_t)n0 * (op.k / 2), kTR * (op.k / 2));
@@ -473,15 +474,14 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             tg2 = rg == 2 ? tag : tg2;
         }
         {  // plane vectors -> f32 (scale, bias term) pairs at [row][group]
-            const bool bf = op.w_dt == STARK_QMM_BF16, biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
             float sv[8], bv[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 const uint32_t hs = (pls[q >> 1] >> (16 * (q & 1))) & 0xffffu;
                 const uint32_t hb = (plb[q >> 1] >> (16 * (q & 1))) & 0xffffu;
-                const float sc = plane_f32(hs, bf);
+                const float sc = plane_f32(hs, BF);
                 sv[q] = sc;
-                bv[q] = biased ? plane_f32(hb, bf) : -8.0f * sc;
+                bv[q] = BIASED ? plane_f32(hb, BF) : -8.0f * sc;
             }
             float2* pw = (float2*)lds.pl[wave];
             if (op.os == 1) {  // lane = (group, rows 8*quarter ..)
@@ -620,8 +620,8 @@ bool stream_eligible(const AffineOp* ops, uint32_t count) {
     return count > 0;
 }
 
-template <bool SIGNED>
-stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t stream) {
+template <bool SIGNED, bool BF, bool BIASED>
+stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipStream_t stream) {
     std::vector<AffineOp> sorted(ops, ops + count);
     std::stable_sort(sorted.begin(), sorted.end(), [](const AffineOp& a, const AffineOp& b) { return a.k > b.k; });
     AffineBatch batch{};
@@ -633,7 +633,7 @@ stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t 
     batch.count = count;
     batch.total = tiles;
     if (tiles == 0) return STARK_QMM_OK;
-    auto kern = qmv_stream<SIGNED>;
+    auto kern = qmv_stream<SIGNED, BF, BIASED>;
     int dev = 0, cus = 0;
     QMM_HIP_CHECK(hipGetDevice(&dev));
     QMM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
@@ -646,6 +646,27 @@ stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t 
     if (st != STARK_QMM_OK) return st;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(kWg), 0, stream, batch, sched);
     QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
+
+// One streaming launch per (plane type, correction) class of the batch.
+template <bool SIGNED>
+stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t stream) {
+    std::vector<AffineOp> cls[2][2];
+    for (uint32_t i = 0; i < count; ++i)
+        cls[ops[i].w_dt == STARK_QMM_BF16][ops[i].corr_kind == STARK_QMM_CORRECTION_BIASES].push_back(ops[i]);
+    for (int bf = 0; bf < 2; ++bf)
+        for (int bi = 0; bi < 2; ++bi) {
+            const std::vector<AffineOp>& v = cls[bf][bi];
+            if (v.empty()) continue;
+            const uint32_t n = (uint32_t)v.size();
+            const stark_qmm_status st =
+                bf ? (bi ? launch_stream_planes<SIGNED, true, true>(v.data(), n, stream)
+                         : launch_stream_planes<SIGNED, true, false>(v.data(), n, stream))
+                   : (bi ? launch_stream_planes<SIGNED, false, true>(v.data(), n, stream)
+                         : launch_stream_planes<SIGNED, false, false>(v.data(), n, stream));
+            if (st != STARK_QMM_OK) return st;
+        }
     return STARK_QMM_OK;
 }
 
