@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define STARK_QMM_ABI_VERSION 1u
+#define STARK_QMM_ABI_VERSION 2u
 
 /* The library is built with hidden visibility; only these entry points are exported. */
 #if defined(__GNUC__)
@@ -67,12 +67,26 @@ enum {
     /* MatmulError::BackendError (error.rs:29-30): a HIP call failed */
     STARK_QMM_DEVICE_FAILURE = 10,
     /* caller workspace smaller than the size query returned */
-    STARK_QMM_WORKSPACE_TOO_SMALL = 11
+    STARK_QMM_WORKSPACE_TOO_SMALL = 11,
+    /* ParameterLoaderError::KeyNotFound (src/parameters/error.rs:11-12) */
+    STARK_QMM_KEY_NOT_FOUND = 12,
+    /* ParameterLoaderError::InvalidTensor / InvalidTensorSize (error.rs:19-32) */
+    STARK_QMM_INVALID_TENSOR = 13,
+    /* ParameterLoaderError::HeaderLoadingError (src/parameters/safetensors_metadata.rs:14-39) */
+    STARK_QMM_HEADER_ERROR = 14,
+    /* ParameterLoaderError::ArrayLoadingError: the file could not be read (error.rs:15-16) */
+    STARK_QMM_IO_ERROR = 15,
+    /* WeightMatrixError::UnsupportedConfiguration (src/encodable_block/weight_matrix.rs:22-28) */
+    STARK_QMM_UNSUPPORTED_CONFIGURATION = 16
 };
 
 /* Data types. The numbers are the GGUF kind ids the hybrid engine already uses
  * for plane dtypes (src/engine/hybrid/weight_metal.rs:486-490). */
 enum { STARK_QMM_F32 = 0, STARK_QMM_F16 = 1, STARK_QMM_BF16 = 30 };
+/* Integer tensor types of a weight file; the first four are the hybrid
+ * engine's private tags (src/engine/hybrid/weights.rs:93-96). */
+enum { STARK_QMM_U32 = 101, STARK_QMM_I64 = 102, STARK_QMM_I32 = 103, STARK_QMM_U8 = 104, STARK_QMM_I8 = 105,
+       STARK_QMM_U64 = 106 };
 
 /* QuantParamsLayout (src/backends/common/kernel/matmul/mod.rs:19-25). */
 enum { STARK_QMM_LAYOUT_OUTPUT_GROUP = 0, /* [N, G] */
@@ -287,6 +301,88 @@ STARK_QMM_API stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_a
  * (different streams, or threads) race; serialize them. Allocates nothing. */
 #define STARK_QMM_ROUTED_STATIC_SCRATCH_BYTES (8ull << 20)
 STARK_QMM_API stark_qmm_status stark_qmm_routed_experts_static(const stark_qmm_routed_args* args, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Weight files: Stark's converted artifact (model.safetensors) and      */
+/* GGUF v3 checkpoints                                                    */
+/* ------------------------------------------------------------------ */
+
+/* Detail text of the last failing weight-file call on this thread (never NULL). */
+STARK_QMM_API const char* stark_qmm_last_error(void);
+
+typedef struct stark_qmm_file stark_qmm_file;
+enum { STARK_QMM_FILE_SAFETENSORS = 0, STARK_QMM_FILE_GGUF = 1 };
+
+typedef struct stark_qmm_tensor_info {
+    uint32_t dtype;      /* safetensors: STARK_QMM_F32 .. STARK_QMM_U64; GGUF: the GGML kind (8 = Q8_0, 12 = Q4_K, ...) */
+    uint32_t rank;
+    uint64_t shape[8];   /* outermost first (GGUF dimensions reversed, as weights.rs:2823 does) */
+    uint64_t offset;     /* byte offset of the payload in its file */
+    uint64_t size;       /* payload bytes */
+    const void* host;    /* read-only mapping of the payload, valid until stark_qmm_file_close */
+} stark_qmm_tensor_info;
+
+/* Opens a weight file. A `.safetensors` file is indexed as ParameterLoader::new
+ * does (src/parameters/loader.rs:80-127; header read_metadata,
+ * src/parameters/safetensors_metadata.rs:113-128). A `.gguf` file, or a
+ * directory of `.gguf` split files, is read as the hybrid engine's
+ * Weights::open / read_gguf (src/engine/hybrid/weights.rs:815-895, 2770-2865):
+ * version 3, alignment, block sizes, overlap and split completeness checked.
+ * Files are mapped read-only; nothing is copied until an upload. */
+STARK_QMM_API stark_qmm_status stark_qmm_file_open(const char* path, stark_qmm_file** out);
+STARK_QMM_API void stark_qmm_file_close(stark_qmm_file* file);
+STARK_QMM_API uint32_t stark_qmm_file_kind(const stark_qmm_file* file);
+STARK_QMM_API uint64_t stark_qmm_file_tensor_count(const stark_qmm_file* file);
+/* Tensor names in sorted order; NULL past the end. */
+STARK_QMM_API const char* stark_qmm_file_tensor_name(const stark_qmm_file* file, uint64_t index);
+STARK_QMM_API stark_qmm_status stark_qmm_file_tensor(const stark_qmm_file* file, const char* name,
+                                                     stark_qmm_tensor_info* info);
+/* Metadata value as text (safetensors __metadata__ strings; GGUF values, arrays as [a,b,...]). */
+STARK_QMM_API stark_qmm_status stark_qmm_file_metadata(const stark_qmm_file* file, const char* key, const char** value);
+/* Copies one tensor's payload to new device memory (hipMalloc; free with
+ * stark_qmm_device_free): GGUF block matrices then feed stark_qmm_mapped_many. */
+STARK_QMM_API stark_qmm_status stark_qmm_file_upload(const stark_qmm_file* file, const char* name, void** device,
+                                                     void* stream);
+STARK_QMM_API stark_qmm_status stark_qmm_device_free(void* device);
+
+/* AnyWeightMatrixSpec (src/config/weight_matrix/): FullPrecisionSpec, MLXSpec
+ * (mlx_spec.rs:5-13) and IntSpec; Layout OutputInput / InputOutput. */
+enum { STARK_QMM_SPEC_FULL_PRECISION = 0, STARK_QMM_SPEC_MLX = 1, STARK_QMM_SPEC_INT = 2 };
+enum { STARK_QMM_WEIGHT_OUTPUT_INPUT = 0, STARK_QMM_WEIGHT_INPUT_OUTPUT = 1 };
+typedef struct stark_qmm_weight_spec {
+    uint32_t struct_size;   /* sizeof(stark_qmm_weight_spec) */
+    uint32_t kind;          /* STARK_QMM_SPEC_* */
+    uint32_t bits, group_size;
+    uint32_t layout;        /* STARK_QMM_WEIGHT_* */
+    uint32_t is_symmetric;  /* IntSpec */
+    uint32_t materialize_affine_input_sum;  /* MLXSpec */
+    /* QuantParams::with_source_output_widths (src/backends/common/kernel/matmul/mod.rs:78-92):
+     * consecutive row spans of a fused matrix (q/k/v, gate/up); count 0 = one source */
+    uint32_t source_output_widths[4];
+    uint32_t source_output_count;
+} stark_qmm_weight_spec;
+
+typedef struct stark_qmm_weight_matrix {
+    uint32_t struct_size;   /* sizeof(stark_qmm_weight_matrix), set by the caller */
+    stark_qmm_b b;          /* ready for stark_qmm_args.b (device pointers owned by this struct) */
+    uint32_t rows, columns; /* physical shape */
+    uint32_t source_output_widths[4];
+    uint32_t source_output_count;
+    void* device[3];        /* weights, scales, biases / zero points */
+} stark_qmm_weight_matrix;
+
+/* Replaces WeightMatrix::load (src/encodable_block/weight_matrix.rs:114-216)
+ * on the artifact's `<prefix>.weights`, `.scales`, `.biases` / `.zero_points`:
+ * the same spec checks (parse_spec, :53-96), shapes, dtypes and byte sizes
+ * (ParameterLeaf::validate, src/parameters/loader.rs:272-305), then copies
+ * the tensors to the device (load time: allocates, and waits for the copy).
+ * Output-input matrices get group-output planes [G, roundup4(N)], input-output
+ * matrices output-group planes [N, G]. */
+STARK_QMM_API stark_qmm_status stark_qmm_weight_matrix_load(const stark_qmm_file* file, const char* prefix,
+                                                            const stark_qmm_weight_spec* spec, uint32_t required_layout,
+                                                            uint32_t output_dim, uint32_t input_dim, uint32_t data_type,
+                                                            stark_qmm_weight_matrix* out, void* stream);
+STARK_QMM_API void stark_qmm_weight_matrix_free(stark_qmm_weight_matrix* matrix);
 
 #ifdef __cplusplus
 }

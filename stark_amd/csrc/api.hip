@@ -109,6 +109,11 @@ const char* stark_qmm_status_string(stark_qmm_status s) {
     case STARK_QMM_OUT_OF_MEMORY: return "out of memory";
     case STARK_QMM_DEVICE_FAILURE: return "device failure";
     case STARK_QMM_WORKSPACE_TOO_SMALL: return "workspace too small";
+    case STARK_QMM_KEY_NOT_FOUND: return "key not found";
+    case STARK_QMM_INVALID_TENSOR: return "invalid tensor";
+    case STARK_QMM_HEADER_ERROR: return "header loading error";
+    case STARK_QMM_IO_ERROR: return "failed to read data";
+    case STARK_QMM_UNSUPPORTED_CONFIGURATION: return "unsupported weight matrix configuration";
     default: return "unknown status";
     }
 }

@@ -29,6 +29,7 @@ LIB_PATH = os.environ.get("QMM_LIB_OVERRIDE") or os.path.join(HERE, "libstark_qm
 
 # ---------------------------------------------------------------- constants
 
+ABI_VERSION = 2
 OK = 0
 INVALID_ARGUMENT = 1
 ABI_MISMATCH = 2
@@ -41,8 +42,14 @@ UNSUPPORTED = 8
 OUT_OF_MEMORY = 9
 DEVICE_FAILURE = 10
 WORKSPACE_TOO_SMALL = 11
+KEY_NOT_FOUND = 12
+INVALID_TENSOR = 13
+HEADER_ERROR = 14
+IO_ERROR = 15
+UNSUPPORTED_CONFIGURATION = 16
 
 F32, F16, BF16 = 0, 1, 30
+U32, I64, I32, U8, I8, U64 = 101, 102, 103, 104, 105, 106
 OUTPUT_GROUP, GROUP_OUTPUT = 0, 1
 SYMMETRIC, BIASES, ZERO_POINTS = 0, 1, 2
 MODE_U4, MODE_I8, MODE_U8, MODE_U5, MODE_U6, MODE_U3 = 0, 1, 2, 3, 4, 5
@@ -105,6 +112,23 @@ class _RoutedArgs(C.Structure):
                 ("sort_expert_ids", C.c_uint32), ("workspace", C.c_void_p), ("workspace_size", C.c_uint64)]
 
 
+class _TensorInfo(C.Structure):
+    _fields_ = [("dtype", C.c_uint32), ("rank", C.c_uint32), ("shape", C.c_uint64 * 8), ("offset", C.c_uint64),
+                ("size", C.c_uint64), ("host", C.c_void_p)]
+
+
+class _WeightSpec(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("kind", C.c_uint32), ("bits", C.c_uint32), ("group_size", C.c_uint32),
+                ("layout", C.c_uint32), ("is_symmetric", C.c_uint32), ("materialize_affine_input_sum", C.c_uint32),
+                ("source_output_widths", C.c_uint32 * 4), ("source_output_count", C.c_uint32)]
+
+
+class _WeightMatrix(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("b", _B), ("rows", C.c_uint32), ("columns", C.c_uint32),
+                ("source_output_widths", C.c_uint32 * 4), ("source_output_count", C.c_uint32),
+                ("device", C.c_void_p * 3)]
+
+
 # Every symbol include/stark_qmm.h declares, with its ctypes signature.
 SIGNATURES = {
     "stark_qmm_abi_version": (C.c_uint32, []),
@@ -129,6 +153,20 @@ SIGNATURES = {
     "stark_qmm_routed_experts_workspace_size": (C.c_uint64, [C.c_uint32] * 5),
     "stark_qmm_routed_experts": (C.c_uint32, [C.POINTER(_RoutedArgs), C.c_void_p]),
     "stark_qmm_routed_experts_static": (C.c_uint32, [C.POINTER(_RoutedArgs), C.c_void_p]),
+    "stark_qmm_last_error": (C.c_char_p, []),
+    "stark_qmm_file_open": (C.c_uint32, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "stark_qmm_file_close": (None, [C.c_void_p]),
+    "stark_qmm_file_kind": (C.c_uint32, [C.c_void_p]),
+    "stark_qmm_file_tensor_count": (C.c_uint64, [C.c_void_p]),
+    "stark_qmm_file_tensor_name": (C.c_char_p, [C.c_void_p, C.c_uint64]),
+    "stark_qmm_file_tensor": (C.c_uint32, [C.c_void_p, C.c_char_p, C.POINTER(_TensorInfo)]),
+    "stark_qmm_file_metadata": (C.c_uint32, [C.c_void_p, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "stark_qmm_file_upload": (C.c_uint32, [C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p), C.c_void_p]),
+    "stark_qmm_device_free": (C.c_uint32, [C.c_void_p]),
+    "stark_qmm_weight_matrix_load": (C.c_uint32, [C.c_void_p, C.c_char_p, C.POINTER(_WeightSpec), C.c_uint32,
+                                                  C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(_WeightMatrix),
+                                                  C.c_void_p]),
+    "stark_qmm_weight_matrix_free": (None, [C.POINTER(_WeightMatrix)]),
 }
 
 _lib = None
@@ -150,7 +188,7 @@ def lib():
             fn = getattr(l, name)
             fn.restype = res
             fn.argtypes = args
-        if l.stark_qmm_abi_version() != 1:
+        if l.stark_qmm_abi_version() != ABI_VERSION:
             raise RuntimeError("libstark_qmm ABI mismatch")
         _lib = l
     return _lib
@@ -235,6 +273,9 @@ class MatmulArguments:
 
 
 def _fill_b(dst: _B, b) -> None:
+    if isinstance(b, LoadedB):
+        C.memmove(C.byref(dst), C.byref(b.raw), C.sizeof(_B))
+        return
     if isinstance(b, FullPrecisionB):
         dst.values = _ptr(b.values)
         dst.codes = None
@@ -495,3 +536,168 @@ def routed_experts_prepared(prepared, stream=None) -> None:
     """Issue a routed_experts call whose arguments were marshalled with
     routed_experts(..., prepare_only=True)."""
     _check(lib().stark_qmm_routed_experts(C.byref(prepared[0]), _stream(stream)), "routed_experts")
+
+
+# ---------------------------------------------------------------- weight files
+
+class WeightFileError(MatmulError):
+    """A weight-file call failed: status plus the library's detail text."""
+
+    def __init__(self, status: int, where: str, detail: str):
+        super().__init__(status, f"{where}: {detail}")
+        self.detail = detail
+
+
+def _wcheck(status: int, where: str):
+    if status != OK:
+        raise WeightFileError(status, where, lib().stark_qmm_last_error().decode())
+
+
+class DeviceBuffer:
+    """Device memory returned by the library (stark_qmm_file_upload); usable
+    wherever the mirror takes a device tensor (its bytes as uint8 elements)."""
+    is_cuda = True
+
+    def __init__(self, ptr: int, nbytes: int):
+        self._ptr, self._n = ptr, nbytes
+
+    def data_ptr(self) -> int:
+        return self._ptr
+
+    def numel(self) -> int:
+        return self._n
+
+    def element_size(self) -> int:
+        return 1
+
+    def free(self) -> None:
+        if self._ptr:
+            lib().stark_qmm_device_free(C.c_void_p(self._ptr))
+            self._ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class TensorInfo:
+    dtype: int
+    shape: tuple
+    offset: int
+    size: int
+    host: int  # address of the read-only mapping
+
+
+class WeightFile:
+    """stark_qmm_file: a Stark artifact (.safetensors, as ParameterLoader) or a
+    GGUF v3 file / split directory (as the hybrid Weights::open)."""
+    SAFETENSORS, GGUF = 0, 1
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        _wcheck(lib().stark_qmm_file_open(os.fsencode(path), C.byref(h)), "open")
+        self._h = h
+
+    @property
+    def kind(self) -> int:
+        return lib().stark_qmm_file_kind(self._h)
+
+    def names(self) -> list:
+        n = lib().stark_qmm_file_tensor_count(self._h)
+        return [lib().stark_qmm_file_tensor_name(self._h, i).decode() for i in range(n)]
+
+    def tensor(self, name: str) -> TensorInfo:
+        info = _TensorInfo()
+        _wcheck(lib().stark_qmm_file_tensor(self._h, name.encode(), C.byref(info)), f"tensor {name}")
+        return TensorInfo(info.dtype, tuple(info.shape[:info.rank]), info.offset, info.size, info.host or 0)
+
+    def host_bytes(self, name: str) -> bytes:
+        t = self.tensor(name)
+        return C.string_at(t.host, t.size)
+
+    def metadata(self, key: str) -> str:
+        v = C.c_char_p()
+        _wcheck(lib().stark_qmm_file_metadata(self._h, key.encode(), C.byref(v)), f"metadata {key}")
+        return v.value.decode()
+
+    def upload(self, name: str, stream=None) -> DeviceBuffer:
+        d = C.c_void_p()
+        _wcheck(lib().stark_qmm_file_upload(self._h, name.encode(), C.byref(d), _stream(stream)), f"upload {name}")
+        return DeviceBuffer(d.value, self.tensor(name).size)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().stark_qmm_file_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+SPEC_FULL_PRECISION, SPEC_MLX, SPEC_INT = 0, 1, 2
+OUTPUT_INPUT, INPUT_OUTPUT = 0, 1
+
+
+@dataclass
+class WeightMatrixSpec:
+    """AnyWeightMatrixSpec: kind SPEC_FULL_PRECISION / SPEC_MLX / SPEC_INT."""
+    kind: int
+    bits: int = 4
+    group_size: int = 64
+    layout: int = OUTPUT_INPUT
+    is_symmetric: bool = False
+    materialize_affine_input_sum: bool = False
+    source_output_widths: Sequence[int] = ()
+
+
+class LoadedB:
+    """The stark_qmm_b of a loaded weight matrix (device memory owned by the
+    WeightMatrix that produced it)."""
+
+    def __init__(self, raw: _B, owner):
+        self.raw, self.owner = raw, owner
+
+
+class WeightMatrix:
+    """WeightMatrix::load (weight_matrix.rs:114-216) through
+    stark_qmm_weight_matrix_load; `.b` goes into MatmulArguments."""
+
+    def __init__(self, file: WeightFile, prefix: str, spec: WeightMatrixSpec, required_layout: int,
+                 output_dim: int, input_dim: int, data_type: int, stream=None):
+        s = _WeightSpec()
+        s.struct_size = C.sizeof(_WeightSpec)
+        s.kind, s.bits, s.group_size, s.layout = spec.kind, spec.bits, spec.group_size, spec.layout
+        s.is_symmetric = int(spec.is_symmetric)
+        s.materialize_affine_input_sum = int(spec.materialize_affine_input_sum)
+        w = list(spec.source_output_widths)
+        s.source_output_count = len(w)
+        for i, v in enumerate(w[:4]):
+            s.source_output_widths[i] = v
+        m = _WeightMatrix()
+        m.struct_size = C.sizeof(_WeightMatrix)
+        st = lib().stark_qmm_weight_matrix_load(file._h, prefix.encode(), C.byref(s), required_layout, output_dim,
+                                                input_dim, data_type, C.byref(m),
+                                                None if stream is None and not torch.cuda.is_available()
+                                                else _stream(stream))
+        _wcheck(st, f"WeightMatrix::load {prefix}")
+        self._m = m
+        self.rows, self.columns = m.rows, m.columns
+        self.source_output_widths = tuple(m.source_output_widths[:m.source_output_count])
+        self.b = LoadedB(m.b, self)
+
+    def free(self) -> None:
+        if getattr(self, "_m", None) is not None:
+            lib().stark_qmm_weight_matrix_free(C.byref(self._m))
+            self._m = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -48,8 +48,8 @@ def test_library_exports_only_the_c_abi():
 
 def test_abi_version_and_status_strings():
     from stark_amd import qmm
-    assert qmm.lib().stark_qmm_abi_version() == 1
-    for s in range(12):
+    assert qmm.lib().stark_qmm_abi_version() == qmm.ABI_VERSION == 2
+    for s in range(17):
         assert qmm.status_string(s) and qmm.status_string(s) != "unknown status"
     assert qmm.status_string(999) == "unknown status"
 
