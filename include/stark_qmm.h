@@ -137,16 +137,35 @@ typedef struct stark_qmm_d_ops {
     float ab_scale;           /* 1.0 for none */
     uint32_t accumulate;      /* d = ... + d */
     const void* bias;         /* [N] in the weights dtype, or NULL */
-    const void* rht_factors;  /* output RHT: must be NULL (STARK_QMM_UNSUPPORTED_D_OP) */
+    /* int32 signs [N]: output RHT (32-point Walsh-Hadamard of each 32 outputs
+     * of a row, times the signs), applied to d after the product, then the
+     * bias (kernel.rs:167, 287-300). F32 / BF16 outputs with N % 32 == 0;
+     * otherwise STARK_QMM_UNSUPPORTED_D_OP. */
+    const void* rht_factors;
     uint32_t has_soft_cap;
     float soft_cap;
 } stark_qmm_d_ops;
 
 /* MatmulArguments (src/backends/common/kernel/matmul/arguments.rs:7-25). */
+/* MatmulA (src/backends/common/kernel/matmul/matmul_a.rs:51-61) and
+ * Int8CodeLayout (matmul_a.rs:6-9). */
+enum { STARK_QMM_A_FULL_PRECISION = 0, STARK_QMM_A_INT8_SYMMETRIC = 1 };
+enum { STARK_QMM_CODES_SEQUENTIAL = 0, STARK_QMM_CODES_GROUPED_BY_NIBBLE = 1 };
+
 typedef struct stark_qmm_args {
     uint32_t struct_size;     /* sizeof(stark_qmm_args) */
-    const void* a;            /* MatmulA::FullPrecision values [M, K] in the input dtype */
-    uint64_t a_offset;        /* element offset into a */
+    const void* a;            /* FullPrecision: values [M, K] in the input dtype; Int8Symmetric: int8 codes [M, K] */
+    uint64_t a_offset;        /* element offset into a (FullPrecision) */
+    /* MatmulA::Int8Symmetric: codes in a (in a_code_layout order), f32 scales
+     * [M, K / a_scale_group_size]; a_group_sums may be NULL. Requires a
+     * quantized 4- or 8-bit B with group 32, 64 or 128 and an activation
+     * group of 32, 64 or 128 dividing K (kernel.rs:130-141), else
+     * STARK_QMM_INCOMPATIBLE_A. */
+    uint32_t a_kind;          /* STARK_QMM_A_* */
+    const float* a_scales;
+    const int32_t* a_group_sums;
+    uint32_t a_scale_group_size;
+    uint32_t a_code_layout;   /* STARK_QMM_CODES_* */
     stark_qmm_b b;
     uint32_t b_leading_dimension; /* FullPrecision B only; 0 = default */
     uint32_t b_transpose;     /* must be 1 for quantized B (the only layout the path uses) */
@@ -301,6 +320,77 @@ STARK_QMM_API stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_a
  * (different streams, or threads) race; serialize them. Allocates nothing. */
 #define STARK_QMM_ROUTED_STATIC_SCRATCH_BYTES (8ull << 20)
 STARK_QMM_API stark_qmm_status stark_qmm_routed_experts_static(const stark_qmm_routed_args* args, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Activation transforms and gated activations                        */
+/* ------------------------------------------------------------------ */
+
+/* ActivationTransformOp (src/backends/common/gpu_types/activation_transform.rs:3-8) */
+enum { STARK_QMM_TRANSFORM_INPUT_RHT = 0, STARK_QMM_TRANSFORM_OUTPUT_RHT = 1, STARK_QMM_TRANSFORM_QUANTIZE = 2,
+       STARK_QMM_TRANSFORM_QUANTIZE_WITH_GROUP_SUMS = 3 };
+
+typedef struct stark_qmm_activation_transform_args {
+    uint32_t struct_size;
+    uint32_t op;                 /* STARK_QMM_TRANSFORM_* */
+    uint32_t data_type;          /* T: F32 or BF16 */
+    uint32_t in_place;           /* read `output` instead of `input` (FP ops) */
+    const void* input;           /* [batch, count] T */
+    void* output;                /* [batch, count] T (FP ops) */
+    const void* bias;            /* [count] in bias_data_type, FP ops, or NULL */
+    uint32_t bias_data_type;
+    int8_t* q_out;               /* [batch, count] codes (quantizing ops) */
+    float* scales_out;           /* [batch, count / scale_group_size] */
+    int32_t* group_sums_out;     /* [batch, count / sum_group_size] */
+    const int32_t* rht_factors;  /* [count] signs */
+    uint32_t batch_size, element_count;
+    uint32_t scale_group_size;   /* 32, 64 or 128 (quantizing ops) */
+    uint32_t sum_group_size;     /* 32, 64 or 128, <= scale_group_size (with group sums) */
+    uint32_t grouped_by_nibble;  /* code order for 4-bit weights (Int8CodeLayout) */
+} stark_qmm_activation_transform_args;
+
+/* Replaces ActivationTransform::encode_* (src/backends/common/kernel/activation_transform.rs;
+ * CPU twin src/backends/cpu/kernel/activation_transform/activation_transform.rs:48-156):
+ * input RHT, output RHT (+ bias), or input RHT then symmetric int8
+ * quantization per scale group (optionally with int32 sums per weight group),
+ * the activations of the int8 (A8W4 / A8W8) products. */
+STARK_QMM_API stark_qmm_status stark_qmm_activation_transform(const stark_qmm_activation_transform_args* args,
+                                                             void* stream);
+
+/* ActivationType (src/backends/common/gpu_types/activation_type.rs:8-16) */
+enum { STARK_QMM_ACT_SILU = 0, STARK_QMM_ACT_GELU_APPROX = 1, STARK_QMM_ACT_GELU_EXACT = 2,
+       STARK_QMM_ACT_IDENTITY = 3, STARK_QMM_ACT_SOFTPLUS = 4, STARK_QMM_ACT_SILU_MATERIALIZED_SIGMOID = 5,
+       STARK_QMM_ACT_GELU_MATERIALIZED_POLYNOMIAL = 6 };
+/* GatedActMulOp (src/backends/common/gpu_types/gated_act_mul.rs:3-7) */
+enum { STARK_QMM_GATED_FULL_PRECISION = 0, STARK_QMM_GATED_QUANTIZE = 1, STARK_QMM_GATED_QUANTIZE_WITH_GROUP_SUMS = 2 };
+
+typedef struct stark_qmm_gated_act_mul_args {
+    uint32_t struct_size;
+    uint32_t op;                 /* STARK_QMM_GATED_* (quantizing ops need hadamard_factors) */
+    uint32_t data_type;          /* T: F32 or BF16 */
+    uint32_t act_type;           /* STARK_QMM_ACT_* */
+    uint32_t interleaved;        /* act_operand rows [value(gated_dim) | gate(gated_dim)] */
+    const void* act_operand;     /* interleaved rows, or gates [batch, gated_dim] */
+    const void* value_operand;   /* separate values: row b at b * value_row_stride + value_offset */
+    void* fp_out;                /* [batch, gated_dim] T */
+    int8_t* q_out;
+    float* scales_out;
+    int32_t* group_sums_out;
+    const int32_t* hadamard_factors; /* [gated_dim] signs, or NULL */
+    uint32_t gated_dim, batch_dim, value_offset, value_row_stride;
+    uint32_t has_activation_alpha;   /* SiLU with alpha */
+    float activation_alpha;
+    uint32_t clip_gate;
+    float gate_clip_min, gate_clip_max;
+    uint32_t clip_value;
+    float value_clip_min, value_clip_max;
+    uint32_t scale_group_size, sum_group_size, grouped_by_nibble;
+} stark_qmm_gated_act_mul_args;
+
+/* Replaces GatedActMul::encode_* (src/backends/common/kernel/gated_act_mul.rs;
+ * CPU twin src/backends/cpu/kernel/gated_act_mul/gated_act_mul.rs:17-152):
+ * value * activation(gate) in T, with optional clipping, SiLU alpha, RHT and
+ * int8 quantization. */
+STARK_QMM_API stark_qmm_status stark_qmm_gated_act_mul(const stark_qmm_gated_act_mul_args* args, void* stream);
 
 /* ------------------------------------------------------------------ */
 /* Weight files: Stark's converted artifact (model.safetensors) and      */

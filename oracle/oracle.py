@@ -54,6 +54,8 @@ class MatmulArgs(C.Structure):
         ("has_soft_cap", C.c_int), ("soft_cap", C.c_float),
         ("gather_indices", C.c_void_p), ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32),
         ("weights_dt", C.c_int), ("input_dt", C.c_int), ("output_dt", C.c_int),
+        ("a_codes", C.c_void_p), ("a_scales", C.c_void_p), ("a_scale_group_size", C.c_uint32),
+        ("a_grouped_by_nibble", C.c_int), ("rht_factors", C.c_void_p),
     ]
 
 
@@ -84,6 +86,14 @@ def _declare(l):
         "so_quantize_affine": (None, [vp, sz, sz, i32, sz, i32, vp, vp, vp]),
         "so_quantize_q8_0": (None, [vp, sz, sz, vp]),
         "so_quantize_q4_k": (None, [vp, sz, sz, vp]),
+        "so_hadamard32": (None, [vp]),
+        "so_min_max_symmetric_divisor": (f, [vp, sz]),
+        "so_quantize_symmetric_i8": (C.c_int8, [f, f]),
+        "so_int8_code_index": (sz, [i32, sz]),
+        "so_activation_transform": (i32, [vp, vp, vp, vp, vp, vp, vp, u32, u32, i32, i32, i32, u32, u32, i32, i32]),
+        "so_activate": (f, [i32, f, i32, i32, f]),
+        "so_gated_act_mul": (i32, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, i32, i32, f, i32, f, f, i32, f, f,
+                                   i32, i32, i32, i32, u32, u32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(l, name)
@@ -155,7 +165,8 @@ def matmul(*, a, m, n, k, codes=None, scales=None, correction=BIASES, correction
            layout=OUTPUT_GROUP, row_count=None, group_count=None, bits=4, group_size=64,
            signed_codes=False, materialize=False, b_values=None, b_leading_dimension=0, b_transpose=True,
            d=None, ab_scale=1.0, accumulate=False, bias=None, soft_cap=None, gather=None,
-           weights_dt=BF16, input_dt=BF16, output_dt=BF16, a_offset=0, threads=0):
+           weights_dt=BF16, input_dt=BF16, output_dt=BF16, a_offset=0, threads=0, a_codes=None, a_scales=None,
+           a_scale_group_size=0, a_grouped_by_nibble=False, rht_factors=None):
     """MatmulCpuKernel::encode restated. Arrays are storage arrays (uint16 bits
     for bf16/f16, float32 for f32). Returns (status, d)."""
     keep = []
@@ -198,6 +209,11 @@ def matmul(*, a, m, n, k, codes=None, scales=None, correction=BIASES, correction
     args.soft_cap = 0.0 if soft_cap is None else soft_cap
     args.gather_indices = _p(arr(gather, np.uint32))
     args.m, args.n, args.k = m, n, k
+    args.a_codes = _p(arr(a_codes, np.int8))
+    args.a_scales = _p(arr(a_scales, np.float32))
+    args.a_scale_group_size = a_scale_group_size
+    args.a_grouped_by_nibble = int(a_grouped_by_nibble)
+    args.rht_factors = _p(arr(rht_factors, np.int32))
     args.weights_dt, args.input_dt, args.output_dt = weights_dt, input_dt, output_dt
     if threads:
         st = lib().so_matmul_parallel(C.byref(args), threads)
@@ -222,6 +238,72 @@ def reference_affine_linear_bf16(input_bits, codes, scales, biases, m, n, k, bit
     lib().so_reference_affine_linear_bf16(_p(input_bits), _p(codes), _p(scales), _p(biases), _p(idx), _p(ob),
                                           _p(of), m, n, k, bank_rows, bits, sos, sgs)
     return of if f32_out else ob
+
+
+# ----------------------------------------------------------------- activation transforms
+
+INPUT_RHT, OUTPUT_RHT, QUANTIZE, QUANTIZE_WITH_GROUP_SUMS = 0, 1, 2, 3
+SILU, GELU_APPROX, GELU_EXACT, IDENTITY, SOFTPLUS, SILU_MATERIALIZED_SIGMOID, GELU_MATERIALIZED_POLYNOMIAL = range(7)
+GAM_FULL_PRECISION, GAM_QUANTIZE, GAM_QUANTIZE_WITH_GROUP_SUMS = 0, 1, 2
+
+
+def hadamard32(v) -> np.ndarray:
+    v = np.array(v, np.float32)
+    assert v.size == 32
+    lib().so_hadamard32(_p(v))
+    return v
+
+
+def int8_code_index(grouped: bool, index: int) -> int:
+    return int(lib().so_int8_code_index(int(grouped), index))
+
+
+def activation_transform(x, factors, batch, count, op, t_dt=F32, bias=None, bias_dt=F32, scale_group=0,
+                         sum_group=0, grouped=False):
+    """ActivationTransform (activation_transform.rs:48-156) out of place.
+    Returns fp output (storage array) or (codes int8, scales f32, sums int32)."""
+    x = np.ascontiguousarray(x)
+    f = np.ascontiguousarray(factors, np.int32)
+    quantize = op in (QUANTIZE, QUANTIZE_WITH_GROUP_SUMS)
+    fp = None if quantize else np.zeros(batch * count, np.float32 if t_dt == F32 else np.uint16)
+    q = np.zeros(batch * count, np.int8) if quantize else None
+    sc = np.zeros(batch * (count // scale_group), np.float32) if quantize else None
+    sums = np.zeros(batch * (count // sum_group), np.int32) if op == QUANTIZE_WITH_GROUP_SUMS else None
+    b = None if bias is None else np.ascontiguousarray(bias)
+    st = lib().so_activation_transform(_p(x), _p(fp), _p(b), _p(q), _p(sc), _p(sums), _p(f), batch, count, op,
+                                       int(grouped), 0, scale_group, sum_group, t_dt, bias_dt)
+    if st:
+        raise ValueError(f"so_activation_transform status {st}")
+    return (q, sc, sums) if quantize else fp
+
+
+def activate(act_type, x, t_dt=F32, alpha=None) -> float:
+    return float(lib().so_activate(act_type, float(x), t_dt, int(alpha is not None), 1.0 if alpha is None else alpha))
+
+
+def gated_act_mul(act, gated_dim, batch, act_type=SILU, value=None, value_offset=0, value_row_stride=0,
+                  interleaved=True, t_dt=F32, alpha=None, gate_clip=None, value_clip=None, op=GAM_FULL_PRECISION,
+                  factors=None, scale_group=0, sum_group=0, grouped=False):
+    """GatedActMul (gated_act_mul.rs:17-152). act: interleaved [batch, value|gate]
+    or gates [batch, gated_dim] with value [.. value_row_stride]; storage arrays."""
+    act = np.ascontiguousarray(act)
+    val = None if value is None else np.ascontiguousarray(value)
+    f = None if factors is None else np.ascontiguousarray(factors, np.int32)
+    quantize = op != GAM_FULL_PRECISION
+    fp = None if quantize else np.zeros(batch * gated_dim, np.float32 if t_dt == F32 else np.uint16)
+    q = np.zeros(batch * gated_dim, np.int8) if quantize else None
+    sc = np.zeros(batch * (gated_dim // scale_group), np.float32) if quantize else None
+    sums = np.zeros(batch * (gated_dim // sum_group), np.int32) if op == GAM_QUANTIZE_WITH_GROUP_SUMS else None
+    gmin, gmax = gate_clip if gate_clip else (0.0, 0.0)
+    vmin, vmax = value_clip if value_clip else (0.0, 0.0)
+    st = lib().so_gated_act_mul(_p(act), _p(val), _p(fp), _p(q), _p(sc), _p(sums), _p(f), gated_dim, batch,
+                                value_offset, value_row_stride, act_type, int(alpha is not None),
+                                1.0 if alpha is None else alpha, int(gate_clip is not None), gmin, gmax,
+                                int(value_clip is not None), vmin, vmax, op, int(grouped), int(interleaved),
+                                int(f is not None), scale_group, sum_group, t_dt)
+    if st:
+        raise ValueError(f"so_gated_act_mul status {st}")
+    return (q, sc, sums) if quantize else fp
 
 
 # ----------------------------------------------------------------- GGUF

@@ -187,7 +187,15 @@ static void matmul_one(const so_matmul_args* a, size_t row, size_t col, int mate
     size_t inner_end = materialize ? 0 : k;
     float midpoint = (float)(1u << (a->bits - 1));
     for (size_t inner = 0; inner < inner_end; ++inner) {
-        float a_value = read_f32(input, a->input_dt, row * k + inner);
+        float a_value;
+        if (a->a_codes) {  /* kernel.rs:193-205 */
+            size_t groups = (k + a->a_scale_group_size - 1) / a->a_scale_group_size;
+            size_t code_index = so_int8_code_index(a->a_grouped_by_nibble, inner);
+            float q = (float)a->a_codes[row * k + code_index];
+            a_value = q * a->a_scales[row * groups + inner / a->a_scale_group_size];
+        } else {
+            a_value = read_f32(input, a->input_dt, row * k + inner);
+        }
         if (!a->codes) {
             size_t ld = a->b_leading_dimension ? a->b_leading_dimension : (a->b_transpose ? k : n);
             size_t index = a->b_transpose ? b_col * ld + inner : inner * ld + b_col;
@@ -223,9 +231,19 @@ static void matmul_one(const so_matmul_args* a, size_t row, size_t col, int mate
     size_t oi = row * n + col;
     float value = a->ab_scale * accumulator;
     if (a->accumulate) value += read_f32(a->d, a->output_dt, oi);
-    if (a->bias) value += read_f32(a->bias, a->weights_dt, col);
+    if (a->bias && !a->rht_factors) value += read_f32(a->bias, a->weights_dt, col);  /* kernel.rs:275 */
     if (a->has_soft_cap) value = a->soft_cap * tanhf(value / a->soft_cap);
     write_f32(a->d, a->output_dt, oi, value);
+}
+
+/* kernel.rs:287-300: output RHT in place over d, then the bias add
+ * (tensor_add_bias.rs:9-32: f32(d) + f32(bias), rounded to d's type). */
+static void matmul_output_rht(const so_matmul_args* a) {
+    so_activation_transform(NULL, a->d, NULL, NULL, NULL, NULL, a->rht_factors, a->m, a->n, SO_OUTPUT_RHT, 0, 1, 0,
+                            0, a->output_dt, SO_F32);
+    if (!a->bias) return;
+    for (size_t i = 0; i < (size_t)a->m * a->n; ++i)
+        write_f32(a->d, a->output_dt, i, read_f32(a->d, a->output_dt, i) + read_f32(a->bias, a->weights_dt, i % a->n));
 }
 
 static int matmul_prepare(const so_matmul_args* a, int* materialize, uint32_t* os, uint32_t* gs, uint32_t* zos,
@@ -233,6 +251,13 @@ static int matmul_prepare(const so_matmul_args* a, int* materialize, uint32_t* o
     int dts[3] = {a->weights_dt, a->input_dt, a->output_dt};
     for (int i = 0; i < 3; ++i)
         if (dts[i] != SO_F32 && dts[i] != SO_F16 && dts[i] != SO_BF16) return 2;
+    if (a->rht_factors && (a->output_dt == SO_F16 || a->n % 32)) return 4;
+    if (a->a_codes) {  /* kernel.rs:130-141 */
+        uint32_t g = a->a_scale_group_size;
+        if (!(g == 32 || g == 64 || g == 128) || a->k % g || !a->codes || !(a->bits == 4 || a->bits == 8) ||
+            !(a->group_size == 32 || a->group_size == 64 || a->group_size == 128))
+            return 3;
+    }
     if (!a->codes) {
         *materialize = 0;
         *os = *gs = *zos = *zgs = 0;
@@ -259,6 +284,7 @@ int so_matmul(const so_matmul_args* a) {
     if (st) return st;
     for (size_t row = 0; row < a->m; ++row)
         for (size_t col = 0; col < a->n; ++col) matmul_one(a, row, col, materialize, os, gs, zos, zgs);
+    if (a->rht_factors) matmul_output_rht(a);
     return 0;
 }
 
@@ -270,6 +296,223 @@ int so_matmul_parallel(const so_matmul_args* a, int threads) {
     long total = (long)a->m * (long)a->n;
 #pragma omp parallel for schedule(static) num_threads(threads)
     for (long i = 0; i < total; ++i) matmul_one(a, (size_t)(i / a->n), (size_t)(i % a->n), materialize, os, gs, zos, zgs);
+    if (a->rht_factors) matmul_output_rht(a);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Activation transforms: src/backends/cpu/kernel/activation_transform/       */
+/* ------------------------------------------------------------------------ */
+
+#define SO_HADAMARD_BLOCK 32 /* src/backends/common/gpu_types/hadamard_order.rs:1 */
+
+/* mod.rs:28-43 */
+void so_hadamard32(float* v) {
+    for (int stride = 1; stride < SO_HADAMARD_BLOCK; stride <<= 1)
+        for (int lane = 0; lane < SO_HADAMARD_BLOCK; ++lane)
+            if ((lane & stride) == 0) {
+                float x = v[lane], y = v[lane | stride];
+                v[lane] = x + y;
+                v[lane | stride] = x - y;
+            }
+    const float scale = 1.0f / sqrtf((float)SO_HADAMARD_BLOCK);
+    for (int i = 0; i < SO_HADAMARD_BLOCK; ++i) v[i] *= scale;
+}
+
+/* mod.rs:9-19: the group's largest magnitude / 127, or 1 when that is zero or
+ * not finite (f32::min/max ignore NaN). */
+float so_min_max_symmetric_divisor(const float* v, size_t n) {
+    float mn = INFINITY, mx = -INFINITY;
+    for (size_t i = 0; i < n; ++i) {
+        mn = fminf(mn, v[i]);
+        mx = fmaxf(mx, v[i]);
+    }
+    float m = fmaxf(fabsf(mn), fabsf(mx));
+    return (isfinite(m) && m > 0.0f) ? m / 127.0f : 1.0f;
+}
+
+/* mod.rs:21-26: round half away from zero, clamp to +-127, as i8 (NaN -> 0) */
+int8_t so_quantize_symmetric_i8(float value, float divisor) {
+    float q = roundf(value / divisor);
+    if (isnan(q)) return 0;
+    if (q < -127.0f) q = -127.0f;
+    if (q > 127.0f) q = 127.0f;
+    return (int8_t)q;
+}
+
+size_t so_int8_code_index(int grouped, size_t index) {
+    if (!grouped) return index;
+    size_t offset = index % 8;
+    return index - offset + (offset % 2) * 4 + offset / 2;
+}
+
+/* activation_transform.rs:14-46 */
+static void quantize_transformed_row(const float* t, size_t n, size_t scale_group, size_t sum_group, int8_t* values,
+                                     float* scales, int32_t* sums, int grouped) {
+    if (sums)
+        for (size_t i = 0; i < n / sum_group; ++i) sums[i] = 0;
+    for (size_t g = 0; g < n / scale_group; ++g) {
+        const float* src = t + g * scale_group;
+        float scale = so_min_max_symmetric_divisor(src, scale_group);
+        scales[g] = scale;
+        for (size_t i = 0; i < scale_group; ++i) {
+            int8_t code = so_quantize_symmetric_i8(src[i], scale);
+            size_t absolute = g * scale_group + i;
+            values[so_int8_code_index(grouped, absolute)] = code;
+            if (sums) sums[absolute / sum_group] += code;
+        }
+    }
+}
+
+/* f32::clamp: NaN stays NaN */
+static float clamp_f32(float x, float lo, float hi) { return x < lo ? lo : (x > hi ? hi : x); }
+
+static float round_to(int dt, float v) { return dt == SO_BF16 ? so_bf16_to_f32(so_f32_to_bf16(v)) : v; }
+
+/* activation_transform.rs:48-156 */
+int so_activation_transform(const void* input, void* fp_out, const void* bias, int8_t* q_out, float* scales_out,
+                            int32_t* group_sums_out, const int32_t* factors, uint32_t batch_size,
+                            uint32_t element_count, int op, int grouped, int in_place, uint32_t scale_group,
+                            uint32_t sum_group, int t_dt, int bias_dt) {
+    const void* src = in_place ? fp_out : input;
+    size_t columns = element_count;
+    if (columns % SO_HADAMARD_BLOCK) return 1;
+    int input_rht = op != SO_OUTPUT_RHT;
+    int quantize = op == SO_QUANTIZE || op == SO_QUANTIZE_WITH_GROUP_SUMS;
+    if (quantize && (!scale_group || columns % scale_group ||
+                     (op == SO_QUANTIZE_WITH_GROUP_SUMS && (!sum_group || columns % sum_group))))
+        return 1;
+    float* transformed = (float*)malloc(columns * sizeof(float));
+    for (size_t row = 0; row < batch_size; ++row) {
+        size_t ro = row * columns;
+        for (size_t s0 = 0; s0 < columns; s0 += SO_HADAMARD_BLOCK) {
+            float stripe[SO_HADAMARD_BLOCK];
+            for (int lane = 0; lane < SO_HADAMARD_BLOCK; ++lane) {
+                float value = read_f32(src, t_dt, ro + s0 + lane);
+                float factor = (float)factors[s0 + lane];
+                stripe[lane] = input_rht ? value * factor : value;
+            }
+            so_hadamard32(stripe);
+            for (int lane = 0; lane < SO_HADAMARD_BLOCK; ++lane) {
+                float factor = (float)factors[s0 + lane];
+                transformed[s0 + lane] = input_rht ? stripe[lane] : stripe[lane] * factor;
+            }
+        }
+        if (quantize) {
+            size_t spr = columns / scale_group;
+            quantize_transformed_row(transformed, columns, scale_group,
+                                     op == SO_QUANTIZE_WITH_GROUP_SUMS ? sum_group : 0, q_out + ro,
+                                     scales_out + row * spr,
+                                     op == SO_QUANTIZE_WITH_GROUP_SUMS ? group_sums_out + row * (columns / sum_group)
+                                                                       : NULL,
+                                     grouped);
+        } else {
+            for (size_t i = 0; i < columns; ++i) {
+                float value = transformed[i];
+                if (bias) value = round_to(t_dt, value) + read_f32(bias, bias_dt, i);
+                write_f32(fp_out, t_dt, ro + i, value);
+            }
+        }
+    }
+    free(transformed);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Activations: src/backends/common/gpu_types/activation_type.rs, in the      */
+/* storage type T (half's bf16 arithmetic rounds after every operation).      */
+/* ------------------------------------------------------------------------ */
+
+#define GELU_K0 0.044715f   /* activation_type.rs:3 */
+#define GELU_K1 0.7978846f  /* activation_type.rs:4 */
+
+float so_activate(int act_type, float x, int dt, int has_alpha, float alpha) {
+    switch (act_type) {
+    case SO_SILU: { /* activation_silu_alpha :35-42 (alpha 1 for plain SILU) */
+        float a = has_alpha ? alpha : 1.0f;
+        return round_to(dt, x / (1.0f + expf(-a * x)));
+    }
+    case SO_SILU_MATERIALIZED_SIGMOID: { /* :48-60 */
+        float exponential = round_to(dt, expf(fabsf(x)));
+        float lower = round_to(dt, 1.0f / round_to(dt, 1.0f + exponential));
+        float sigmoid = x < 0.0f ? lower : round_to(dt, 1.0f - lower);
+        return round_to(dt, x * sigmoid);
+    }
+    case SO_GELU_APPROX: { /* :62-67 */
+        float tan_arg = GELU_K1 * (x + GELU_K0 * x * x * x);
+        return round_to(dt, 0.5f * x * (1.0f + tanhf(tan_arg)));
+    }
+    case SO_GELU_MATERIALIZED_POLYNOMIAL: { /* :69-76 */
+        float cubic = round_to(dt, x * x * x);
+        float term = round_to(dt, round_to(dt, GELU_K0) * cubic);
+        float inner = round_to(dt, x + term);
+        float argument = round_to(dt, round_to(dt, GELU_K1) * inner);
+        float activated = round_to(dt, tanhf(argument));
+        return round_to(dt, round_to(dt, 0.5f * x) * round_to(dt, 1.0f + activated));
+    }
+    case SO_GELU_EXACT: /* :78-82 */
+        return round_to(dt, 0.5f * x * (1.0f + erff(x * 0.70710677f)));
+    case SO_SOFTPLUS: /* :84-92 */
+        if (x > 20.0f) return x;
+        return round_to(dt, logf(1.0f + expf(x)));
+    default: /* IDENTITY */
+        return x;
+    }
+}
+
+/* gated_act_mul.rs:17-152 */
+int so_gated_act_mul(const void* act, const void* value_operand, void* fp_out, int8_t* q_out, float* scales_out,
+                     int32_t* sums_out, const int32_t* factors, uint32_t gated_dim, uint32_t batch_dim,
+                     uint32_t value_offset, uint32_t value_row_stride, int act_type, int has_alpha, float alpha,
+                     int clip_gate, float gate_min, float gate_max, int clip_value, float value_min,
+                     float value_max, int op, int grouped, int interleaved, int use_hadamard, uint32_t scale_group,
+                     uint32_t sum_group, int dt) {
+    int quantize = op == SO_GAM_QUANTIZE || op == SO_GAM_QUANTIZE_WITH_GROUP_SUMS;
+    int emit_sums = op == SO_GAM_QUANTIZE_WITH_GROUP_SUMS;
+    if (quantize && !use_hadamard) return 1;
+    if (quantize && (!scale_group || gated_dim % scale_group)) return 1;
+    if (emit_sums && (!sum_group || gated_dim % sum_group)) return 1;
+    if (use_hadamard && gated_dim % SO_HADAMARD_BLOCK) return 1;
+    float* transformed = use_hadamard ? (float*)malloc((size_t)gated_dim * sizeof(float)) : NULL;
+    for (size_t batch = 0; batch < batch_dim; ++batch) {
+        for (size_t g = 0; g < gated_dim; ++g) {
+            size_t act_index;
+            float value;
+            if (interleaved) {
+                size_t base = batch * 2 * gated_dim;
+                act_index = base + gated_dim + g;
+                value = read_f32(act, dt, base + g);
+            } else {
+                act_index = batch * gated_dim + g;
+                value = read_f32(value_operand, dt, batch * value_row_stride + value_offset + g);
+            }
+            float gate = read_f32(act, dt, act_index);
+            if (clip_gate) gate = round_to(dt, clamp_f32(gate, gate_min, gate_max));
+            float activated = (has_alpha && act_type == SO_SILU) ? so_activate(SO_SILU, gate, dt, 1, alpha)
+                                                                 : so_activate(act_type, gate, dt, 0, 1.0f);
+            if (clip_value) value = round_to(dt, clamp_f32(value, value_min, value_max));
+            float result = round_to(dt, value * activated);
+            if (transformed) transformed[g] = result;
+            else write_f32(fp_out, dt, batch * gated_dim + g, result);
+        }
+        if (transformed) {
+            for (size_t s0 = 0; s0 < gated_dim; s0 += SO_HADAMARD_BLOCK) {
+                float stripe[SO_HADAMARD_BLOCK];
+                for (int lane = 0; lane < SO_HADAMARD_BLOCK; ++lane)
+                    stripe[lane] = transformed[s0 + lane] * (float)factors[s0 + lane];
+                so_hadamard32(stripe);
+                memcpy(transformed + s0, stripe, sizeof stripe);
+            }
+            if (quantize) {
+                quantize_transformed_row(transformed, gated_dim, scale_group, emit_sums ? sum_group : 0,
+                                         q_out + batch * gated_dim, scales_out + batch * (gated_dim / scale_group),
+                                         emit_sums ? sums_out + batch * (gated_dim / sum_group) : NULL, grouped);
+            } else {
+                for (size_t g = 0; g < gated_dim; ++g) write_f32(fp_out, dt, batch * gated_dim + g, transformed[g]);
+            }
+        }
+    }
+    free(transformed);
     return 0;
 }
 

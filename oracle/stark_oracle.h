@@ -74,9 +74,20 @@ typedef struct so_matmul_args {
     const uint32_t* gather_indices; /* [m*n] or NULL */
     uint32_t m, n, k;
     int weights_dt, input_dt, output_dt;
+    /* MatmulA::Int8Symmetric (src/backends/common/kernel/matmul/matmul_a.rs:51-61):
+     * a_codes non-NULL replaces the FullPrecision A: int8 codes [m, k] in
+     * a_code_layout order, f32 scales [m, k / a_scale_group_size] */
+    const int8_t* a_codes;
+    const float* a_scales;
+    uint32_t a_scale_group_size;
+    int a_grouped_by_nibble;
+    /* MatmulDOps::rht_factors: output RHT then bias (kernel.rs:167, 287-300) */
+    const int32_t* rht_factors;
 } so_matmul_args;
 
-/* Status: 0 ok, 1 unsupported layout (undersized codes / policy), 2 unsupported dtype. */
+/* Status: 0 ok, 1 unsupported layout (undersized codes / policy), 2 unsupported
+ * dtype, 3 incompatible A (int8 activations with unsupported groups or codes),
+ * 4 unsupported D-op (output RHT on an f16 output or a width not a multiple of 32). */
 int so_matmul(const so_matmul_args* args);
 /* Row-parallel variant (OpenMP over output columns); identical arithmetic per output. */
 int so_matmul_parallel(const so_matmul_args* args, int threads);
@@ -94,6 +105,40 @@ int so_routed_experts(const uint16_t* input, const float* logits, const float* e
                       int bits, uint32_t group_size, int plane_dt, uint32_t rows, uint32_t model, uint32_t hidden,
                       uint32_t experts, uint32_t active, int round_logits, int round_weights, int round_products,
                       int round_accumulator, int sort_ids, uint16_t* output);
+
+/* ---- activation transforms (src/backends/cpu/kernel/activation_transform/) */
+/* mod.rs:28-43: the 32-point Walsh-Hadamard butterfly, then * 1/sqrt(32). */
+void so_hadamard32(float* values);
+/* mod.rs:9-26 */
+float so_min_max_symmetric_divisor(const float* values, size_t count);
+int8_t so_quantize_symmetric_i8(float value, float divisor);
+/* Int8CodeLayout::index (src/backends/common/kernel/matmul/matmul_a.rs:31-46) */
+size_t so_int8_code_index(int grouped_by_nibble, size_t index);
+/* ActivationTransformOp (src/backends/common/gpu_types/activation_transform.rs:3-8) */
+enum { SO_INPUT_RHT = 0, SO_OUTPUT_RHT = 1, SO_QUANTIZE = 2, SO_QUANTIZE_WITH_GROUP_SUMS = 3 };
+/* activation_transform.rs:48-156. T (t_dt) and BiasT (bias_dt) are F32 or
+ * BF16; in_place reads fp_out. Returns 0, or 1 for a width not a multiple of 32. */
+int so_activation_transform(const void* input, void* fp_out, const void* bias, int8_t* q_out, float* scales_out,
+                            int32_t* group_sums_out, const int32_t* rht_factors, uint32_t batch_size,
+                            uint32_t element_count, int op, int grouped_by_nibble, int in_place,
+                            uint32_t scale_group_size, uint32_t sum_group_size, int t_dt, int bias_dt);
+/* ActivationType (src/backends/common/gpu_types/activation_type.rs:8-16) */
+enum { SO_SILU = 0, SO_GELU_APPROX = 1, SO_GELU_EXACT = 2, SO_IDENTITY = 3, SO_SOFTPLUS = 4,
+       SO_SILU_MATERIALIZED_SIGMOID = 5, SO_GELU_MATERIALIZED_POLYNOMIAL = 6 };
+/* ActivationType::activate / activation_silu_alpha (activation_type.rs:19-111)
+ * on a value stored in t_dt, result rounded to t_dt. */
+float so_activate(int act_type, float x, int t_dt, int has_alpha, float alpha);
+/* GatedActMulOp (src/backends/common/gpu_types/gated_act_mul.rs:3-7) */
+enum { SO_GAM_FULL_PRECISION = 0, SO_GAM_QUANTIZE = 1, SO_GAM_QUANTIZE_WITH_GROUP_SUMS = 2 };
+/* src/backends/cpu/kernel/gated_act_mul/gated_act_mul.rs:17-152. Returns 0, or
+ * 1 when the op's preconditions fail (quantize without RHT, widths). */
+int so_gated_act_mul(const void* act_operand, const void* value_operand, void* fp_out, int8_t* q_out,
+                     float* scales_out, int32_t* group_sums_out, const int32_t* hadamard_factors,
+                     uint32_t gated_dim, uint32_t batch_dim, uint32_t value_offset, uint32_t value_row_stride,
+                     int act_type, int has_alpha, float alpha, int clip_gate, float gate_min, float gate_max,
+                     int clip_value, float value_min, float value_max, int op, int grouped_by_nibble,
+                     int interleaved, int use_hadamard, uint32_t scale_group_size, uint32_t sum_group_size,
+                     int t_dt);
 
 /* backends/cpu/kernel/matmul/vision.rs:249-336 (BF16-effective reference dot). */
 void so_reference_affine_linear_bf16(const uint16_t* input, const uint8_t* weights, const uint16_t* scales,

@@ -136,18 +136,24 @@ stark_qmm_status stark_qmm_set_reference_accumulation(stark_qmm_kernel* k, uint3
     return STARK_QMM_OK;
 }
 
-stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kr, const stark_qmm_args* args, void* stream_ptr) {
-    if (!kr || !args) return STARK_QMM_INVALID_ARGUMENT;
-    if (args->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
-    hipStream_t stream = (hipStream_t)stream_ptr;
+}  // extern "C"
+
+namespace {
+
+// The product of MatmulCpuKernel::encode (kernel.rs:58-282) with the D ops in
+// `dops` (the output RHT, when requested, runs after it).
+stark_qmm_status encode_product(stark_qmm_kernel* kr, const stark_qmm_args* args, const stark_qmm_d_ops& dops,
+                                hipStream_t stream) {
     const stark_qmm_b& b = args->b;
-    const stark_qmm_d_ops& dops = args->d_ops;
-    if (dops.rht_factors) return STARK_QMM_UNSUPPORTED_D_OP;
     const uint32_t m = args->m, n = args->n, k = args->k;
     const size_t xsz = kr->x_dt == STARK_QMM_F32 ? 4 : 2;
-    const void* x = args->a ? (const uint8_t*)args->a + args->a_offset * xsz : nullptr;
+    if (args->a_kind > STARK_QMM_A_INT8_SYMMETRIC || args->a_code_layout > STARK_QMM_CODES_GROUPED_BY_NIBBLE)
+        return STARK_QMM_INVALID_ARGUMENT;
+    const bool a8 = args->a_kind == STARK_QMM_A_INT8_SYMMETRIC;
+    const void* x = args->a && !a8 ? (const uint8_t*)args->a + args->a_offset * xsz : nullptr;
 
     if (!b.codes) {
+        if (a8) return STARK_QMM_INCOMPATIBLE_A;
         // MatmulB::FullPrecision
         if (b.params.materialize_affine_input_sum) return STARK_QMM_UNSUPPORTED_LAYOUT;
         if (!b.values || (!x && m && n && k) || (!args->d && m && n)) return STARK_QMM_INVALID_ARGUMENT;
@@ -178,14 +184,27 @@ stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kr, const stark_qmm_args* ar
         const uint32_t gs = b.group_size;
         if (kr->w_dt != STARK_QMM_BF16 || kr->x_dt != STARK_QMM_BF16 || kr->d_dt != STARK_QMM_BF16 ||
             b.mode != STARK_QMM_MODE_U4 || b.correction != STARK_QMM_CORRECTION_BIASES || b.signed_codes ||
-            !args->b_transpose || !(gs == 16 || gs == 32 || gs == 64 || gs == 128) || (k % 4) != 0)
+            !args->b_transpose || a8 || !(gs == 16 || gs == 32 || gs == 64 || gs == 128) || (k % 4) != 0)
             return STARK_QMM_UNSUPPORTED_LAYOUT;
+    }
+    if (a8) {
+        // MatmulA::Int8Symmetric compatibility (kernel.rs:130-141)
+        const uint32_t ag = args->a_scale_group_size, gs = b.group_size;
+        if (!(ag == 32 || ag == 64 || ag == 128) || k % ag != 0 || !(gs == 32 || gs == 64 || gs == 128) ||
+            !(b.mode == STARK_QMM_MODE_U4 || b.mode == STARK_QMM_MODE_U8))
+            return STARK_QMM_INCOMPATIBLE_A;
     }
     AffineOp op;
     int bits;
     stark_qmm_status st = build_affine_op(kr, b, m, n, k, x, args->d, dops, args->gather_indices, &op, &bits);
     if (st != STARK_QMM_OK) return st;
     if (m == 0 || n == 0) return STARK_QMM_OK;
+    if (a8) {
+        if (!args->d || (k && (!args->a || !args->a_scales))) return STARK_QMM_INVALID_ARGUMENT;
+        A8Operand q{(const int8_t*)args->a, args->a_scales, args->a_scale_group_size,
+                    args->a_code_layout == STARK_QMM_CODES_GROUPED_BY_NIBBLE ? 1u : 0u};
+        return launch_affine_a8(op, q, bits, stream);
+    }
     if (!args->d || (!x && k)) return STARK_QMM_INVALID_ARGUMENT;
     if (materialize && m == 1) return launch_affine_materialized(op, stream);
     // Prefill-sized products run the dequant-GEMM (bf16-rounded weight tiles, as
@@ -195,6 +214,26 @@ stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kr, const stark_qmm_args* ar
         return launch_affine_gemm(op, bits, stream);
     if (affine_fast_eligible(op, bits)) return launch_affine_gemv(&op, 1, bits, stream);
     return launch_affine_generic(op, bits, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kr, const stark_qmm_args* args, void* stream_ptr) {
+    if (!kr || !args) return STARK_QMM_INVALID_ARGUMENT;
+    if (args->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
+    hipStream_t stream = (hipStream_t)stream_ptr;
+    stark_qmm_d_ops dops = args->d_ops;
+    const int32_t* rht = (const int32_t*)args->d_ops.rht_factors;
+    if (rht) {
+        // Output RHT over each 32 outputs of a row, then the bias (kernel.rs:167, 287-300).
+        if (kr->d_dt == STARK_QMM_F16 || args->n % 32 != 0) return STARK_QMM_UNSUPPORTED_D_OP;
+        dops.bias = nullptr;
+    }
+    stark_qmm_status st = encode_product(kr, args, dops, stream);
+    if (st != STARK_QMM_OK || !rht || args->m == 0 || args->n == 0) return st;
+    return launch_output_rht(args->d, kr->d_dt, args->d_ops.bias, kr->w_dt, rht, args->m, args->n, stream);
 }
 
 stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_args* args, uint32_t count,
@@ -207,8 +246,7 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
     for (uint32_t i = 0; i < count; ++i) {
         const stark_qmm_args* a = &args[i];
         if (a->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
-        if (a->d_ops.rht_factors) return STARK_QMM_UNSUPPORTED_D_OP;
-        if (!a->b.codes || a->b.params.materialize_affine_input_sum || a->m == 0 || a->n == 0) {
+        if (a->d_ops.rht_factors || a->a_kind != STARK_QMM_A_FULL_PRECISION || !a->b.codes || a->b.params.materialize_affine_input_sum || a->m == 0 || a->n == 0) {
             rest.push_back(i);
             continue;
         }

@@ -263,6 +263,18 @@ stark_qmm_status launch_gguf_gemv(const GgufOp* ops, uint32_t count, uint32_t* s
 // status |= 1 when any of x[0..n) is not finite (mapped.hip).
 stark_qmm_status launch_finite_check(const float* x, uint64_t n, uint32_t* status, hipStream_t stream);
 
+// Output RHT of a product (transforms.hip): d <- RHT(d) * factors, then + bias.
+stark_qmm_status launch_output_rht(void* d, uint32_t d_dt, const void* bias, uint32_t bias_dt,
+                                   const int32_t* factors, uint32_t rows, uint32_t n, hipStream_t stream);
+// Int8-activation products (qmv_a8.hip).
+struct A8Operand {
+    const int8_t* codes;   // [M, K] in code layout order
+    const float* scales;   // [M, K / group]
+    uint32_t group;        // activation scale group
+    uint32_t grouped;      // Int8CodeLayout::GroupedByNibble
+};
+stark_qmm_status launch_affine_a8(const AffineOp& op, const A8Operand& a, int bits, hipStream_t stream);
+
 // Largest M the GEMV kernel handles in one weight pass.
 constexpr uint32_t kGemvMaxM = 2;
 

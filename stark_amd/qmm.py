@@ -85,7 +85,9 @@ class _DOps(C.Structure):
 
 
 class _Args(C.Structure):
-    _fields_ = [("struct_size", C.c_uint32), ("a", C.c_void_p), ("a_offset", C.c_uint64), ("b", _B),
+    _fields_ = [("struct_size", C.c_uint32), ("a", C.c_void_p), ("a_offset", C.c_uint64), ("a_kind", C.c_uint32),
+                ("a_scales", C.c_void_p), ("a_group_sums", C.c_void_p), ("a_scale_group_size", C.c_uint32),
+                ("a_code_layout", C.c_uint32), ("b", _B),
                 ("b_leading_dimension", C.c_uint32), ("b_transpose", C.c_uint32), ("d", C.c_void_p),
                 ("d_ops", _DOps), ("gather_indices", C.c_void_p), ("m", C.c_uint32), ("n", C.c_uint32),
                 ("k", C.c_uint32)]
@@ -129,6 +131,27 @@ class _WeightMatrix(C.Structure):
                 ("device", C.c_void_p * 3)]
 
 
+class _TransformArgs(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("op", C.c_uint32), ("data_type", C.c_uint32), ("in_place", C.c_uint32),
+                ("input", C.c_void_p), ("output", C.c_void_p), ("bias", C.c_void_p), ("bias_data_type", C.c_uint32),
+                ("q_out", C.c_void_p), ("scales_out", C.c_void_p), ("group_sums_out", C.c_void_p),
+                ("rht_factors", C.c_void_p), ("batch_size", C.c_uint32), ("element_count", C.c_uint32),
+                ("scale_group_size", C.c_uint32), ("sum_group_size", C.c_uint32),
+                ("grouped_by_nibble", C.c_uint32)]
+
+
+class _GatedArgs(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("op", C.c_uint32), ("data_type", C.c_uint32), ("act_type", C.c_uint32),
+                ("interleaved", C.c_uint32), ("act_operand", C.c_void_p), ("value_operand", C.c_void_p),
+                ("fp_out", C.c_void_p), ("q_out", C.c_void_p), ("scales_out", C.c_void_p),
+                ("group_sums_out", C.c_void_p), ("hadamard_factors", C.c_void_p), ("gated_dim", C.c_uint32),
+                ("batch_dim", C.c_uint32), ("value_offset", C.c_uint32), ("value_row_stride", C.c_uint32),
+                ("has_activation_alpha", C.c_uint32), ("activation_alpha", C.c_float), ("clip_gate", C.c_uint32),
+                ("gate_clip_min", C.c_float), ("gate_clip_max", C.c_float), ("clip_value", C.c_uint32),
+                ("value_clip_min", C.c_float), ("value_clip_max", C.c_float), ("scale_group_size", C.c_uint32),
+                ("sum_group_size", C.c_uint32), ("grouped_by_nibble", C.c_uint32)]
+
+
 # Every symbol include/stark_qmm.h declares, with its ctypes signature.
 SIGNATURES = {
     "stark_qmm_abi_version": (C.c_uint32, []),
@@ -167,6 +190,8 @@ SIGNATURES = {
                                                   C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(_WeightMatrix),
                                                   C.c_void_p]),
     "stark_qmm_weight_matrix_free": (None, [C.POINTER(_WeightMatrix)]),
+    "stark_qmm_activation_transform": (C.c_uint32, [C.POINTER(_TransformArgs), C.c_void_p]),
+    "stark_qmm_gated_act_mul": (C.c_uint32, [C.POINTER(_GatedArgs), C.c_void_p]),
 }
 
 _lib = None
@@ -257,9 +282,25 @@ class MatmulDOps:
     soft_cap: Optional[float] = None
 
 
+# Int8CodeLayout (matmul_a.rs:6-9)
+SEQUENTIAL, GROUPED_BY_NIBBLE = 0, 1
+
+
+@dataclass
+class Int8SymmetricA:
+    """MatmulA::Int8Symmetric (matmul_a.rs:51-61): activation a[m, k] =
+    values[m, index(k)] * scales[m, k // scale_group_size] with int8 values in
+    `code_layout` order (as ActivationTransform::encode_quantize writes them)."""
+    values: torch.Tensor
+    scales: torch.Tensor
+    scale_group_size: int
+    group_sums: Optional[torch.Tensor] = None
+    code_layout: int = SEQUENTIAL
+
+
 @dataclass
 class MatmulArguments:
-    a: torch.Tensor
+    a: object  # torch.Tensor (MatmulA::FullPrecision) | Int8SymmetricA
     b: object  # QuantizedB | FullPrecisionB
     d: torch.Tensor
     m: int
@@ -297,8 +338,17 @@ def _fill_b(dst: _B, b) -> None:
 def _args(a: MatmulArguments) -> _Args:
     s = _Args()
     s.struct_size = C.sizeof(_Args)
-    s.a = _ptr(a.a)
-    s.a_offset = a.a_offset
+    if isinstance(a.a, Int8SymmetricA):
+        q = a.a
+        s.a = _ptr(q.values)
+        s.a_kind = 1
+        s.a_scales = _ptr(q.scales)
+        s.a_group_sums = _ptr(q.group_sums)
+        s.a_scale_group_size = q.scale_group_size
+        s.a_code_layout = q.code_layout
+    else:
+        s.a = _ptr(a.a)
+        s.a_offset = a.a_offset
     _fill_b(s.b, a.b)
     s.b_leading_dimension = a.b_leading_dimension
     s.b_transpose = int(a.b_transpose)
@@ -363,6 +413,163 @@ class MatmulKernel:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------- activation transforms
+
+# ActivationTransformOp / ActivationType / GatedActMulOp ids of the C ABI
+INPUT_RHT, OUTPUT_RHT, QUANTIZE, QUANTIZE_WITH_GROUP_SUMS = 0, 1, 2, 3
+(ACT_SILU, ACT_GELU_APPROX, ACT_GELU_EXACT, ACT_IDENTITY, ACT_SOFTPLUS, ACT_SILU_MATERIALIZED_SIGMOID,
+ ACT_GELU_MATERIALIZED_POLYNOMIAL) = range(7)
+GATED_FULL_PRECISION, GATED_QUANTIZE, GATED_QUANTIZE_WITH_GROUP_SUMS = 0, 1, 2
+HADAMARD_BLOCK = 32
+
+
+@dataclass(frozen=True)
+class ActivationQuantization:
+    """ActivationQuantization (activation_transform.rs:18-55); build with new()."""
+    scale_group_size: int
+    sum_group_size: Optional[int]
+    code_layout: int
+
+    @staticmethod
+    def new(scale_group_size: int, weight_group_size: int, emit_group_sums: bool,
+            code_layout: int = SEQUENTIAL) -> Optional["ActivationQuantization"]:
+        ok = scale_group_size in (32, 64, 128) and weight_group_size in (32, 64, 128) and \
+            scale_group_size >= weight_group_size
+        return ActivationQuantization(scale_group_size, weight_group_size if emit_group_sums else None,
+                                      code_layout) if ok else None
+
+
+class ActivationTransform:
+    """ActivationTransform (activation_transform.rs:57-260) over
+    stark_qmm_activation_transform."""
+
+    def __init__(self, data_type: int, op: int, in_place: bool = False, bias_data_type: Optional[int] = None,
+                 quantization: Optional[ActivationQuantization] = None):
+        self.data_type, self.op, self.in_place = data_type, op, in_place
+        self.bias_data_type, self.quantization = bias_data_type, quantization
+
+    @classmethod
+    def input_rht(cls, data_type: int, in_place: bool = False):
+        return cls(data_type, INPUT_RHT, in_place)
+
+    @classmethod
+    def output_rht(cls, data_type: int, bias_data_type: Optional[int] = None, in_place: bool = False):
+        return cls(data_type, OUTPUT_RHT, in_place, bias_data_type)
+
+    @classmethod
+    def quantize(cls, data_type: int, quantization: ActivationQuantization):
+        op = QUANTIZE if quantization.sum_group_size is None else QUANTIZE_WITH_GROUP_SUMS
+        return cls(data_type, op, False, None, quantization)
+
+    def _base(self, factors, batch_size, element_count) -> _TransformArgs:
+        s = _TransformArgs()
+        s.struct_size = C.sizeof(_TransformArgs)
+        s.op, s.data_type = self.op, self.data_type
+        s.rht_factors = _ptr(factors)
+        s.batch_size, s.element_count = batch_size, element_count
+        return s
+
+    def _run(self, s, stream, where):
+        _check(lib().stark_qmm_activation_transform(C.byref(s), _stream(stream)), where)
+
+    def encode_fp(self, input: torch.Tensor, output: torch.Tensor, rht_factors: torch.Tensor, batch_size: int,
+                  element_count: int, stream=None) -> None:
+        assert self.quantization is None and not self.in_place and self.bias_data_type is None
+        s = self._base(rht_factors, batch_size, element_count)
+        s.input, s.output = _ptr(input), _ptr(output)
+        self._run(s, stream, "ActivationTransform::encode_fp")
+
+    def encode_fp_in_place(self, data: torch.Tensor, rht_factors: torch.Tensor, bias: Optional[torch.Tensor],
+                           batch_size: int, element_count: int, stream=None) -> None:
+        assert self.quantization is None and self.in_place and (bias is None) == (self.bias_data_type is None)
+        s = self._base(rht_factors, batch_size, element_count)
+        s.in_place = 1
+        s.output = _ptr(data)
+        s.bias = _ptr(bias)
+        s.bias_data_type = self.bias_data_type or 0
+        self._run(s, stream, "ActivationTransform::encode_fp_in_place")
+
+    def encode_quantize(self, input: torch.Tensor, q_out: torch.Tensor, scales_out: torch.Tensor,
+                        group_sums_out: Optional[torch.Tensor], rht_factors: torch.Tensor, batch_size: int,
+                        element_count: int, stream=None) -> None:
+        q = self.quantization
+        assert q is not None and (q.sum_group_size is None) == (group_sums_out is None)
+        s = self._base(rht_factors, batch_size, element_count)
+        s.input, s.q_out, s.scales_out, s.group_sums_out = _ptr(input), _ptr(q_out), _ptr(scales_out), \
+            _ptr(group_sums_out)
+        s.scale_group_size = q.scale_group_size
+        s.sum_group_size = q.sum_group_size or 0
+        s.grouped_by_nibble = int(q.code_layout == GROUPED_BY_NIBBLE)
+        self._run(s, stream, "ActivationTransform::encode_quantize")
+
+
+@dataclass
+class GatedActMulSettings:
+    """GatedActMulSettings (gated_act_mul.rs:21-27): clip bounds are (min, max) or None."""
+    activation_alpha: Optional[float] = None
+    gate_clipping: Optional[tuple] = None
+    value_clipping: Optional[tuple] = None
+
+
+class GatedActMul:
+    """GatedActMul (gated_act_mul.rs:29-190) over stark_qmm_gated_act_mul."""
+
+    def __init__(self, data_type: int, interleaved: bool, use_hadamard: bool, settings: GatedActMulSettings,
+                 quantization: Optional[ActivationQuantization]):
+        self.data_type, self.interleaved, self.use_hadamard = data_type, interleaved, use_hadamard
+        self.settings, self.quantization = settings, quantization
+
+    @classmethod
+    def full_precision(cls, data_type: int, interleaved: bool, use_hadamard: bool,
+                       settings: GatedActMulSettings = GatedActMulSettings()):
+        return cls(data_type, interleaved, use_hadamard, settings, None)
+
+    @classmethod
+    def quantized(cls, data_type: int, quantization: ActivationQuantization,
+                  settings: GatedActMulSettings = GatedActMulSettings()):
+        return cls(data_type, True, True, settings, quantization)
+
+    def _base(self, act_operand, factors, gated_dim, batch_dim, act_type) -> _GatedArgs:
+        s = _GatedArgs()
+        s.struct_size = C.sizeof(_GatedArgs)
+        s.data_type, s.act_type, s.interleaved = self.data_type, act_type, int(self.interleaved)
+        s.act_operand = _ptr(act_operand)
+        s.hadamard_factors = _ptr(factors)
+        s.gated_dim, s.batch_dim = gated_dim, batch_dim
+        st = self.settings
+        if st.activation_alpha is not None:
+            s.has_activation_alpha, s.activation_alpha = 1, st.activation_alpha
+        if st.gate_clipping is not None:
+            s.clip_gate, (s.gate_clip_min, s.gate_clip_max) = 1, st.gate_clipping
+        if st.value_clipping is not None:
+            s.clip_value, (s.value_clip_min, s.value_clip_max) = 1, st.value_clipping
+        return s
+
+    def encode_fp(self, act_operand: torch.Tensor, value_operand: Optional[torch.Tensor], output: torch.Tensor,
+                  hadamard_factors: Optional[torch.Tensor], gated_dim: int, batch_dim: int, value_offset: int,
+                  value_row_stride: int, act_type: int, stream=None) -> None:
+        assert self.quantization is None and self.interleaved == (value_operand is None)
+        assert self.use_hadamard == (hadamard_factors is not None)
+        s = self._base(act_operand, hadamard_factors, gated_dim, batch_dim, act_type)
+        s.op = GATED_FULL_PRECISION
+        s.value_operand, s.fp_out = _ptr(value_operand), _ptr(output)
+        s.value_offset, s.value_row_stride = value_offset, value_row_stride
+        _check(lib().stark_qmm_gated_act_mul(C.byref(s), _stream(stream)), "GatedActMul::encode_fp")
+
+    def encode_quantized(self, act_operand: torch.Tensor, values: torch.Tensor, scales: torch.Tensor,
+                         group_sums: Optional[torch.Tensor], hadamard_factors: torch.Tensor, gated_dim: int,
+                         batch_dim: int, act_type: int, stream=None) -> None:
+        q = self.quantization
+        assert q is not None and (q.sum_group_size is None) == (group_sums is None)
+        s = self._base(act_operand, hadamard_factors, gated_dim, batch_dim, act_type)
+        s.op = GATED_QUANTIZE if q.sum_group_size is None else GATED_QUANTIZE_WITH_GROUP_SUMS
+        s.q_out, s.scales_out, s.group_sums_out = _ptr(values), _ptr(scales), _ptr(group_sums)
+        s.scale_group_size = q.scale_group_size
+        s.sum_group_size = q.sum_group_size or q.scale_group_size
+        s.grouped_by_nibble = int(q.code_layout == GROUPED_BY_NIBBLE)
+        _check(lib().stark_qmm_gated_act_mul(C.byref(s), _stream(stream)), "GatedActMul::encode_quantized")
 
 
 # ---------------------------------------------------------------- hybrid engine
