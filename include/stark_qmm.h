@@ -322,6 +322,39 @@ STARK_QMM_API stark_qmm_status stark_qmm_routed_experts(const stark_qmm_routed_a
 STARK_QMM_API stark_qmm_status stark_qmm_routed_experts_static(const stark_qmm_routed_args* args, void* stream);
 
 /* ------------------------------------------------------------------ */
+/* BF16-effective affine reference dot                                 */
+/* ------------------------------------------------------------------ */
+
+typedef struct stark_qmm_reference_affine_args {
+    uint32_t struct_size;
+    const void* input;           /* bf16 [M, K] at input + input_offset */
+    uint64_t input_offset;       /* bytes */
+    uint64_t input_size;         /* bytes available at input */
+    /* FullPrecision (codes == NULL): bf16 values [bank, K], values_size bytes.
+     * Quantized: U4/U5/U6/U8 codes, group 64, bf16 scales and biases (correction
+     * BIASES), unsigned codes; the bank is codes_size / (K * bits / 8) rows and
+     * params must describe exactly that bank. */
+    stark_qmm_b weights;
+    uint64_t values_size;
+    uint64_t scales_size, biases_size; /* bytes */
+    uint32_t source_output_width_count; /* non-zero: a fused-source matrix, which keeps its own route */
+    const uint32_t* indices;     /* [M*N] bank row per output, or NULL (row = column, N <= bank) */
+    uint64_t indices_size;       /* bytes */
+    void* output;                /* [M, N] in output_dtype */
+    uint32_t output_dtype;       /* BF16, or F32 = the bf16 result widened */
+    uint32_t m, n, k;
+} stark_qmm_reference_affine_args;
+
+/* Replaces ReferenceAffineBF16Matmul::encode
+ * (src/encodable_block/linear/reference_affine.rs:105-280; kernel
+ * src/backends/cpu/kernel/matmul/vision.rs:249-336): w = bf16(code * scale +
+ * bias), 32 fma partial sums over K in steps of 32 and the fixed 8x4 tree,
+ * bit-identical to the reference. Bounds as ReferenceAffinePlan
+ * (reference_affine.rs:55-96); a gathered row outside the bank gives NaN. The
+ * caller provides the output (the reference allocates it). */
+STARK_QMM_API stark_qmm_status stark_qmm_reference_affine_bf16(const stark_qmm_reference_affine_args* args, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* Activation transforms and gated activations                        */
 /* ------------------------------------------------------------------ */
 

@@ -131,6 +131,14 @@ class _WeightMatrix(C.Structure):
                 ("device", C.c_void_p * 3)]
 
 
+class _RefAffineArgs(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("input", C.c_void_p), ("input_offset", C.c_uint64),
+                ("input_size", C.c_uint64), ("weights", _B), ("values_size", C.c_uint64), ("scales_size", C.c_uint64),
+                ("biases_size", C.c_uint64), ("source_output_width_count", C.c_uint32), ("indices", C.c_void_p),
+                ("indices_size", C.c_uint64), ("output", C.c_void_p), ("output_dtype", C.c_uint32),
+                ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32)]
+
+
 class _TransformArgs(C.Structure):
     _fields_ = [("struct_size", C.c_uint32), ("op", C.c_uint32), ("data_type", C.c_uint32), ("in_place", C.c_uint32),
                 ("input", C.c_void_p), ("output", C.c_void_p), ("bias", C.c_void_p), ("bias_data_type", C.c_uint32),
@@ -190,6 +198,7 @@ SIGNATURES = {
                                                   C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(_WeightMatrix),
                                                   C.c_void_p]),
     "stark_qmm_weight_matrix_free": (None, [C.POINTER(_WeightMatrix)]),
+    "stark_qmm_reference_affine_bf16": (C.c_uint32, [C.POINTER(_RefAffineArgs), C.c_void_p]),
     "stark_qmm_activation_transform": (C.c_uint32, [C.POINTER(_TransformArgs), C.c_void_p]),
     "stark_qmm_gated_act_mul": (C.c_uint32, [C.POINTER(_GatedArgs), C.c_void_p]),
 }
@@ -236,8 +245,8 @@ def _ptr(t: Optional[torch.Tensor]):
     return t.data_ptr()
 
 
-def _nbytes(t: torch.Tensor) -> int:
-    return t.numel() * t.element_size()
+def _nbytes(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
 
 
 def _stream(stream) -> int:
@@ -413,6 +422,39 @@ class MatmulKernel:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------- BF16-effective reference dot
+
+class ReferenceAffineBF16Matmul:
+    """ReferenceAffineBF16Matmul (reference_affine.rs:105-280) over
+    stark_qmm_reference_affine_bf16. encode() returns the [m, n] output it
+    allocates, as the reference returns its scratch buffer."""
+
+    def __init__(self, output_type: int):
+        if output_type not in (BF16, F32):
+            raise MatmulError(UNSUPPORTED_DATA_TYPE, "ReferenceAffineBF16Matmul::new")
+        self.output_type = output_type
+
+    def encode(self, input: torch.Tensor, input_offset: int, weights, indices: Optional[torch.Tensor], m: int,
+               n: int, k: int, stream=None, source_output_widths: Sequence[int] = ()) -> torch.Tensor:
+        s = _RefAffineArgs()
+        s.struct_size = C.sizeof(_RefAffineArgs)
+        s.input, s.input_offset, s.input_size = _ptr(input), input_offset, _nbytes(input)
+        _fill_b(s.weights, weights)
+        if isinstance(weights, FullPrecisionB):
+            s.values_size = _nbytes(weights.values)
+        elif isinstance(weights, QuantizedB):
+            s.scales_size = _nbytes(weights.scales)
+            s.biases_size = _nbytes(weights.correction_data)
+        s.source_output_width_count = len(source_output_widths)
+        s.indices, s.indices_size = _ptr(indices), _nbytes(indices)
+        out = torch.empty(m * n, dtype=torch.float32 if self.output_type == F32 else torch.int16,
+                          device=input.device)
+        s.output, s.output_dtype = _ptr(out), self.output_type
+        s.m, s.n, s.k = m, n, k
+        _check(lib().stark_qmm_reference_affine_bf16(C.byref(s), _stream(stream)), "ReferenceAffineBF16Matmul::encode")
+        return out
 
 
 # ---------------------------------------------------------------- activation transforms
