@@ -496,6 +496,34 @@ def bf16_effective_reference(O, W, x, m, n, k, bits, gs, layout, correction, w_d
     return xf @ w.T, np.abs(xf) @ np.abs(w).T
 
 
+def _ref_strides(layout, n, k):
+    return (k // 64, 1) if layout == 0 else (1, (n + 3) // 4 * 4)
+
+
+def test_prefill_gemm_full_width(qmm, oracle):
+    """Config-4 prefill at full width: M = 2048, N = 12288, K = 4096, 4-bit g64
+    with GroupOutput planes (the converted artifact's layout), bf16 output.
+    Rows 0, 2047 and 14 random rows against the oracle's BF16-effective
+    reference dot (vision.rs:249-336) on every column."""
+    m, n, k = 2048, 12288, 4096
+    rng = np.random.default_rng(2048)
+    W = H.affine_weights(oracle, rng, n, k, 4, 64, 1, 1, H.BF16)
+    x = H.activations(oracle, rng, m, k, H.BF16)
+    d = torch_empty(m * n, H.BF16)
+    qmm.MatmulKernel(H.BF16, H.BF16, H.BF16).encode(qmm.MatmulArguments(a=H.to_dev(x), m=m, n=n, k=k, d=d, b=qmm.QuantizedB(
+        codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]), params=qmm.QuantParams(1, n, k // 64),
+        mode=qmm.MODE_U4, correction_data=H.to_dev(W["corr"]))))
+    torch.cuda.synchronize()
+    got = oracle.bf16_to_f32(H.from_dev(d, np.uint16)).reshape(m, n)
+    rows = np.concatenate([[0, m - 1], rng.choice(np.arange(1, m - 1), 14, replace=False)])
+    xs = x.reshape(m, k)[rows].ravel()
+    sos, sgs = _ref_strides(1, n, k)
+    ref = oracle.reference_affine_linear_bf16(xs, W["codes"], W["scales"], W["corr"], len(rows), n, k, bits=4,
+                                              sos=sos, sgs=sgs, f32_out=True).reshape(len(rows), n)
+    _, mag = bf16_effective_reference(oracle, W, xs, len(rows), n, k, 4, 64, 1, 1, H.BF16, False)
+    check(got[rows].ravel(), ref.ravel(), mag=mag.ravel(), label="full-width prefill")
+
+
 @pytest.mark.parametrize("m,n,k", [(17, 96, 512), (64, 256, 1024), (200, 300, 4096), (2048, 128, 256), (520, 136, 320),
                                    (130, 1000, 192)])
 @pytest.mark.parametrize("bits", [4, 8])
@@ -518,6 +546,11 @@ def test_prefill_gemm_shapes(qmm, oracle, m, n, k, bits):
     got = H.from_dev(d, np.float32).reshape(m, n)
     want, mag = bf16_effective_reference(oracle, W, x, m, n, k, bits, 64, layout, 1, H.BF16, False)
     check(got.ravel(), want.ravel(), mag=mag.ravel(), label=f"gemm m{m} n{n} k{k} b{bits}")
+    # the oracle's restatement of the reference's BF16-effective dot (vision.rs:249-336)
+    sos, sgs = _ref_strides(layout, n, k)
+    ref = oracle.reference_affine_linear_bf16(x, W["codes"], W["scales"], W["corr"], m, n, k, bits=bits, sos=sos,
+                                              sgs=sgs, f32_out=True)
+    check(got.ravel(), ref, mag=mag.ravel(), label=f"gemm vs reference dot m{m} n{n} k{k} b{bits}")
     st, exact = oracle.matmul(a=x, m=m, n=n, k=k, codes=W["codes"], scales=W["scales"], correction_data=W["corr"],
                               layout=layout, bits=bits, group_size=64, output_dt=H.F32, threads=8)
     assert st == 0
