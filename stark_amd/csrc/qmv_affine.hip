@@ -22,6 +22,8 @@
 //     s*sum(x*q) + b*sum(x) = 16s * sum(x*(1+q/16)) + (b - 16s) * sum(x)
 // * other types: v_cvt_f32_ubyte + f32 FMA;
 // * rows are reduced across the wave at the end.
+#include <cstdlib>
+
 #include "qmm_common.h"
 
 namespace qmm {
@@ -569,11 +571,19 @@ stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stre
 // (weights are re-streamed once per pair of M rows).
 stark_qmm_status launch_affine_gemv(const AffineOp* ops_in, uint32_t count_in, int bits, hipStream_t stream) {
     if (count_in == 0) return STARK_QMM_OK;
+    // Diagnostic switch: STARK_QMM_FORCE_VALU_DECODE=1 sends the products the
+    // matrix-core kernels would take to the VALU decode kernel where it is
+    // eligible (for counter comparisons of the two designs; results stay within
+    // the parity bar either way).
+    static const bool force_valu = [] {
+        const char* e = getenv("STARK_QMM_FORCE_VALU_DECODE");
+        return e && e[0] == '1';
+    }();
     // decode-shaped 4-bit products go to the wave-independent decode kernel
     std::vector<AffineOp> mfma, decode, others;
     for (uint32_t i = 0; i < count_in; ++i) {
         const AffineOp& o = ops_in[i];
-        if (mfma_eligible(o, bits)) {
+        if (mfma_eligible(o, bits) && !(force_valu && decode_eligible(o, bits))) {
             mfma.push_back(o);
             continue;
         }
