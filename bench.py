@@ -536,6 +536,7 @@ def config3(args, torch, Q):
                                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
 
 
+PEAK_MFMA_INT8_TOPS = 5000.0
 PEAK_MFMA_BF16_TFLOPS = 2500.0
 
 
@@ -570,8 +571,50 @@ def config4(args, torch, Q):
                       "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_MFMA_BF16_TFLOPS,
                                    "unit": "TFLOP/s", "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4),
                                    "traffic": None}}))
+    a8_prefill_line(args, torch, Q, layer, stream)
     if args.decode_tokens:
         decode_line(args, torch)
+
+
+def a8_prefill_line(args, torch, Q, layer, stream):
+    """Config 4 prefill with int8 activations (MatmulA::Int8Symmetric, the
+    A8W4 path): M=2048 codes per projection input (activation groups of 128,
+    grouped-by-nibble order, made by the library's own quantizing transform),
+    the same W4 g64 weights, on the int8 matrix-core GEMM."""
+    Mtok, AG = 2048, 128
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 5)
+    kern = Q.MatmulKernel(Q.BF16, Q.BF16, Q.BF16)
+    quant = Q.ActivationTransform.quantize(Q.BF16, Q.ActivationQuantization.new(AG, GROUP, False, Q.GROUPED_BY_NIBBLE))
+    acts = {}
+    for k in (4096, 12288):
+        x = torch.randn(Mtok * k, generator=gen, device="cuda").to(torch.bfloat16)
+        f = (torch.randint(0, 2, (k,), generator=gen, device="cuda", dtype=torch.int32) * 2 - 1)
+        codes = torch.empty(Mtok * k, dtype=torch.int8, device="cuda")
+        scales = torch.empty(Mtok * k // AG, dtype=torch.float32, device="cuda")
+        quant.encode_quantize(x.view(torch.int16), codes, scales, None, f, Mtok, k, stream)
+        acts[k] = Q.Int8SymmetricA(values=codes, scales=scales, scale_group_size=AG, code_layout=Q.GROUPED_BY_NIBBLE)
+    outs = [torch.empty(Mtok * mat["n"], dtype=torch.int16, device="cuda") for mat in layer]
+    args_list = [Q.MatmulArguments(a=acts[mat["k"]], m=Mtok, n=mat["n"], k=mat["k"], d=out,
+                                   b=Q.QuantizedB(codes=mat["codes"], scales=mat["scales"],
+                                                  params=Q.QuantParams(Q.GROUP_OUTPUT, mat["n"], mat["k"] // GROUP),
+                                                  correction_data=mat["biases"]))
+                 for mat, out in zip(layer, outs)]
+    ms = timed(torch, lambda i: [kern.encode(a, stream) for a in args_list], args.steps, args.warmup, stream)
+    ops = sum(2 * Mtok * n * k for _, n, k in SHAPES)
+    tops = ops / (ms * 1e-3) / 1e12
+    print(json.dumps({"metric": "Qwen3-8B A8W4 prefill int8 GEMM TOP/s", "value": round(tops, 1), "unit": "TOP/s",
+                      "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+                      "data": "synthetic: N(0,0.02) weights W4 g64, N(0,1) activations RHT-quantized to int8 "
+                              "(scale groups of 128)",
+                      "config": {"workload": f"config 4 prefill, int8 activations: M={Mtok} through "
+                                             "q,k,v,o,gate,up,down (one layer)",
+                                 "ops_per_step": ops, "prefill_tokens_per_s_36_layers":
+                                     round(Mtok * 1000.0 / (ms * LAYERS), 1)},
+                      "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": PEAK_MFMA_INT8_TOPS,
+                                   "unit": "TOP/s", "frac": round(tops / PEAK_MFMA_INT8_TOPS, 4),
+                                   "traffic": None}}))
 
 
 def decode_measure(args, torch):

@@ -156,10 +156,283 @@ __global__ __launch_bounds__(256) void qmv_a8_generic(AffineOp op, A8Operand a, 
     epilogue(op, m, n, acc);
 }
 
+
+// ---- Prefill form (M > 16): int8 GEMM on the matrix cores.
+// A 128x128 output tile per workgroup (4 waves, 64x64 each, 4x4 blocks of
+// v_mfma_i32_16x16x64_i8; a 32-wide chunk masks the other half's activations). K is
+// walked in steps of 64; each step's activation codes and weight codes (4-bit
+// unpacked to bytes, 8-bit as q - 128) are staged in LDS as int8 in the same
+// k order, so every MFMA sums q_a * q_w exactly in int32 over one flush chunk
+// of G = min(activation group, weight group, 64) values. Per chunk and output
+//   acc += (scale_a * s) * C + (scale_a * sum q_a) * bias_term
+// (8-bit weights: bias_term + 128 s, for the q - 128 offset), in f32. The
+// chunk sums of q_a come from v_dot4 during staging. The k order inside a
+// chunk does not matter (integer sums), so sequential activation codes meet
+// weight bytes permuted to sequential order and grouped-by-nibble codes meet
+// the nibble split as it falls out of the weight word.
+#ifndef QMM_A8_WPE
+#define QMM_A8_WPE 2
+#endif
+constexpr int kGB = 128;         // tile rows (M) and columns (N)
+constexpr int kGK = 64;          // k per step
+constexpr int kGRow = kGK + 16;  // LDS row bytes: the 80-byte stride spreads a 16-row read over the banks
+
+struct A8GemmLds {
+    u32x4 a[2][kGB][kGRow / 16];  // int8 codes, 16 per element
+    u32x4 b[2][kGB][kGRow / 16];
+    float sa[2][2][kGB];  // [buf][chunk][row] activation scale
+    float ua[2][2][kGB];  // [buf][chunk][row] activation scale * chunk sum of codes
+    float ws[2][2][kGB];  // [buf][chunk][col] weight scale
+    float wb[2][2][kGB];  // [buf][chunk][col] bias term (8-bit: + 128 s)
+};
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t a8_rsrc(const void* p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)min(bytes, (size_t)0x7fffffff), 0x00020000);
+}
+
+template <int AUX = 0>
+__device__ __forceinline__ u32x4 a8_load16_impl(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+}
+// aux 2: nontemporal (weights are streamed once per output tile row)
+__device__ __forceinline__ u32x4 a8_load16(__amdgpu_buffer_rsrc_t r, uint32_t off, int nt = 0) {
+    return nt ? a8_load16_impl<2>(r, off) : a8_load16_impl<0>(r, off);
+}
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int BITS, int G, bool SIGNED, bool GROUPED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_A8_WPE))) void qgemm_a8(AffineOp op, A8Operand a) {
+    __shared__ A8GemmLds lds;
+    constexpr int NCH = kGK / G;  // flush chunks per step
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t M = op.m, N = op.n, K = op.k, GA = K / a.group;
+    const uint32_t m0 = blockIdx.y * kGB, n0 = blockIdx.x * kGB;
+    const size_t wrow = (size_t)K * BITS / 8;
+
+    // staging roles: activation rows ar and 64 + ar, 16 bytes at aq * 16;
+    // 4-bit weights: row tid / 2, 16 bytes (32 codes) at (tid % 2) * 16;
+    // 8-bit weights: rows ar and 64 + ar, 16 bytes at aq * 16;
+    // weight metadata: column tid (tid < 128).
+    // Every load is a buffer load whose resource ends at the operand's last
+    // byte: rows past M or N read zeros, with no branch around any load.
+    const uint32_t ar = tid >> 2, aq = tid & 3;
+    const uint32_t lga = 31 - __builtin_clz(a.group), lgw = 31 - __builtin_clz(op.group_size);
+    const __amdgpu_buffer_rsrc_t ra = a8_rsrc(a.codes, (size_t)M * K);
+    const __amdgpu_buffer_rsrc_t rsa = a8_rsrc(a.scales, (size_t)M * GA * 4);
+    const __amdgpu_buffer_rsrc_t rw = a8_rsrc(op.codes, (size_t)N * wrow);
+    const __amdgpu_buffer_rsrc_t rps = a8_rsrc(op.scales, 0x7fffffffu);
+    const __amdgpu_buffer_rsrc_t rpb = a8_rsrc(op.corr, 0x7fffffffu);
+    const bool biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES, bfp = op.w_dt == STARK_QMM_BF16;
+    struct Stage {
+        u32x4 xa[2];
+        u32x4 wc[BITS / 4];
+        float sa[2];
+        uint32_t s[NCH], b[NCH];  // raw plane values
+    };
+    auto load = [&](Stage& st, uint32_t k0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t m = m0 + ar + 64 * h;
+            st.xa[h] = a8_load16(ra, m * K + k0 + aq * 16);
+            st.sa[h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                     rsa, (m * GA + ((k0 + aq * 16) >> lga)) * 4, 0, 0));
+        }
+#pragma unroll
+        for (int h = 0; h < BITS / 4; ++h) {
+            const uint32_t r = BITS == 4 ? (uint32_t)tid >> 1 : ar + 64 * h;
+            const uint32_t off = BITS == 4 ? ((uint32_t)tid & 1) * 16 : aq * 16;
+            st.wc[h] = a8_load16(rw, (n0 + r) * (uint32_t)wrow + k0 * BITS / 8 + off, 2);
+        }
+        // plane entries of column n0 + tid (threads past 128 read a valid
+        // entry too and never store it); past N they are ignored
+        const uint32_t n = min(n0 + ((uint32_t)tid & (kGB - 1)), N - 1);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t md = n * op.os + ((k0 + c * G) >> lgw) * op.gs;
+            st.s[c] = __builtin_amdgcn_raw_buffer_load_b16(rps, md * 2, 0, 0);
+            st.b[c] = __builtin_amdgcn_raw_buffer_load_b16(rpb, biased ? md * 2 : 0x80000000u, 0, 0);
+        }
+    };
+    auto store = [&](const Stage& st, int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t r = ar + 64 * h;
+            lds.a[buf][r][aq] = st.xa[h];
+            int sum = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_sdot4((int)st.xa[h][t], 0x01010101, sum, false);
+            sum += __shfl_xor(sum, 1, 64);
+            if (G == 64) sum += __shfl_xor(sum, 2, 64);
+            if (G == 64 ? aq == 0 : (aq & 1) == 0) {
+                const uint32_t c = G == 64 ? 0 : aq >> 1;
+                lds.sa[buf][c][r] = st.sa[h];
+                lds.ua[buf][c][r] = st.sa[h] * (float)sum;
+            }
+        }
+        if (BITS == 4) {
+            const uint32_t r = (uint32_t)tid >> 1, off = ((uint32_t)tid & 1) * 32;
+            uint32_t out[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                uint32_t w = st.wc[0][t];
+                if (SIGNED) w ^= 0x88888888u;
+                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;  // (v0,v2,v4,v6), (v1,v3,v5,v7)
+                out[2 * t] = GROUPED ? lo : __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+                out[2 * t + 1] = GROUPED ? hi : __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+            }
+            lds.b[buf][r][off / 16] = u32x4{out[0], out[1], out[2], out[3]};
+            lds.b[buf][r][off / 16 + 1] = u32x4{out[4], out[5], out[6], out[7]};
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                u32x4 w = st.wc[h];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) w[t] ^= SIGNED ? 0u : 0x80808080u;  // q - 128 as int8
+                if (GROUPED) {
+                    const uint32_t e0 = __builtin_amdgcn_perm(w[1], w[0], 0x06040200u);
+                    const uint32_t o0 = __builtin_amdgcn_perm(w[1], w[0], 0x07050301u);
+                    const uint32_t e1 = __builtin_amdgcn_perm(w[3], w[2], 0x06040200u);
+                    const uint32_t o1 = __builtin_amdgcn_perm(w[3], w[2], 0x07050301u);
+                    w = u32x4{e0, o0, e1, o1};
+                }
+                lds.b[buf][ar + 64 * h][aq] = w;
+            }
+        }
+        if (tid < kGB) {
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const float sc = bfp ? bf16_bits_to_f32(st.s[c]) : f16_bits_to_f32(st.s[c]);
+                const float bt = biased ? (bfp ? bf16_bits_to_f32(st.b[c]) : f16_bits_to_f32(st.b[c]))
+                                        : -sc * (float)(1 << (BITS - 1));
+                lds.ws[buf][c][tid] = sc;
+                lds.wb[buf][c][tid] = BITS == 8 ? bt + 128.0f * sc : bt;
+            }
+        }
+    };
+
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint32_t li = lane & 15, lq = lane >> 4;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+    // per chunk: the wave's B fragments and weight metadata once, then each
+    // row block's 4 MFMAs and its flush (16 int32 accumulators live at a time)
+    auto compute = [&](int buf) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 1
+        for (int c = 0; c < NCH; ++c) {
+            float s4[4], b4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s4[j] = lds.ws[buf][c][wn * 64 + 16 * j + li];
+                b4[j] = lds.wb[buf][c][wn * 64 + 16 * j + li];
+            }
+            u32x4 bfr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bfr[j] = lds.b[buf][wn * 64 + 16 * j + li][lq];
+            i32x4_t cz = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                u32x4 af = lds.a[buf][wm * 64 + 16 * i + li][lq];
+                // a 32-wide chunk keeps the activation bytes of its own half of
+                // the step (lanes 16 lq read bytes 16 lq ..), the other half zero
+                if (G == 32 && (lq >> 1) != (uint32_t)c) af = u32x4{0, 0, 0, 0};
+                i32x4_t C[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    C[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, af),
+                                                                 __builtin_bit_cast(i32x4_t, bfr[j]),
+                                                                 cz, 0, 0, 0);
+                // C element e of block (i, j): row 4 lq + e, column li
+                const f32x4 sa = *(const f32x4*)&lds.sa[buf][c][wm * 64 + 16 * i + 4 * lq];
+                const f32x4 ua = *(const f32x4*)&lds.ua[buf][c][wm * 64 + 16 * i + 4 * lq];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[i][j][e] = fmaf(sa[e] * s4[j], (float)C[j][e], fmaf(ua[e], b4[j], acc[i][j][e]));
+                // the next row block's MFMAs start after this flush: their zero
+                // accumulator input is tied to this block's results, so only one
+                // block's 16 int32 sums are live (two waves per SIMD fit the registers)
+                asm volatile("" : "+v"(cz) : "v"(acc[i][0]), "v"(acc[i][1]), "v"(acc[i][2]), "v"(acc[i][3]));
+            }
+            // keep the chunks apart: hoisting the next chunk's fragments and
+            // MFMAs above this flush would not fit the register budget
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    const auto barrier = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+    // one register stage: step s computes from LDS buffer s % 2 while step
+    // s + 1's loads fly; they are staged into the other buffer after the compute
+    // (the last step's re-read of its own tile lands in a buffer not read again)
+    const uint32_t steps = K / kGK;
+    Stage stg;
+    load(stg, 0);
+    store(stg, 0);
+    barrier();
+    for (uint32_t st = 0; st < steps; ++st) {
+        load(stg, min(st + 1, steps - 1) * kGK);
+        compute(st & 1);
+        store(stg, (st & 1) ^ 1);
+        barrier();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = m0 + wm * 64 + 16 * i + 4 * lq + e;
+                const uint32_t n = n0 + wn * 64 + 16 * j + li;
+                if (m < M && n < N) epilogue(op, m, n, acc[i][j][e]);
+            }
+}
+
+template <int BITS, int G>
+void launch_gemm_a8(const AffineOp& op, const A8Operand& a, hipStream_t stream) {
+    const dim3 grid((op.n + kGB - 1) / kGB, (op.m + kGB - 1) / kGB);
+    const bool sg = (op.flags & FLAG_SIGNED) != 0, gr = a.grouped != 0;
+    if (sg && gr)
+        hipLaunchKernelGGL((qgemm_a8<BITS, G, true, true>), grid, dim3(256), 0, stream, op, a);
+    else if (sg)
+        hipLaunchKernelGGL((qgemm_a8<BITS, G, true, false>), grid, dim3(256), 0, stream, op, a);
+    else if (gr)
+        hipLaunchKernelGGL((qgemm_a8<BITS, G, false, true>), grid, dim3(256), 0, stream, op, a);
+    else
+        hipLaunchKernelGGL((qgemm_a8<BITS, G, false, false>), grid, dim3(256), 0, stream, op, a);
+}
+
 }  // namespace
 
 stark_qmm_status launch_affine_a8(const AffineOp& op, const A8Operand& a, int bits, hipStream_t stream) {
     if (op.m == 0 || op.n == 0) return STARK_QMM_OK;
+    // prefill sizes: the int8 GEMM on the matrix cores
+    if (op.m > 16 && !op.gather && op.k % kGK == 0 && (((uintptr_t)op.codes | (uintptr_t)a.codes) & 15) == 0 &&
+        op.corr_kind != STARK_QMM_CORRECTION_ZERO_POINTS && op.w_dt != STARK_QMM_F32 &&
+        (uint64_t)op.m * op.k < (1ull << 31) && (uint64_t)op.n * op.k * bits / 8 < (1ull << 31)) {
+        const bool g32 = a.group == 32 || op.group_size == 32;
+        if (bits == 4 && g32)
+            launch_gemm_a8<4, 32>(op, a, stream);
+        else if (bits == 4)
+            launch_gemm_a8<4, 64>(op, a, stream);
+        else if (g32)
+            launch_gemm_a8<8, 32>(op, a, stream);
+        else
+            launch_gemm_a8<8, 64>(op, a, stream);
+        QMM_HIP_CHECK(hipGetLastError());
+        return STARK_QMM_OK;
+    }
     const uint32_t vpp = bits == 4 ? 32 : 16;
     const bool fast = !op.gather && op.k % vpp == 0 && ((uintptr_t)op.codes & 15) == 0 &&
                       ((size_t)op.k * bits / 8) % 16 == 0 && ((uintptr_t)a.codes & 3) == 0 && op.k % 4 == 0;

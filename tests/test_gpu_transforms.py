@@ -409,3 +409,47 @@ def test_output_rht_dop_full_precision_a(qmm, oracle, out_dt, m):
     mag = H.dequant_magnitude(oracle, w["codes"], w["scales"], w["corr"], n, k, 4, 64, 0, 1, BF16, x, BF16, m)
     mag = np.repeat(mag.reshape(m, n // 32, 32).sum(-1, keepdims=True), 32, axis=-1) / np.sqrt(32)
     check(got, want, mag=mag, label=f"rht m{m}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("ag,wg,grouped", [(128, 64, True), (64, 64, False), (32, 32, True), (128, 32, False),
+                                           (32, 128, True)])
+def test_a8_prefill_gemm(qmm, oracle, bits, ag, wg, grouped):
+    """M > 16 runs the int8 GEMM on v_mfma_i32_16x16x64_i8 (partial tiles in
+    M, N and K steps), against the oracle within the accumulation bar."""
+    rng = np.random.default_rng(bits * 31 + ag + wg + grouped)
+    for m, n, k in ((40, 136, 512), (130, 96, 384)):
+        _a8_case(qmm, oracle, rng, m, n, k, bits, wg, ag, grouped, label=f"gemm m{m} n{n} k{k}")
+    _a8_case(qmm, oracle, rng, 33, 64, 256, bits, wg, ag, grouped, correction=0, signed=True, label="sym signed")
+    _a8_case(qmm, oracle, rng, 20, 64, 256, bits, wg, ag, grouped, bias=True, rht=True, out_dt=BF16, label="rht bf16")
+
+
+def test_a8_prefill_full_width(qmm, oracle):
+    """The A8W4 prefill shape: M = 2048, N = 4096, K = 4096 (activation groups
+    128, weight groups 64, grouped codes), 24 sampled rows against the oracle."""
+    rng = np.random.default_rng(77)
+    m, n, k, ag, wg = 2048, 4096, 4096, 128, 64
+    w = H.affine_weights(oracle, rng, n, k, bits=4, gs=wg)
+    q, sc = _a8_inputs(oracle, rng, m, k, ag, True)
+    d = _dev_empty(m * n, torch.float32)
+    b = qmm.QuantizedB(codes=H.to_dev(w["codes"]), scales=H.to_dev(w["scales"]),
+                       params=qmm.QuantParams(layout=0, row_count=n, group_count=k // wg), mode=qmm.MODE_U4,
+                       group_size=wg, correction=qmm.BIASES, correction_data=H.to_dev(w["corr"]))
+    A = qmm.Int8SymmetricA(values=H.to_dev(q), scales=H.to_dev(sc), scale_group_size=ag,
+                           code_layout=qmm.GROUPED_BY_NIBBLE)
+    qmm.MatmulKernel(BF16, BF16, F32).encode(qmm.MatmulArguments(a=A, b=b, d=d, m=m, n=n, k=k))
+    torch.cuda.synchronize()
+    got = d.cpu().numpy().reshape(m, n)
+    rows = np.concatenate([[0, m - 1], rng.choice(np.arange(1, m - 1), 22, replace=False)])
+    qs = q.reshape(m, k)[rows].ravel()
+    ss = sc.reshape(m, k // ag)[rows].ravel()
+    st, want = oracle.matmul(a=np.zeros(len(rows) * k, np.uint16), m=len(rows), n=n, k=k, codes=w["codes"],
+                             scales=w["scales"], correction=1, correction_data=w["corr"], layout=0, row_count=n,
+                             group_count=k // wg, bits=4, group_size=wg, output_dt=F32, a_codes=qs, a_scales=ss,
+                             a_scale_group_size=ag, a_grouped_by_nibble=True, threads=8)
+    assert st == 0
+    xf = (qs.astype(np.float32).reshape(len(rows), k)[:, [oracle.int8_code_index(True, i) for i in range(k)]]
+          * np.repeat(ss.reshape(len(rows), k // ag), ag, axis=1)).astype(np.float32)
+    mag = H.dequant_magnitude(oracle, w["codes"], w["scales"], w["corr"], n, k, 4, wg, 0, 1, BF16, xf.ravel(), F32,
+                              len(rows))
+    check(got[rows].ravel(), want, mag=mag, label="a8 prefill full width")
