@@ -328,7 +328,8 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
 //    workgroups per CU: more bytes in flight only lengthen the queues.
 //  - Activations are staged per wave (no barrier) into one of kXR regions,
 //    as x * 2^E with a per-group exponent E (group_shift in qmm_common.h),
-//    tagged (op, chunk), so consecutive tiles of an op reuse them; the plane
+//    tagged (activation id, chunk), so consecutive tiles of ops that read the
+//    same activations (q/k/v, gate/up) reuse them; the plane
 //    vectors of a unit are loaded with the unit and pass through a
 //    wave-private LDS block at the flush.
 constexpr int kXR = 3;         // activation regions per wave
@@ -437,7 +438,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         const uint32_t t0 = (e & 0xffffffu) * kTR, n0 = min(t0, op.n - kTR);
         const uint32_t c = wave + 4 * ri;
         const uint32_t rg = ri % kXR;
-        const uint32_t tag = ((e >> 24) << 16) | c;
+        const uint32_t tag = (op.xid << 16) | c;
         u32x4* xpw = lds.xp[wave][rg];
         float* xsw = lds.xs[wave][rg];
         int* xew = lds.xe[wave][rg];
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         const uint32_t nc = more ? wave + 4 * nr : c;
         const AffineOp& nop = kb_->op[ne >> 24];
         const uint32_t nn0 = tile_row(nop, ne);
-        issue_aux(nop, nn0, nc, more && tag_of(nr % kXR) != (((ne >> 24) << 16) | nc));
+        issue_aux(nop, nn0, nc, more && tag_of(nr % kXR) != ((nop.xid << 16) | nc));
         const __amdgpu_buffer_rsrc_t ncr = code_rsrc(nop, nn0);
         const uint32_t nvo = more ? r * (nop.k / 2) + nc * UB + piece : OOB;
 
@@ -628,6 +629,14 @@ stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipSt
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = sorted[i];
+        // ops that read the same activations (q/k/v, gate/up) stage them once
+        uint32_t x = i;
+        for (uint32_t j = 0; j < i; ++j)
+            if (sorted[j].x == sorted[i].x && sorted[j].k == sorted[i].k) {
+                x = j;
+                break;
+            }
+        batch.op[i].xid = x;
         tiles += (sorted[i].n + kTR - 1) / kTR;
     }
     batch.count = count;
