@@ -355,6 +355,35 @@ typedef struct stark_qmm_reference_affine_args {
 STARK_QMM_API stark_qmm_status stark_qmm_reference_affine_bf16(const stark_qmm_reference_affine_args* args, void* stream);
 
 /* ------------------------------------------------------------------ */
+/* Sampling after the lm_head                                          */
+/* ------------------------------------------------------------------ */
+
+typedef struct stark_qmm_sampling_args {
+    uint32_t struct_size;
+    const void* logits;          /* [batch, vocab] in data_type (F32 or BF16) */
+    uint32_t data_type;
+    uint32_t* output;            /* [batch] token ids; 0xFFFFFFFF: non-finite logits or nothing left */
+    const uint64_t* seeds;       /* [batch] Philox keys: stochastic (Gumbel) sampling; NULL: greedy */
+    const uint32_t* bitmask;     /* [batch, ceil(vocab / 32)] allowed tokens, or NULL */
+    uint32_t has_temperature;
+    float temperature;
+    uint32_t has_top_k;
+    uint32_t top_k;
+    uint32_t has_top_p;
+    float top_p;
+    uint32_t has_min_p;
+    float min_p;
+    uint32_t vocab_size, batch_size;
+} stark_qmm_sampling_args;
+
+/* Replaces Sampling::encode's UnifiedSampling kernel
+ * (src/backends/cpu/kernel/sampling/unified_sampling.rs:14-117; noise
+ * src/encodable_block/sampling/gumbel.rs): bitmask, temperature, top-k / top-p /
+ * min-p prefix of the sorted logits, Gumbel noise from Philox4x32-10, argmax.
+ * Options are validated as SamplingMethod::validate (sampling/mod.rs:73-101). */
+STARK_QMM_API stark_qmm_status stark_qmm_unified_sampling(const stark_qmm_sampling_args* args, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* Activation transforms and gated activations                        */
 /* ------------------------------------------------------------------ */
 

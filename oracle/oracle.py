@@ -94,6 +94,10 @@ def _declare(l):
         "so_activate": (f, [i32, f, i32, i32, f]),
         "so_gated_act_mul": (i32, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, i32, i32, f, i32, f, f, i32, f, f,
                                    i32, i32, i32, i32, u32, u32, i32]),
+        "so_philox4x32_10": (None, [vp, vp, vp]),
+        "so_unit_interval": (f, [u32]),
+        "so_gumbel": (f, [C.c_uint64, u32, u32]),
+        "so_unified_sampling": (i32, [vp, i32, vp, vp, vp, i32, f, i32, u32, i32, f, i32, f, u32, u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(l, name)
@@ -304,6 +308,38 @@ def gated_act_mul(act, gated_dim, batch, act_type=SILU, value=None, value_offset
     if st:
         raise ValueError(f"so_gated_act_mul status {st}")
     return (q, sc, sums) if quantize else fp
+
+
+# ----------------------------------------------------------------- sampling
+
+def philox4x32_10(ctr, key):
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(4, np.uint32)
+    lib().so_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def gumbel(seed: int, index: int, vocab: int) -> float:
+    return float(lib().so_gumbel(seed, index, vocab))
+
+
+def unified_sampling(logits, batch, vocab, t_dt=F32, seeds=None, bitmask=None, temperature=None, top_k=None,
+                     top_p=None, min_p=None):
+    """UnifiedSampling (unified_sampling.rs:14-117). logits: storage array
+    [batch, vocab]; returns uint32 token ids (0xFFFFFFFF: none)."""
+    lg = np.ascontiguousarray(logits)
+    sd = None if seeds is None else np.ascontiguousarray(seeds, np.uint64)
+    bm = None if bitmask is None else np.ascontiguousarray(bitmask, np.uint32)
+    out = np.zeros(batch, np.uint32)
+    st = lib().so_unified_sampling(_p(lg), t_dt, _p(out), _p(sd), _p(bm), int(temperature is not None),
+                                   0.0 if temperature is None else temperature, int(top_k is not None),
+                                   0 if top_k is None else top_k, int(top_p is not None),
+                                   0.0 if top_p is None else top_p, int(min_p is not None),
+                                   0.0 if min_p is None else min_p, vocab, batch)
+    if st:
+        raise MemoryError("so_unified_sampling")
+    return out
 
 
 # ----------------------------------------------------------------- GGUF

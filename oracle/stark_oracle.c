@@ -988,3 +988,130 @@ void so_quantize_q4_k(const float* w, size_t rows, size_t cols, uint8_t* out) {
         }
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* UnifiedSampling: src/backends/cpu/kernel/sampling/unified_sampling.rs     */
+/* ------------------------------------------------------------------------ */
+
+/* Philox4x32-10 (Salmon et al., SC'11) as src/encodable_block/sampling/gumbel.rs:1-57 */
+void so_philox4x32_10(const uint32_t ctr_in[4], const uint32_t key_in[2], uint32_t out[4]) {
+    uint32_t c[4] = {ctr_in[0], ctr_in[1], ctr_in[2], ctr_in[3]};
+    uint32_t k[2] = {key_in[0], key_in[1]};
+    for (int round = 0; round < 10; ++round) {
+        if (round) {
+            k[0] += 0x9E3779B9u;
+            k[1] += 0xBB67AE85u;
+        }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c[0], p1 = (uint64_t)0xCD9E8D57u * c[2];
+        const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0, hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+        const uint32_t n0 = hi1 ^ c[1] ^ k[0], n2 = hi0 ^ c[3] ^ k[1];
+        c[0] = n0;
+        c[1] = lo1;
+        c[2] = n2;
+        c[3] = lo0;
+    }
+    memcpy(out, c, sizeof c);
+}
+
+/* gumbel.rs:49-57: uniform in [2^-24, 1 - 2^-24] from the top 24 bits of a word */
+float so_unit_interval(uint32_t word) {
+    uint32_t v = word >> 8;
+    if (v < 1) v = 1;
+    return (float)v * (1.0f / 16777216.0f);
+}
+
+/* gumbel.rs:59-79: -ln(-ln u) of word `word` of Philox(ctr = (offset, 0, 0, 0), key = seed) */
+float so_gumbel(uint64_t seed, uint32_t logit_index, uint32_t vocab) {
+    const uint32_t thread_idx = logit_index % 1024u;
+    const uint32_t thread_offset = ((vocab + 4096u - 1u) / 4096u) * thread_idx;
+    const uint32_t block_idx = logit_index / 1024u;
+    const uint32_t offset = thread_offset + block_idx / 4u, word = block_idx % 4u;
+    const uint32_t ctr[4] = {offset, 0, 0, 0}, key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t out[4];
+    so_philox4x32_10(ctr, key, out);
+    return -logf(-logf(so_unit_interval(out[word])));
+}
+
+typedef struct {
+    float value;
+    uint32_t index;
+} so_scored;
+
+static int so_scored_desc(const void* a, const void* b) {
+    const so_scored* x = (const so_scored*)a;
+    const so_scored* y = (const so_scored*)b;
+    /* b.1.partial_cmp(&a.1).unwrap_or(Equal).then(a.0.cmp(&b.0)) */
+    if (x->value > y->value) return -1;
+    if (x->value < y->value) return 1;
+    return x->index < y->index ? -1 : (x->index > y->index ? 1 : 0);
+}
+
+/* unified_sampling.rs:14-117, one batch row after another. Options are
+ * passed as flags plus values; seeds / bitmask may be NULL when unused. */
+int so_unified_sampling(const void* logits, int dt, uint32_t* output, const uint64_t* seeds, const uint32_t* bitmask,
+                        int has_temperature, float temperature, int has_top_k, uint32_t top_k, int has_top_p,
+                        float top_p, int has_min_p, float min_p, uint32_t vocab, uint32_t batch) {
+    float* l = (float*)malloc(sizeof(float) * vocab);
+    so_scored* sorted = (so_scored*)malloc(sizeof(so_scored) * vocab);
+    if (!l || !sorted) {
+        free(l);
+        free(sorted);
+        return 1;
+    }
+    const uint32_t words = (vocab + 31u) / 32u;
+    for (uint32_t b = 0; b < batch; ++b) {
+        int bad = 0;
+        for (uint32_t i = 0; i < vocab; ++i) {
+            l[i] = read_f32(logits, dt, (size_t)b * vocab + i);
+            if (!isfinite(l[i])) bad = 1;
+        }
+        if (bad) {
+            output[b] = 0xffffffffu;
+            continue;
+        }
+        if (bitmask)
+            for (uint32_t i = 0; i < vocab; ++i)
+                if ((bitmask[(size_t)b * words + i / 32] & (1u << (i % 32))) == 0) l[i] = -INFINITY;
+        if (has_temperature) {
+            const float recip = 1.0f / temperature;
+            int center = 0;
+            for (uint32_t i = 0; i < vocab; ++i)
+                if (isfinite(l[i]) && !isfinite(l[i] * recip)) center = 1;
+            float shift = 0.0f;
+            if (center) {
+                shift = -INFINITY;
+                for (uint32_t i = 0; i < vocab; ++i) shift = fmaxf(shift, l[i]);
+            }
+            for (uint32_t i = 0; i < vocab; ++i) {
+                if (center) l[i] -= shift;
+                l[i] *= recip;
+            }
+        }
+        if (has_top_k || has_top_p || has_min_p) {
+            for (uint32_t i = 0; i < vocab; ++i) sorted[i] = (so_scored){l[i], i};
+            qsort(sorted, vocab, sizeof(so_scored), so_scored_desc);
+            const float mx = sorted[0].value;
+            float norm = 0.0f;
+            for (uint32_t i = 0; i < vocab; ++i) norm += expf(sorted[i].value - mx);
+            for (uint32_t i = 0; i < vocab; ++i) l[i] = -INFINITY;
+            float mass = 0.0f;
+            for (uint32_t r = 0; r < vocab; ++r) {
+                if ((has_top_k && r >= top_k) || (has_top_p && mass >= top_p) ||
+                    (has_min_p && sorted[r].value < mx + logf(min_p)))
+                    break;
+                l[sorted[r].index] = sorted[r].value;
+                mass += expf(sorted[r].value - mx) / norm;
+            }
+        }
+        if (seeds)
+            for (uint32_t i = 0; i < vocab; ++i) l[i] += so_gumbel(seeds[b], i, vocab);
+        /* max_by(partial_cmp.then(b.0.cmp(&a.0))): the largest value, the lowest index among equals */
+        uint32_t best = 0;
+        for (uint32_t i = 1; i < vocab; ++i)
+            if (l[i] > l[best]) best = i;
+        output[b] = isfinite(l[best]) ? best : 0xffffffffu;
+    }
+    free(l);
+    free(sorted);
+    return 0;
+}

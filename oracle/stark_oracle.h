@@ -177,6 +177,15 @@ void so_quantize_affine(const float* w, size_t rows, size_t cols, int bits, size
 void so_quantize_q8_0(const float* w, size_t rows, size_t cols, uint8_t* out);
 void so_quantize_q4_k(const float* w, size_t rows, size_t cols, uint8_t* out);
 
+/* UnifiedSampling (src/backends/cpu/kernel/sampling/unified_sampling.rs) and its noise
+ * (src/encodable_block/sampling/gumbel.rs). */
+void so_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+float so_unit_interval(uint32_t word);
+float so_gumbel(uint64_t seed, uint32_t logit_index, uint32_t vocab);
+int so_unified_sampling(const void* logits, int dt, uint32_t* output, const uint64_t* seeds, const uint32_t* bitmask,
+                        int has_temperature, float temperature, int has_top_k, uint32_t top_k, int has_top_p,
+                        float top_p, int has_min_p, float min_p, uint32_t vocab, uint32_t batch);
+
 #ifdef __cplusplus
 }
 #endif

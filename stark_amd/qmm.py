@@ -139,6 +139,14 @@ class _RefAffineArgs(C.Structure):
                 ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32)]
 
 
+class _SamplingArgs(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("logits", C.c_void_p), ("data_type", C.c_uint32),
+                ("output", C.c_void_p), ("seeds", C.c_void_p), ("bitmask", C.c_void_p),
+                ("has_temperature", C.c_uint32), ("temperature", C.c_float), ("has_top_k", C.c_uint32),
+                ("top_k", C.c_uint32), ("has_top_p", C.c_uint32), ("top_p", C.c_float), ("has_min_p", C.c_uint32),
+                ("min_p", C.c_float), ("vocab_size", C.c_uint32), ("batch_size", C.c_uint32)]
+
+
 class _TransformArgs(C.Structure):
     _fields_ = [("struct_size", C.c_uint32), ("op", C.c_uint32), ("data_type", C.c_uint32), ("in_place", C.c_uint32),
                 ("input", C.c_void_p), ("output", C.c_void_p), ("bias", C.c_void_p), ("bias_data_type", C.c_uint32),
@@ -199,6 +207,7 @@ SIGNATURES = {
                                                   C.c_void_p]),
     "stark_qmm_weight_matrix_free": (None, [C.POINTER(_WeightMatrix)]),
     "stark_qmm_reference_affine_bf16": (C.c_uint32, [C.POINTER(_RefAffineArgs), C.c_void_p]),
+    "stark_qmm_unified_sampling": (C.c_uint32, [C.POINTER(_SamplingArgs), C.c_void_p]),
     "stark_qmm_activation_transform": (C.c_uint32, [C.POINTER(_TransformArgs), C.c_void_p]),
     "stark_qmm_gated_act_mul": (C.c_uint32, [C.POINTER(_GatedArgs), C.c_void_p]),
 }
@@ -455,6 +464,42 @@ class ReferenceAffineBF16Matmul:
         s.m, s.n, s.k = m, n, k
         _check(lib().stark_qmm_reference_affine_bf16(C.byref(s), _stream(stream)), "ReferenceAffineBF16Matmul::encode")
         return out
+
+
+# ---------------------------------------------------------------- sampling
+
+@dataclass
+class SamplingMethod:
+    """SamplingMethod (src/encodable_block/sampling/mod.rs:28-40): greedy when
+    `stochastic` is False (no seeds), else Gumbel sampling with the filters."""
+    stochastic: bool = False
+    temperature: Optional[float] = None
+    top_k: Optional[int] = None
+    top_p: Optional[float] = None
+    min_p: Optional[float] = None
+
+
+def unified_sampling(logits: torch.Tensor, data_type: int, vocab_size: int, batch_size: int,
+                     method: SamplingMethod = SamplingMethod(), seeds: Optional[torch.Tensor] = None,
+                     bitmask: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """UnifiedSampling over stark_qmm_unified_sampling; returns [batch] uint32
+    token ids as an int32 tensor (0xFFFFFFFF reads as -1)."""
+    out = torch.empty(batch_size, dtype=torch.int32, device=logits.device)
+    s = _SamplingArgs()
+    s.struct_size = C.sizeof(_SamplingArgs)
+    s.logits, s.data_type, s.output = _ptr(logits), data_type, _ptr(out)
+    if method.stochastic and seeds is None:
+        raise ValueError("stochastic sampling needs seeds")
+    s.seeds = _ptr(seeds) if method.stochastic else None
+    s.bitmask = _ptr(bitmask)
+    for name in ("temperature", "top_k", "top_p", "min_p"):
+        v = getattr(method, name)
+        if v is not None:
+            setattr(s, "has_" + name, 1)
+            setattr(s, name, v)
+    s.vocab_size, s.batch_size = vocab_size, batch_size
+    _check(lib().stark_qmm_unified_sampling(C.byref(s), _stream(stream)), "Sampling::encode")
+    return out
 
 
 # ---------------------------------------------------------------- activation transforms
