@@ -657,7 +657,8 @@ def decode_measure(args, torch):
     torch.cuda.empty_cache()
     return dict(tokens_per_s=round(tps, 1), ms_per_token=round(ms, 5), timed_tokens=timed_tokens,
                 workload=f"config 4 decode: {gen_tokens} greedy tokens after a {ctx}-token context, 36 layers, "
-                         "vocab 151936 (W8 lm_head), one HIP graph replay per token",
+                         "vocab 151936 (W8 lm_head), one HIP graph replay per token; RMS norms and gated SiLU run as "
+                         "input prologues of the products",
                 hbm_bytes_per_token_algorithmic=per_token, achieved_gbs=round(gbs, 1),
                 frac_of_hbm_peak=round(gbs / PEAK_HBM_GBS, 4))
 

@@ -193,6 +193,35 @@ STARK_QMM_API stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kernel, const 
 STARK_QMM_API stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kernel, const stark_qmm_args* args, uint32_t count,
                                        void* stream);
 
+/* Input prologue of a batched product. No counterpart in the reference: its
+ * decoder runs the RMS norm and the gated activation as kernels of their own
+ * ahead of the products that read them. This entry point is for decode loops
+ * that want those folded into the products' activation staging, saving one
+ * launch and one round trip of the row each:
+ *   STARK_QMM_PROLOGUE_RMS_NORM:  a' = bf16(bf16(a * r) * w[k]),
+ *       r = 1 / sqrt(sum(a^2) / K + eps), w = data (bf16 [K]);
+ *   STARK_QMM_PROLOGUE_SILU_GATE: a' = bf16(up[k] * bf16(a / (1 + exp(-a)))),
+ *       up = data (bf16 [K]) -- GatedActMul's SiLU with no alpha or clips.
+ * The transformed row is bit-identical to the one the separate kernel writes. */
+enum { STARK_QMM_PROLOGUE_NONE = 0, STARK_QMM_PROLOGUE_RMS_NORM = 1, STARK_QMM_PROLOGUE_SILU_GATE = 2 };
+
+typedef struct stark_qmm_prologue {
+    uint32_t struct_size;   /* sizeof(stark_qmm_prologue) */
+    uint32_t kind;          /* STARK_QMM_PROLOGUE_* */
+    const void* data;       /* bf16 [K], 16-byte aligned */
+    float eps;              /* RMS norm only */
+} stark_qmm_prologue;
+
+/* stark_qmm_encode_many with a prologue on the shared input row: every
+ * args[i] is a FullPrecision-A product with the same a (and a_offset) and K,
+ * BF16 input, M = 1, 4-bit codes with group 64, K % 4096 == 0, N >= 32, no
+ * gather, no output RHT, at most 8 entries; anything else returns
+ * STARK_QMM_UNSUPPORTED (so do a kernel in reference-accumulation mode and
+ * STARK_QMM_PROLOGUE_NONE). Outputs must not alias the row or data. */
+STARK_QMM_API stark_qmm_status stark_qmm_encode_many_prologue(stark_qmm_kernel* kernel, const stark_qmm_args* args,
+                                                            uint32_t count, const stark_qmm_prologue* prologue,
+                                                            void* stream);
+
 /* Replaces MatmulKernel::set_reference_accumulation (kernel.rs:34-37): when
  * enabled, every M uses the GEMV/verify kernels (f32 dequant semantics). */
 STARK_QMM_API stark_qmm_status stark_qmm_set_reference_accumulation(stark_qmm_kernel* kernel, uint32_t enabled);

@@ -281,4 +281,37 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
     return STARK_QMM_OK;
 }
 
+
+stark_qmm_status stark_qmm_encode_many_prologue(stark_qmm_kernel* kr, const stark_qmm_args* args, uint32_t count,
+                                                const stark_qmm_prologue* pro, void* stream_ptr) {
+    if (!kr || !pro || (!args && count)) return STARK_QMM_INVALID_ARGUMENT;
+    if (pro->struct_size != sizeof(stark_qmm_prologue)) return STARK_QMM_ABI_MISMATCH;
+    if (pro->kind != STARK_QMM_PROLOGUE_RMS_NORM && pro->kind != STARK_QMM_PROLOGUE_SILU_GATE)
+        return STARK_QMM_UNSUPPORTED;
+    if (!pro->data || ((uintptr_t)pro->data & 15)) return STARK_QMM_INVALID_ARGUMENT;
+    if (kr->reference_accumulation || kr->x_dt != STARK_QMM_BF16 || count > (uint32_t)kMaxBatchOps)
+        return STARK_QMM_UNSUPPORTED;
+    std::vector<AffineOp> ops;
+    for (uint32_t i = 0; i < count; ++i) {
+        const stark_qmm_args* a = &args[i];
+        if (a->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
+        if (a->d_ops.rht_factors || a->a_kind != STARK_QMM_A_FULL_PRECISION || !a->b.codes ||
+            a->b.params.materialize_affine_input_sum || a->gather_indices || a->m != 1 ||
+            a->b.mode != STARK_QMM_MODE_U4 || a->a != args[0].a || a->a_offset != args[0].a_offset ||
+            a->k != args[0].k)
+            return STARK_QMM_UNSUPPORTED;
+        const void* x = a->a ? (const uint8_t*)a->a + a->a_offset * 2 : nullptr;
+        if (!x || !a->d) return STARK_QMM_INVALID_ARGUMENT;
+        AffineOp op;
+        int bits;
+        const stark_qmm_status st =
+            build_affine_op(kr, a->b, a->m, a->n, a->k, x, a->d, a->d_ops, nullptr, &op, &bits);
+        if (st != STARK_QMM_OK) return st;
+        if (a->n == 0) continue;
+        ops.push_back(op);
+    }
+    const StreamPrologue p{pro->kind, pro->data, pro->eps};
+    return launch_stream_prologue(ops.data(), (uint32_t)ops.size(), p, (hipStream_t)stream_ptr);
+}
+
 }  // extern "C"

@@ -207,6 +207,17 @@ struct AffineBatch {
     uint32_t total;     // work tiles over all ops
     uint32_t nib_mask;  // 0x00780078: nibble-pair mask, passed in so it stays in an SGPR
     uint32_t nib_one;   // 0x3F803F80: bf16 1.0 pair, likewise
+    // streaming kernel's input prologue (every op of the launch reads the same row)
+    const void* pro_data;  // RMS-norm weights or the gated product's up values, [K] bf16
+    float pro_eps;
+};
+
+// Input prologue of a streaming launch: the activation row is transformed
+// while it is staged (kind: STARK_QMM_PROLOGUE_*).
+struct StreamPrologue {
+    uint32_t kind;
+    const void* data;
+    float eps;
 };
 
 // Launch helpers implemented in qmv_affine.hip.
@@ -229,6 +240,11 @@ stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed
 // Matrix-core kernel for 4/8-bit products with M <= 16 (qmv_mfma.hip).
 bool mfma_eligible(const AffineOp& op, int bits);
 stark_qmm_status launch_affine_mfma(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream);
+// Streaming kernel with an input prologue: ops that all read one bf16 row
+// (same x and K), each mfma_eligible for 4 bits, m == 1, group 64, K % 4096 == 0,
+// N >= 32; otherwise STARK_QMM_UNSUPPORTED.
+stark_qmm_status launch_stream_prologue(const AffineOp* ops, uint32_t count, const StreamPrologue& pro,
+                                        hipStream_t stream);
 // Full-precision B operand (MatmulB::FullPrecision).
 struct DenseOp {
     const void* w;           // [N, ld] (transpose) or [K, ld]

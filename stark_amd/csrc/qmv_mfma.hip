@@ -345,6 +345,7 @@ struct StreamLds {
     float red[2][4][kTR];           // per-wave row sums, double-buffered by tile parity
     u32x4 zero[4][4];
     uint32_t list[kListLds];        // the workgroup's first kListLds schedule entries
+    float ssq[4];                   // per-wave sums of squares of the row (RMS-norm prologue)
 };
 
 template <int AUX = 0>
@@ -362,9 +363,54 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Input prologues of the streaming kernel, applied to 8 bf16 values of the
+// row (t) with the matching 8 values of the prologue operand (w) as they are
+// staged; both are elementwise and written in the same operations as the
+// decode loop's separate kernels (rms_norm_kernel, silu_mul_kernel), so the
+// staged row is bit-identical to the one those write:
+//  - RMS norm: bf16(bf16(x * inv) * w), inv = 1 / sqrt(sum(x^2) / K + eps);
+//  - SiLU gate: bf16(up * bf16(silu(g))), the activation of GatedActMul's SiLU
+//    (crates/stark-engine/src/backends/cpu/kernel/gated_act_mul/gated_act_mul.rs)
+//    with the hardware exp2 and reciprocal in place of expf and a division:
+//    within one bf16 ulp of it (both round the f32 result to bf16).
+// Two f32 values to a bf16 pair (lo, hi), round to nearest even, in one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    const bf16x2_v v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+__device__ __forceinline__ u32x4 prologue_norm(u32x4 t, u32x4 w, float inv) {
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t n = bf16_pair(lo_f32(t[q]) * inv, hi_f32(t[q]) * inv);
+        o[q] = bf16_pair(lo_f32(n) * lo_f32(w[q]), hi_f32(n) * hi_f32(w[q]));
+    }
+    return o;
+}
+
+// silu(g) = g / (1 + e^-g) with the hardware exp2 and reciprocal
+__device__ __forceinline__ float silu_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
+__device__ __forceinline__ u32x4 prologue_silu(u32x4 g, u32x4 u) {
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t sg = bf16_pair(silu_f32(lo_f32(g[q])), silu_f32(hi_f32(g[q])));
+        o[q] = bf16_pair(lo_f32(u[q]) * lo_f32(sg), hi_f32(u[q]) * hi_f32(sg));
+    }
+    return o;
+}
+
 // BF: bf16 planes (else f16); BIASED: bias plane (else symmetric). Both are
 // compile-time so that the per-unit plane conversion is straight-line code.
-template <bool SIGNED, bool BF, bool BIASED>
+// PRO: input prologue (STARK_QMM_PROLOGUE_*; every op reads the same row).
+template <bool SIGNED, bool BF, bool BIASED, int PRO = STARK_QMM_PROLOGUE_NONE>
 __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void qmv_stream(AffineBatch batch, Schedule sched) {
     (void)batch;
     constexpr uint32_t UB = kUnitK / 2;    // bytes of a row per unit
@@ -393,14 +439,31 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         return min((e & 0xffffffu) * kTR, op.n - kTR);
     };
 
+    // RMS-norm prologue: the row's first 8192 values are loaded before the
+    // first unit's loads (so that waiting for them waits for nothing else) and
+    // summed after those are issued
+    u32x4 q4[4];
+    const AffineOp& o0 = kb_->op[((cu32*)sched.tiles)[lo] >> 24];
+    const __amdgpu_buffer_rsrc_t x0r = rsrc(o0.x, o0.k * 2);
+    if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, (tid + j * kWg) * 16);
+    }
+
     u32x4 ring[8];
     u32x4 xv[2], pls, plb;  // plb reads zero when the op has no bias plane
+    u32x4 pv[2];            // prologue operand at the activations' positions
     // Activations (when need_x) and plane vectors of unit (op, tile at n0, chunk c).
     const auto issue_aux = [&](const AffineOp& op, uint32_t n0, uint32_t c, bool need_x) {
         const __amdgpu_buffer_rsrc_t xr = rsrc(op.x, op.k * 2);
         const uint32_t xo = need_x ? (c * kUnitK + lane * 8) * 2 : OOB;
         xv[0] = buf_load(xr, xo);
         xv[1] = buf_load(xr, xo + 1024);
+        if constexpr (PRO != STARK_QMM_PROLOGUE_NONE) {
+            const __amdgpu_buffer_rsrc_t pr = rsrc(kb_->pro_data, op.k * 2);
+            pv[0] = buf_load(pr, xo);
+            pv[1] = buf_load(pr, xo + 1024);
+        }
         // group-output [G][N4]: lane = (group, quarter of the 32 rows);
         // output-group [N][G]: lane = (row, half of the 16 groups)
         const size_t off = op.os == 1 ? (size_t)(c * 16 + ((lane >> 2) & 15)) * op.gs + n0 + 8 * (lane & 3)
@@ -426,8 +489,34 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
 #pragma unroll
         for (int s = 0; s < 8; ++s) ring[s] = buf_load<kBufNt>(cr, vo, step_soff(*opp, s));
     }
+    if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM) {
+        // sum of squares: thread t takes 8-value vectors t, t + 256, ... in
+        // order, then the wave sums (xor butterfly) and the four waves in
+        // order; loads past the row read zero and add nothing
+        float ss = 0.0f;
+        const uint32_t nv = o0.k / 8;
+        for (uint32_t v0 = 0;;) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float a = __uint_as_float(q4[j][q] << 16), b = __uint_as_float(q4[j][q] & 0xffff0000u);
+                    ss = fmaf(a, a, fmaf(b, b, ss));
+                }
+            v0 += 4 * kWg;
+            if (v0 >= nv) break;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, (v0 + tid + j * kWg) * 16);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) lds.ssq[wave] = ss;
+    }
     lds.list[tid] = list_v;
     lds_barrier();
+    float inv = 0.0f;
+    if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM)
+        inv = 1.0f / sqrtf((lds.ssq[0] + lds.ssq[1] + lds.ssq[2] + lds.ssq[3]) / (float)opp->k + kb_->pro_eps);
     uint32_t tg0 = ~0u, tg1 = ~0u, tg2 = ~0u;  // (op << 16 | chunk) held by each activation region
     const auto tag_of = [&](uint32_t rg) { return rg == 0 ? tg0 : rg == 1 ? tg1 : tg2; };
     f32x4 acc[4] = {};
@@ -445,7 +534,9 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         if (tag_of(rg) != tag) {  // stage this unit's activations (loaded with the unit)
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
-                const u32x4 t = xv[m];
+                u32x4 t = xv[m];
+                if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM) t = prologue_norm(t, pv[m], inv);
+                if constexpr (PRO == STARK_QMM_PROLOGUE_SILU_GATE) t = prologue_silu(t, pv[m]);
                 // the group's exponent: its 8 vectors sit in 8 consecutive lanes
                 const int E = group_shift(group_max<8>(bf16x8_exp_max(t)));
                 const float se = pow2i(E), so = pow2i(E - 4);
@@ -622,7 +713,8 @@ bool stream_eligible(const AffineOp* ops, uint32_t count) {
 }
 
 template <bool SIGNED, bool BF, bool BIASED>
-stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipStream_t stream) {
+stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipStream_t stream,
+                                      const StreamPrologue* pro = nullptr) {
     std::vector<AffineOp> sorted(ops, ops + count);
     std::stable_sort(sorted.begin(), sorted.end(), [](const AffineOp& a, const AffineOp& b) { return a.k > b.k; });
     AffineBatch batch{};
@@ -642,7 +734,14 @@ stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipSt
     batch.count = count;
     batch.total = tiles;
     if (tiles == 0) return STARK_QMM_OK;
-    auto kern = qmv_stream<SIGNED, BF, BIASED>;
+    const uint32_t pk = pro ? pro->kind : (uint32_t)STARK_QMM_PROLOGUE_NONE;
+    if (pro) {
+        batch.pro_data = pro->data;
+        batch.pro_eps = pro->eps;
+    }
+    auto kern = pk == STARK_QMM_PROLOGUE_RMS_NORM    ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_RMS_NORM>
+                : pk == STARK_QMM_PROLOGUE_SILU_GATE ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_SILU_GATE>
+                                                     : qmv_stream<SIGNED, BF, BIASED>;
     int dev = 0, cus = 0;
     QMM_HIP_CHECK(hipGetDevice(&dev));
     QMM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
@@ -660,7 +759,8 @@ stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipSt
 
 // One streaming launch per (plane type, correction) class of the batch.
 template <bool SIGNED>
-stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t stream) {
+stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t stream,
+                               const StreamPrologue* pro = nullptr) {
     std::vector<AffineOp> cls[2][2];
     for (uint32_t i = 0; i < count; ++i)
         cls[ops[i].w_dt == STARK_QMM_BF16][ops[i].corr_kind == STARK_QMM_CORRECTION_BIASES].push_back(ops[i]);
@@ -670,10 +770,10 @@ stark_qmm_status launch_stream(const AffineOp* ops, uint32_t count, hipStream_t 
             if (v.empty()) continue;
             const uint32_t n = (uint32_t)v.size();
             const stark_qmm_status st =
-                bf ? (bi ? launch_stream_planes<SIGNED, true, true>(v.data(), n, stream)
-                         : launch_stream_planes<SIGNED, true, false>(v.data(), n, stream))
-                   : (bi ? launch_stream_planes<SIGNED, false, true>(v.data(), n, stream)
-                         : launch_stream_planes<SIGNED, false, false>(v.data(), n, stream));
+                bf ? (bi ? launch_stream_planes<SIGNED, true, true>(v.data(), n, stream, pro)
+                         : launch_stream_planes<SIGNED, true, false>(v.data(), n, stream, pro))
+                   : (bi ? launch_stream_planes<SIGNED, false, true>(v.data(), n, stream, pro)
+                         : launch_stream_planes<SIGNED, false, false>(v.data(), n, stream, pro));
             if (st != STARK_QMM_OK) return st;
         }
     return STARK_QMM_OK;
@@ -773,6 +873,26 @@ stark_qmm_status launch_affine_mfma(const AffineOp* ops, uint32_t count, int bit
                                                           : launch_class<8>(c, v.data() + s, n, stream);
                     if (st != STARK_QMM_OK) return st;
                 }
+    return STARK_QMM_OK;
+}
+
+stark_qmm_status launch_stream_prologue(const AffineOp* ops, uint32_t count, const StreamPrologue& pro,
+                                        hipStream_t stream) {
+    if (count == 0) return STARK_QMM_OK;
+    if (count > (uint32_t)kMaxBatchOps || !stream_eligible(ops, count)) return STARK_QMM_UNSUPPORTED;
+    std::vector<AffineOp> sg[2];
+    for (uint32_t i = 0; i < count; ++i) {
+        const AffineOp& o = ops[i];
+        if (!mfma_eligible(o, 4) || o.x != ops[0].x || o.k != ops[0].k) return STARK_QMM_UNSUPPORTED;
+        sg[(o.flags & FLAG_SIGNED) != 0].push_back(o);
+    }
+    for (int s = 0; s < 2; ++s) {
+        if (sg[s].empty()) continue;
+        const uint32_t n = (uint32_t)sg[s].size();
+        const stark_qmm_status st = s ? launch_stream<true>(sg[s].data(), n, stream, &pro)
+                                      : launch_stream<false>(sg[s].data(), n, stream, &pro);
+        if (st != STARK_QMM_OK) return st;
+    }
     return STARK_QMM_OK;
 }
 

@@ -22,6 +22,10 @@ constexpr int kMaxChunks = 1024;  // chunks the reduction takes (capacity <= 655
 
 __device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+// f32 -> bf16 round to nearest even on v_cvt_pk_bf16_f32 (the conversion of
+// the products' input prologues)
+__device__ __forceinline__ uint16_t hw_bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
 __device__ __forceinline__ uint16_t to_bf(float f) {
     uint32_t x = __float_as_uint(f);
     if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
@@ -40,7 +44,8 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// out = x * rsqrt(mean(x^2) + eps) * w, one row of n (n % 256 == 0), 256 threads.
+// out = x * rsqrt(mean(x^2) + eps) * w, one row of n (n % 256 == 0), 256 threads;
+// the bf16 roundings on v_cvt_pk_bf16_f32, as the products' RMS-norm prologue.
 // Every load of a thread is a 16-byte vector issued before the first use (the
 // row is read once; rows up to 8192 stay in registers for the second pass).
 __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out,
@@ -76,8 +81,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float a = __uint_as_float(xd[e] << 16), b = __uint_as_float(xd[e] & 0xffff0000u);
-            const uint16_t lo = to_bf(bf(to_bf(a * inv)) * __uint_as_float(wd[e] << 16));
-            const uint16_t hi = to_bf(bf(to_bf(b * inv)) * __uint_as_float(wd[e] & 0xffff0000u));
+            const uint16_t lo = hw_bf(bf(hw_bf(a * inv)) * __uint_as_float(wd[e] << 16));
+            const uint16_t hi = hw_bf(bf(hw_bf(b * inv)) * __uint_as_float(wd[e] & 0xffff0000u));
             od[e] = (uint32_t)lo | ((uint32_t)hi << 16);
         }
         ((uint4*)out)[i] = uint4{od[0], od[1], od[2], od[3]};
@@ -403,13 +408,15 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
     if (lane == 0) *(float2*)&pml[prow * 2] = float2{m, l};
 }
 
-// a = silu(g) * u in bf16 steps (gated_act_mul semantics).
+// a = silu(g) * u in bf16 steps (gated_act_mul semantics), silu(g) = g / (1 +
+// e^-g) with the hardware exp2 and reciprocal, each rounding on
+// v_cvt_pk_bf16_f32: the operations of the products' SiLU-gate prologue.
 __global__ void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* out, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float x = bf(g[i]);
-    const float s = bf(to_bf(x / (1.0f + __expf(-x))));
-    out[i] = to_bf(s * bf(u[i]));
+    const float s = bf(hw_bf(x * __builtin_amdgcn_rcpf(1.0f + __expf(-x))));
+    out[i] = hw_bf(s * bf(u[i]));
 }
 
 // Greedy token: index of the largest logit (lowest index on ties), one

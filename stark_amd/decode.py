@@ -17,6 +17,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 from dataclasses import dataclass
+from typing import Optional
 
 import torch
 
@@ -88,11 +89,21 @@ def quantize_affine_gpu(w: torch.Tensor, bits: int = 4, group: int = 64):
 
 class Qwen3Decoder:
     """Random-init Qwen3-architecture decoder on one GPU (bf16 activations and
-    KV cache; weights quantized W4 g64, lm_head W8 g64; embeddings bf16)."""
+    KV cache; weights quantized W4 g64, lm_head W8 g64; embeddings bf16).
 
-    def __init__(self, cfg: Qwen3Config, capacity: int, seed: int = 0, device: str = "cuda"):
+    fused: the attention/MLP RMS norms and the gated SiLU run as input
+    prologues of the products that read them (stark_qmm_encode_many_prologue;
+    bit-identical rows, three launches fewer per layer). None = whenever the
+    shapes allow it (hidden and intermediate multiples of 4096)."""
+
+    def __init__(self, cfg: Qwen3Config, capacity: int, seed: int = 0, device: str = "cuda",
+                 fused: Optional[bool] = None):
         self.cfg, self.cap = cfg, capacity
         H, I, hd = cfg.hidden, cfg.intermediate, cfg.head_dim
+        eligible = H % 4096 == 0 and I % 4096 == 0
+        if fused and not eligible:
+            raise ValueError("the fused prologues need hidden and intermediate sizes that are multiples of 4096")
+        self.fused = eligible if fused is None else fused
         qd, kd = cfg.q_heads * hd, cfg.kv_heads * hd
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
@@ -153,6 +164,21 @@ class Qwen3Decoder:
     def _prepare(self):
         K4 = self.kern4
         self.batches = []
+        if self.fused:
+            eps = self.cfg.eps
+            for L in self.layers:
+                self.batches.append(dict(
+                    qkv=K4.prepare_many_prologue([self._args(L["q"], self.x, self.q), self._args(L["k"], self.x, self.k),
+                                                  self._args(L["v"], self.x, self.v)],
+                                                 Q.PROLOGUE_RMS_NORM, L["attn_norm"], eps),
+                    o=K4.prepare_many([self._args(L["o"], self.attn, self.x, accumulate=True)]),
+                    gu=K4.prepare_many_prologue([self._args(L["gate"], self.x, self.g),
+                                                 self._args(L["up"], self.x, self.u)],
+                                                Q.PROLOGUE_RMS_NORM, L["mlp_norm"], eps),
+                    down=K4.prepare_many_prologue([self._args(L["down"], self.g, self.x, accumulate=True)],
+                                                  Q.PROLOGUE_SILU_GATE, self.u)))
+            self.lm_batch = self.kern_lm.prepare_many([self._args(self.lm_head, self.h, self.logits)])
+            return
         for L in self.layers:
             self.batches.append(dict(
                 qkv=K4.prepare_many([self._args(L["q"], self.h, self.q), self._args(L["k"], self.h, self.k),
@@ -188,8 +214,9 @@ class Qwen3Decoder:
         _ok(D.stark_decode_embed(p(self.embed), p(self.token), p(self.x), H, cfg.vocab, sp), "embed")
         t(-1, "embed")
         for i, (L, B) in enumerate(zip(self.layers, self.batches)):
-            _ok(D.stark_decode_rms_norm(p(self.x), p(L["attn_norm"]), p(self.h), H, cfg.eps, sp), "attn_norm")
-            t(i, "attn_norm")
+            if not self.fused:  # else the qkv products normalise x as they stage it
+                _ok(D.stark_decode_rms_norm(p(self.x), p(L["attn_norm"]), p(self.h), H, cfg.eps, sp), "attn_norm")
+                t(i, "attn_norm")
             self.kern4.encode_prepared(B["qkv"], s)
             t(i, "qkv")
             # q/k norm + RoPE, KV write and attention partials in one launch, then the chunk reduction
@@ -199,12 +226,14 @@ class Qwen3Decoder:
             t(i, "attention")
             self.kern4.encode_prepared(B["o"], s)
             t(i, "o")
-            _ok(D.stark_decode_rms_norm(p(self.x), p(L["mlp_norm"]), p(self.h), H, cfg.eps, sp), "mlp_norm")
-            t(i, "mlp_norm")
+            if not self.fused:
+                _ok(D.stark_decode_rms_norm(p(self.x), p(L["mlp_norm"]), p(self.h), H, cfg.eps, sp), "mlp_norm")
+                t(i, "mlp_norm")
             self.kern4.encode_prepared(B["gu"], s)
             t(i, "gate_up")
-            _ok(D.stark_decode_silu_mul(p(self.g), p(self.u), p(self.a), I, sp), "silu_mul")
-            t(i, "silu_mul")
+            if not self.fused:  # else the down product stages silu(g) * u
+                _ok(D.stark_decode_silu_mul(p(self.g), p(self.u), p(self.a), I, sp), "silu_mul")
+                t(i, "silu_mul")
             self.kern4.encode_prepared(B["down"], s)
             t(i, "down")
         _ok(D.stark_decode_rms_norm(p(self.x), p(self.final_norm), p(self.h), H, cfg.eps, sp), "final_norm")

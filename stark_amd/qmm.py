@@ -168,6 +168,15 @@ class _GatedArgs(C.Structure):
                 ("sum_group_size", C.c_uint32), ("grouped_by_nibble", C.c_uint32)]
 
 
+class _Prologue(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("kind", C.c_uint32), ("data", C.c_void_p), ("eps", C.c_float)]
+
+
+# Input prologues of stark_qmm_encode_many_prologue (no counterpart in the
+# reference: its decoder launches the RMS norm and the gated SiLU separately).
+PROLOGUE_NONE, PROLOGUE_RMS_NORM, PROLOGUE_SILU_GATE = 0, 1, 2
+
+
 # Every symbol include/stark_qmm.h declares, with its ctypes signature.
 SIGNATURES = {
     "stark_qmm_abi_version": (C.c_uint32, []),
@@ -175,6 +184,8 @@ SIGNATURES = {
     "stark_qmm_create": (C.c_uint32, [C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_void_p)]),
     "stark_qmm_encode": (C.c_uint32, [C.c_void_p, C.POINTER(_Args), C.c_void_p]),
     "stark_qmm_encode_many": (C.c_uint32, [C.c_void_p, C.POINTER(_Args), C.c_uint32, C.c_void_p]),
+    "stark_qmm_encode_many_prologue": (C.c_uint32, [C.c_void_p, C.POINTER(_Args), C.c_uint32, C.POINTER(_Prologue),
+                                                    C.c_void_p]),
     "stark_qmm_set_reference_accumulation": (C.c_uint32, [C.c_void_p, C.c_uint32]),
     "stark_qmm_destroy": (None, [C.c_void_p]),
     "stark_qmm_mapped_many": (C.c_uint32, [C.POINTER(_MappedOp), C.c_uint32, C.POINTER(C.c_void_p), C.c_void_p]),
@@ -387,6 +398,8 @@ def _args(a: MatmulArguments) -> _Args:
 class PreparedBatch:
     array: object  # ctypes array of stark_qmm_args
     keep: list     # the MatmulArguments whose tensors the array points into
+    prologue: object = None  # _Prologue, for batches issued through stark_qmm_encode_many_prologue
+    prologue_data: object = None  # the tensor the prologue reads
 
 
 class MatmulKernel:
@@ -419,7 +432,32 @@ class MatmulKernel:
         return PreparedBatch((_Args * len(arguments))(*[_args(a) for a in arguments]), list(arguments))
 
     def encode_prepared(self, batch: "PreparedBatch", stream=None) -> None:
+        if batch.prologue is not None:
+            _check(lib().stark_qmm_encode_many_prologue(self._h, batch.array, len(batch.keep), C.byref(batch.prologue),
+                                                        _stream(stream)), "encode_many_prologue")
+            return
         _check(lib().stark_qmm_encode_many(self._h, batch.array, len(batch.keep), _stream(stream)), "encode_many")
+
+    @staticmethod
+    def _prologue(kind: int, data, eps: float):
+        if data is None or data.dtype != torch.bfloat16 or not data.is_contiguous():
+            raise ValueError("the prologue operand must be a contiguous bf16 tensor")
+        return _Prologue(C.sizeof(_Prologue), kind, data.data_ptr(), float(eps))
+
+    def encode_many_prologue(self, arguments: Sequence[MatmulArguments], kind: int, data, eps: float = 0.0,
+                             stream=None) -> None:
+        """encode_many with an input prologue on the row every entry reads:
+        PROLOGUE_RMS_NORM (data = norm weights [K], eps) or PROLOGUE_SILU_GATE
+        (the row is the gate, data = up [K])."""
+        arr = (_Args * len(arguments))(*[_args(a) for a in arguments])
+        pro = self._prologue(kind, data, eps)
+        _check(lib().stark_qmm_encode_many_prologue(self._h, arr, len(arguments), C.byref(pro), _stream(stream)),
+               "encode_many_prologue")
+
+    def prepare_many_prologue(self, arguments: Sequence[MatmulArguments], kind: int, data,
+                              eps: float = 0.0) -> "PreparedBatch":
+        return PreparedBatch((_Args * len(arguments))(*[_args(a) for a in arguments]), list(arguments),
+                             self._prologue(kind, data, eps), data)
 
     def close(self) -> None:
         if getattr(self, "_h", None):

@@ -65,9 +65,7 @@ def test_create_validates_dtypes_like_reference():
     assert e.value.status == qmm.UNSUPPORTED_DATA_TYPE
 
 
-def _raw_encode(qmm, **over):
-    """Encode with raw device-free pointers: every case below must be rejected
-    before any HIP call."""
+def _raw_args(qmm, **over):
     s = qmm._Args()
     s.struct_size = C.sizeof(qmm._Args)
     s.a = 0x1000
@@ -91,6 +89,13 @@ def _raw_encode(qmm, **over):
         for p in parts[:-1]:
             obj = getattr(obj, p)
         setattr(obj, parts[-1], v)
+    return s
+
+
+def _raw_encode(qmm, **over):
+    """Encode with raw device-free pointers: every case below must be rejected
+    before any HIP call."""
+    s = _raw_args(qmm, **over)
     h = C.c_void_p()
     assert qmm.lib().stark_qmm_create(qmm.BF16, qmm.BF16, qmm.BF16, C.byref(h)) == 0
     st = qmm.lib().stark_qmm_encode(h, C.byref(s), None)
@@ -113,6 +118,45 @@ def test_encode_rejections_without_device():
     assert _raw_encode(qmm, **{"b.correction": qmm.BIASES, "b.correction_data": None}) == qmm.INVALID_ARGUMENT
     # empty products are a no-op
     assert _raw_encode(qmm, m=0) == qmm.OK
+
+
+def test_encode_many_prologue_rejections_without_device():
+    """stark_qmm_encode_many_prologue takes only batches the streaming kernel
+    runs (one shared bf16 row, M = 1, 4-bit g64, K % 4096 == 0, N >= 32)."""
+    from stark_amd import qmm
+    big = dict(k=4096, n=64, **{"b.codes_size": 64 * 2048, "b.params.row_count": 64, "b.params.group_count": 64})
+
+    def run(entries, kind=qmm.PROLOGUE_RMS_NORM, data=0x7000, size=None, ref_acc=False, x_dt=qmm.BF16):
+        arr = (qmm._Args * len(entries))(*entries)
+        pro = qmm._Prologue(C.sizeof(qmm._Prologue) if size is None else size, kind, data, 1e-6)
+        h = C.c_void_p()
+        assert qmm.lib().stark_qmm_create(qmm.BF16, x_dt, qmm.BF16, C.byref(h)) == 0
+        if ref_acc:
+            qmm.lib().stark_qmm_set_reference_accumulation(h, 1)
+        st = qmm.lib().stark_qmm_encode_many_prologue(h, arr, len(entries), C.byref(pro), None)
+        qmm.lib().stark_qmm_destroy(h)
+        return st
+
+    ok = _raw_args(qmm, **big)
+    assert run([ok], size=8) == qmm.ABI_MISMATCH
+    assert run([_raw_args(qmm, struct_size=8, **big)]) == qmm.ABI_MISMATCH
+    assert run([ok], kind=qmm.PROLOGUE_NONE) == qmm.UNSUPPORTED
+    assert run([ok], kind=9) == qmm.UNSUPPORTED
+    assert run([ok], data=None) == qmm.INVALID_ARGUMENT
+    assert run([ok], data=0x7008) == qmm.INVALID_ARGUMENT  # 16-byte alignment
+    assert run([ok], ref_acc=True) == qmm.UNSUPPORTED
+    assert run([ok], x_dt=qmm.F32) == qmm.UNSUPPORTED
+    assert run([_raw_args(qmm)]) == qmm.UNSUPPORTED  # K = 128
+    assert run([_raw_args(qmm, m=2, **big)]) == qmm.UNSUPPORTED
+    assert run([_raw_args(qmm, **dict(big, n=16))]) == qmm.UNSUPPORTED
+    assert run([ok, _raw_args(qmm, a=0x1100, **big)]) == qmm.UNSUPPORTED  # two different rows
+    assert run([ok, _raw_args(qmm, **dict(big, k=8192, **{"b.codes_size": 64 * 4096}))]) == qmm.UNSUPPORTED
+    assert run([_raw_args(qmm, **{"b.mode": qmm.MODE_U8, **big})]) == qmm.UNSUPPORTED
+    assert run([_raw_args(qmm, **{"d_ops.rht_factors": 0x6000, **big})]) == qmm.UNSUPPORTED
+    assert run([_raw_args(qmm, gather_indices=0x6000, **big)]) == qmm.UNSUPPORTED
+    assert run([ok] * 9) == qmm.UNSUPPORTED
+    assert run([_raw_args(qmm, **dict(big, **{"b.codes_size": 100}))]) == qmm.UNSUPPORTED_LAYOUT
+    assert run([]) == qmm.OK
 
 
 def test_mapped_many_validation_without_device():

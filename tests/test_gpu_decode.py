@@ -309,7 +309,7 @@ def test_decode_step_full_size_layer_by_layer(D):
     element within 2 bf16 ulps of the stage's largest value."""
     cfg = D.Qwen3Config()
     assert (cfg.layers, cfg.hidden, cfg.vocab, cfg.intermediate) == (36, 4096, 151936, 12288)
-    m = D.Qwen3Decoder(cfg, capacity=4096 + 8, seed=11)
+    m = D.Qwen3Decoder(cfg, capacity=4096 + 8, seed=11, fused=False)  # every stage a launch of its own
     m.fill_context(4096, seed=12)
     tok, pos = int(m.token.item()), int(m.pos.item())
     assert pos == 4096
@@ -382,6 +382,41 @@ def test_decode_step_full_size_layer_by_layer(D):
     assert int(m.token.item()) == int(torch.argmax(m.logits).item())
     assert int(m.pos.item()) == pos + 1
     print("worst relative RMS error per stage:", {k: f"{v:.2e}" for k, v in worst.items()})
+
+
+def test_fused_prologues_match_separate_kernels_full_size(D):
+    """The default full-size decoder folds the two RMS norms and the gated
+    SiLU of every layer into the products (input prologues). Staged rows are
+    bit-identical to what the separate kernels write, so two greedy tokens of
+    the fused and the unfused decoder agree bit for bit: logits, tokens, the
+    residual row and the new KV rows of every layer."""
+    cfg = D.Qwen3Config()
+    runs = []
+    for fused in (True, False):
+        m = D.Qwen3Decoder(cfg, capacity=4096 + 8, seed=21, fused=fused)
+        assert m.fused == fused
+        m.fill_context(4096, seed=22)
+        for _ in range(2):
+            m.step()
+        torch.cuda.synchronize()
+        runs.append(dict(logits=m.logits.clone(), x=m.x.clone(), hist=m.history[4096:4098].clone(),
+                         kv=[torch.cat([L["kcache"][:, 4096:4098], L["vcache"][:, 4096:4098]]).clone()
+                             for L in m.layers]))
+        del m
+        torch.cuda.empty_cache()
+    a, b = runs
+    assert torch.equal(a["logits"], b["logits"])
+    assert torch.equal(a["x"], b["x"])
+    assert torch.equal(a["hist"], b["hist"])
+    for i, (ka, kb) in enumerate(zip(a["kv"], b["kv"])):
+        assert torch.equal(ka, kb), f"layer {i} KV rows differ"
+
+
+def test_fused_needs_stream_shapes(D):
+    cfg = D.Qwen3Config(hidden=512, layers=1, q_heads=8, kv_heads=2, head_dim=128, intermediate=1024, vocab=1000)
+    with pytest.raises(ValueError):
+        D.Qwen3Decoder(cfg, capacity=16, fused=True)
+    assert not D.Qwen3Decoder(cfg, capacity=16).fused
 
 
 def test_decode_step_full_size_end_to_end(D):
