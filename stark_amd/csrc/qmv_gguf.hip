@@ -145,12 +145,17 @@ struct GLds {
     };
     float sc[G::TPW][G::GX][kRows];  // per (group, row) scale
     float bi[G::TPW][G::GX][kRows];  // per (group, row) bias term
-    u32x4 xp[G::MR][G::PASS / 8];    // activation rows (hi, lo per real row), 8-bit pair order
+    // activation rows (hi, lo per real row), 8-bit pair order; rows padded by
+    // 64 bytes (16 banks) so that the 16 rows one MFMA A read touches fall on
+    // two bank offsets instead of one
+    u32x4 xp[G::MR][G::PASS / 8 + 4];
     // per-group activation sums and 133 - E (activations staged as x * 2^E):
     // per A row in the slot form; per real row (hi + lo) in the dense form,
-    // whose flush adds the two parts anyway (this keeps two workgroups per CU)
-    float xs[G::DENSE ? G::RR : G::MR][G::GX];
-    alignas(16) int xe[G::DENSE ? G::RR : G::MR][G::GX];
+    // whose flush adds the two parts anyway (this keeps two workgroups per CU),
+    // with rows padded to an odd length there (the dense flush reads rows 2kq
+    // and 2kq + 1 of one group: four banks, not one)
+    float xs[G::DENSE ? G::RR : G::MR][G::GX + (G::DENSE ? 1 : 0)];
+    alignas(16) int xe[G::DENSE ? G::RR : G::MR][G::GX + (G::DENSE ? 1 : 0)];
     u32x4 zero[4];
 };
 
