@@ -97,7 +97,9 @@ struct MfmaLds {
     // wave's groups are read (and discarded), hence the S extra entries
     uint16_t sc[G::GPP + G::S][kRows];        // raw scale plane of the tile [group][row]
     uint16_t bi[G::GPP + G::S][kRows];        // raw bias plane
-    u32x4 xp[G::MR][G::XK / 8];               // activation pairs per 8 values, in MFMA k order
+    // activation pairs per 8 values, in MFMA k order; rows padded by 16 bytes
+    // so that the A rows one MFMA read touches (up to 8) start on distinct banks
+    u32x4 xp[G::MR][G::XK / 8 + 1];
     float xs[G::MR][G::XK / GS + G::S];       // activation sum per group
     alignas(16) int xe[G::MR][G::XK / GS + G::S];  // 133 - E per group (activations staged as x * 2^E)
     float red[4][G::MR][kRows];               // per-wave partial outputs

@@ -39,9 +39,13 @@ struct SmLds {
         float red[kSmTiles][4][16][kRows];               // per-wave partial outputs, after the last pass
     };
     float2 pl[kSmTiles][kSmGroups][kRows];  // (scale, bias term) [tile][group][row]
-    u32x4 xp[16][kSmPass / 8];              // activation rows, MFMA pair order, scaled
-    float xs[16][kSmGroups];                // per-group activation sums
-    int xe[16][kSmGroups];                  // per-group 133 - E (activations staged as x * 2^E)
+    // activation rows, MFMA pair order, scaled; rows padded by 64 bytes so that
+    // the 16 rows of one A read alternate between the two halves of the banks
+    u32x4 xp[16][kSmPass / 8 + 4];
+    // per-group activation sums and 133 - E (activations staged as x * 2^E);
+    // rows of odd length: the flush reads rows 4kq + i of one group
+    float xs[16][kSmGroups + 1];
+    int xe[16][kSmGroups + 1];
 };
 
 template <bool SIGNED>
