@@ -14,11 +14,35 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
+
 namespace {
 
 constexpr int kHd = 128;      // head dim
 constexpr int kChunk = 64;    // attention positions per partial workgroup
 constexpr int kMaxChunks = 1024;  // chunks the reduction takes (capacity <= 65536)
+
+// RoPE frequencies in revolutions per position, theta^(-2i/hd) / (2 pi) for
+// the 64 rotation pairs, computed on the host in double and passed by value:
+// the angle pos * f is then one f32 product (as pos * inv_freq was), reduced
+// exactly to its fraction of a turn, and sine and cosine come from the
+// hardware v_sin_f32 / v_cos_f32 on that fraction.
+struct RopeTable {
+    float f[kHd / 2];
+};
+
+__device__ __forceinline__ void rope_sincos(const RopeTable& t, uint32_t i, int32_t pos, float& sn, float& cs) {
+    const float turn = __builtin_amdgcn_fractf((float)pos * t.f[i]);
+    sn = __builtin_amdgcn_sinf(turn);
+    cs = __builtin_amdgcn_cosf(turn);
+}
+
+RopeTable rope_table(float theta) {
+    RopeTable t;
+    for (int i = 0; i < kHd / 2; ++i)
+        t.f[i] = (float)(std::pow((double)theta, -2.0 * i / kHd) / (2.0 * 3.14159265358979323846));
+    return t;
+}
 
 __device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -99,7 +123,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
 __global__ __launch_bounds__(64) void qk_norm_rope_kernel(uint16_t* q, const uint16_t* k, const uint16_t* v,
                                                           const uint16_t* qw, const uint16_t* kw, uint16_t* kcache,
                                                           uint16_t* vcache, const int32_t* pos_ptr, uint32_t qh,
-                                                          uint32_t kvh, uint32_t cap, float theta, float eps) {
+                                                          uint32_t kvh, uint32_t cap, RopeTable rope, float eps) {
     const uint32_t h = blockIdx.x, i = threadIdx.x;
     const int32_t pos = *pos_ptr;
     const bool is_q = h < qh;
@@ -109,10 +133,8 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(uint16_t* q, const uin
     const float inv = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)kHd + eps);
     const float na = bf(to_bf(bf(to_bf(a * inv)) * bf(w[i])));
     const float nb = bf(to_bf(bf(to_bf(b * inv)) * bf(w[i + 64])));
-    // inv_freq_i = theta^(-2i/hd), angle = pos * inv_freq_i
-    const float freq = powf(theta, -2.0f * (float)i / (float)kHd);
     float sn, cs;
-    sincosf((float)pos * freq, &sn, &cs);
+    rope_sincos(rope, i, pos, sn, cs);
     const uint16_t ra = to_bf(na * cs - nb * sn), rb = to_bf(nb * cs + na * sn);
     if (is_q) {
         q[(size_t)h * kHd + i] = ra;
@@ -273,13 +295,12 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 __device__ __forceinline__ void norm_rope_pair(float a, float b, const uint16_t* w, uint32_t i, int32_t pos,
-                                               float theta, float eps, uint16_t& ra, uint16_t& rb) {
+                                               const RopeTable& rope, float eps, uint16_t& ra, uint16_t& rb) {
     const float inv = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)kHd + eps);
     const float na = bf(to_bf(bf(to_bf(a * inv)) * bf(w[i])));
     const float nb = bf(to_bf(bf(to_bf(b * inv)) * bf(w[i + 64])));
-    const float freq = powf(theta, -2.0f * (float)i / (float)kHd);
     float sn, cs;
-    sincosf((float)pos * freq, &sn, &cs);
+    rope_sincos(rope, i, pos, sn, cs);
     ra = to_bf(na * cs - nb * sn);
     rb = to_bf(nb * cs + na * sn);
 }
@@ -300,7 +321,7 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
                                                             const uint16_t* vnew, const uint16_t* qw,
                                                             const uint16_t* kw, uint16_t* kcache, uint16_t* vcache,
                                                             float* po, float* pml, const int32_t* pos_ptr, uint32_t kvh, uint32_t cap,
-                                                            uint32_t nchunks, float scale, float theta, float eps) {
+                                                            uint32_t nchunks, float scale, RopeTable rope, float eps) {
     constexpr int kRowK = kHd / 2 + 4;
     constexpr int kVec = kChunk * kHd / 8;
     __shared__ __attribute__((aligned(16))) uint32_t ks[kChunk * kRowK];
@@ -330,7 +351,7 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
         {
             const uint16_t* src = q + (size_t)(g * G + h) * kHd;
             uint16_t ra, rb;
-            norm_rope_pair(bf(src[lane]), bf(src[lane + 64]), qw, lane, pos, theta, eps, ra, rb);
+            norm_rope_pair(bf(src[lane]), bf(src[lane + 64]), qw, lane, pos, rope, eps, ra, rb);
             qs[h][lane] = ra;
             qs[h][lane + 64] = rb;
         }
@@ -347,7 +368,7 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
             const uint32_t r = (uint32_t)pos - p0;
             uint16_t ra, rb;
             const uint16_t* ksrc = knew + (size_t)g * kHd;
-            norm_rope_pair(bf(ksrc[lane]), bf(ksrc[lane + 64]), kw, lane, pos, theta, eps, ra, rb);
+            norm_rope_pair(bf(ksrc[lane]), bf(ksrc[lane + 64]), kw, lane, pos, rope, eps, ra, rb);
             const uint16_t va = vnew[(size_t)g * kHd + lane], vb = vnew[(size_t)g * kHd + lane + 64];
             uint16_t* ks16 = (uint16_t*)&ks[r * kRowK];
             uint16_t* vs16 = (uint16_t*)&vs[r * (kHd / 2)];
@@ -505,7 +526,7 @@ int stark_decode_qk_norm_rope(void* q, const void* k, const void* v, const void*
                               float eps, void* stream) {
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(qh + kvh), dim3(64), 0, (hipStream_t)stream, (uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)qw, (const uint16_t*)kw,
-                       (uint16_t*)kcache, (uint16_t*)vcache, pos, qh, kvh, cap, theta, eps);
+                       (uint16_t*)kcache, (uint16_t*)vcache, pos, qh, kvh, cap, rope_table(theta), eps);
     return hipGetLastError() == hipSuccess ? 0 : 10;
 }
 
@@ -541,12 +562,13 @@ int stark_decode_attention_fused(const void* q, const void* k, const void* v, co
     if ((cap + kChunk - 1) / kChunk > (uint32_t)kMaxChunks) return 1;
     const uint32_t nchunks = (cap + kChunk - 1) / kChunk, G = qh / kvh;
     const float scale = 1.0f / sqrtf((float)kHd);
+    const RopeTable rope = rope_table(theta);
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(kvh, nchunks);
 #define QMM_ATTN_F(GG)                                                                                          \
     hipLaunchKernelGGL(attn_fused_kernel<GG>, grid, dim3(64 * GG), 0, s, (const uint16_t*)q, (const uint16_t*)k, \
                        (const uint16_t*)v, (const uint16_t*)qw, (const uint16_t*)kw, (uint16_t*)kcache,          \
-                       (uint16_t*)vcache, po, pml, pos, kvh, cap, nchunks, scale, theta, eps)
+                       (uint16_t*)vcache, po, pml, pos, kvh, cap, nchunks, scale, rope, eps)
     switch (G) {
     case 1: QMM_ATTN_F(1); break;
     case 2: QMM_ATTN_F(2); break;
