@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(kWavesPerEu
 // Workgroups of `kern` that fit the device at once (a multiple of 8), cached
 // per (kernel, device).
 template <class Kern>
-uint32_t persistent_grid(Kern kern) {
+uint32_t persistent_grid(Kern kern, int block = kWg) {
     static std::mutex mu;
     static std::map<std::pair<const void*, int>, uint32_t> cache;
     int dev = 0, cus = 0, per_cu = 0;
@@ -113,7 +113,7 @@ uint32_t persistent_grid(Kern kern) {
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kWg, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, block, 0) != hipSuccess)
         return 0;
     const uint32_t grid = (uint32_t)std::max(8, cus * std::max(per_cu, 1) / 8 * 8);
     cache.emplace(key, grid);
@@ -337,15 +337,16 @@ constexpr int kTR = 32;        // tile rows
 constexpr int kUnitK = 1024;   // k values per unit (16 groups of 64)
 constexpr int kListLds = kWg;  // schedule entries staged in LDS at kernel start (one per thread)
 
+template <int WV>  // waves per workgroup
 struct StreamLds {
-    u32x4 xp[4][kXR][kUnitK / 8];  // activation pairs (x0,x4)(x1,x5).. per 8 values; x*2^E, odd values x*2^(E-4)
-    float xs[4][kXR][kUnitK / 64];  // activation sum per group
-    int xe[4][kXR][kUnitK / 64];    // 133 - E per group: the flush's ldexp (activations staged as x * 2^E)
-    f32x4 pl[4][kTR * 8];          // (scale, bias term) of [row][group] of the wave's unit
-    float red[2][4][kTR];           // per-wave row sums, double-buffered by tile parity
-    u32x4 zero[4][4];
-    uint32_t list[kListLds];        // the workgroup's first kListLds schedule entries
-    float ssq[4];                   // per-wave sums of squares of the row (RMS-norm prologue)
+    u32x4 xp[WV][kXR][kUnitK / 8];  // activation pairs (x0,x4)(x1,x5).. per 8 values; x*2^E, odd values x*2^(E-4)
+    float xs[WV][kXR][kUnitK / 64];  // activation sum per group
+    int xe[WV][kXR][kUnitK / 64];    // 133 - E per group: the flush's ldexp (activations staged as x * 2^E)
+    f32x4 pl[WV][kTR * 8];          // (scale, bias term) of [row][group] of the wave's unit
+    float red[2][WV][kTR];           // per-wave row sums, double-buffered by tile parity
+    u32x4 zero[WV][4];
+    uint32_t list[kListLds];         // the workgroup's first kListLds schedule entries
+    float ssq[4];                    // sums of squares of the row by the first four waves (RMS-norm prologue)
 };
 
 template <int AUX = 0>
@@ -410,13 +411,18 @@ __device__ __forceinline__ u32x4 prologue_silu(u32x4 g, u32x4 u) {
 // BF: bf16 planes (else f16); BIASED: bias plane (else symmetric). Both are
 // compile-time so that the per-unit plane conversion is straight-line code.
 // PRO: input prologue (STARK_QMM_PROLOGUE_*; every op reads the same row).
-template <bool SIGNED, bool BF, bool BIASED, int PRO = STARK_QMM_PROLOGUE_NONE>
-__global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void qmv_stream(AffineBatch batch, Schedule sched) {
+// WV: waves per workgroup, each taking every WV-th unit of a tile (4: two
+// workgroups per CU; 12: one workgroup of three waves per SIMD, for launches
+// of 12288-deep products with fewer tiles than CUs, whose tiles then keep
+// three times the loads in flight).
+template <bool SIGNED, bool BF, bool BIASED, int PRO = STARK_QMM_PROLOGUE_NONE, int WV = 4>
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4 ? 2 : WV / 4))) void qmv_stream(
+    AffineBatch batch, Schedule sched) {
     (void)batch;
     constexpr uint32_t UB = kUnitK / 2;    // bytes of a row per unit
     constexpr uint32_t OOB = 0x80000000u;  // buffer offset past every resource: reads zero, no traffic
     constexpr uint32_t PLANE = 0x7fffffffu;  // plane resources: addressed by the op's strides
-    __shared__ StreamLds lds;
+    __shared__ StreamLds<WV> lds;
     const AffineBatch* kb_ = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
     typedef const __attribute__((address_space(4))) uint32_t cu32;
     const uint32_t lo = ((cu32*)sched.begin)[blockIdx.x], hi = ((cu32*)sched.begin)[blockIdx.x + 1];
@@ -429,7 +435,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     if (lane < 4) lds.zero[wave][lane] = u32x4{0, 0, 0, 0};
     // The workgroup's schedule entries go to LDS once, so that no unit waits on
     // a scalar miss for its successor. Their load is issued first and written
-    // to LDS after the first unit's loads are on their way (kListLds == kWg).
+    // to LDS after the first unit's loads are on their way (by the first kListLds threads).
     const uint32_t list_v = tid < min(hi - lo, (uint32_t)kListLds) ? sched.tiles[lo + tid] : 0u;
     const auto entry = [&](uint32_t t) {
         return t - lo < (uint32_t)kListLds ? __builtin_amdgcn_readfirstlane(lds.list[t - lo])
@@ -447,7 +453,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const __amdgpu_buffer_rsrc_t x0r = rsrc(o0.x, o0.k * 2);
     if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, (tid + j * kWg) * 16);
+        for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, tid < (uint32_t)kWg ? (tid + j * kWg) * 16 : OOB);
     }
 
     u32x4 ring[8];
@@ -489,10 +495,11 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
 #pragma unroll
         for (int s = 0; s < 8; ++s) ring[s] = buf_load<kBufNt>(cr, vo, step_soff(*opp, s));
     }
-    if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM) {
-        // sum of squares: thread t takes 8-value vectors t, t + 256, ... in
-        // order, then the wave sums (xor butterfly) and the four waves in
-        // order; loads past the row read zero and add nothing
+    if (PRO == STARK_QMM_PROLOGUE_RMS_NORM && wave < 4) {
+        // sum of squares by the first 256 threads: thread t takes 8-value
+        // vectors t, t + 256, ... in order, then the wave sums (xor butterfly)
+        // and the four waves in order; loads past the row read zero and add
+        // nothing
         float ss = 0.0f;
         const uint32_t nv = o0.k / 8;
         for (uint32_t v0 = 0;;) {
@@ -512,7 +519,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
         if (lane == 0) lds.ssq[wave] = ss;
     }
-    lds.list[tid] = list_v;
+    if (tid < (uint32_t)kListLds) lds.list[tid] = list_v;
     lds_barrier();
     float inv = 0.0f;
     if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM)
@@ -523,9 +530,9 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     uint32_t par = 0;
     for (;;) {
         const AffineOp& op = *opp;
-        const uint32_t R = op.k / (4 * kUnitK);
+        const uint32_t R = op.k / (WV * kUnitK);
         const uint32_t t0 = (e & 0xffffffu) * kTR, n0 = min(t0, op.n - kTR);
-        const uint32_t c = wave + 4 * ri;
+        const uint32_t c = wave + WV * ri;
         const uint32_t rg = ri % kXR;
         const uint32_t tag = (op.xid << 16) | c;
         u32x4* xpw = lds.xp[wave][rg];
@@ -598,7 +605,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         }
         const bool more = ni < hi;
         const uint32_t ne = more ? entry(ni) : e;
-        const uint32_t nc = more ? wave + 4 * nr : c;
+        const uint32_t nc = more ? wave + WV * nr : c;
         const AffineOp& nop = kb_->op[ne >> 24];
         const uint32_t nn0 = tile_row(nop, ne);
         issue_aux(nop, nn0, nc, more && tag_of(nr % kXR) != ((nop.xid << 16) | nc));
@@ -685,8 +692,13 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             if (tid < (uint32_t)kTR) {
                 const uint32_t n = n0 + tid;
                 if (n >= t0) {  // rows of the previous tile (shifted last tile) are not written again
-                    float o = op.ab_scale * ((lds.red[par][0][tid] + lds.red[par][1][tid]) +
-                                             (lds.red[par][2][tid] + lds.red[par][3][tid]));
+                    // the waves' sums in fixed order: fours added pairwise, then the fours in turn
+                    float o = (lds.red[par][0][tid] + lds.red[par][1][tid]) + (lds.red[par][2][tid] + lds.red[par][3][tid]);
+#pragma unroll
+                    for (int w = 4; w < WV; w += 4)
+                        o += (lds.red[par][w][tid] + lds.red[par][w + 1][tid]) +
+                             (lds.red[par][w + 2][tid] + lds.red[par][w + 3][tid]);
+                    o *= op.ab_scale;
                     if (op.flags & FLAG_ACCUMULATE) o += load_as_f32(op.d, op.d_dt, n);
                     if (op.bias) o += load_as_f32(op.bias, op.w_dt, n);
                     if (op.flags & FLAG_SOFT_CAP) o = op.soft_cap * tanhf(o / op.soft_cap);
@@ -739,20 +751,30 @@ stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipSt
         batch.pro_data = pro->data;
         batch.pro_eps = pro->eps;
     }
-    auto kern = pk == STARK_QMM_PROLOGUE_RMS_NORM    ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_RMS_NORM>
-                : pk == STARK_QMM_PROLOGUE_SILU_GATE ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_SILU_GATE>
-                                                     : qmv_stream<SIGNED, BF, BIASED>;
     int dev = 0, cus = 0;
     QMM_HIP_CHECK(hipGetDevice(&dev));
     QMM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    // two workgroups (eight waves) per CU, a multiple of the 8 XCDs
-    const uint32_t grid = std::min(std::min(persistent_grid(kern), (uint32_t)std::max(8, cus * 2 / 8 * 8)),
-                                   (tiles + 7) / 8 * 8);
+    // Twelve waves per workgroup (one unit of a 12288-deep tile each) when the
+    // launch has fewer tiles than CUs: its workgroups cannot fill the chip, so
+    // each keeps three times the loads in flight instead.
+    bool deep = tiles < (uint32_t)cus;
+    for (uint32_t i = 0; i < count; ++i) deep = deep && sorted[i].k % (12 * kUnitK) == 0;
+    const auto pick = [&](auto wv) {
+        constexpr int W = decltype(wv)::value;
+        return pk == STARK_QMM_PROLOGUE_RMS_NORM    ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_RMS_NORM, W>
+               : pk == STARK_QMM_PROLOGUE_SILU_GATE ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_SILU_GATE, W>
+                                                    : qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_NONE, W>;
+    };
+    auto kern = deep ? pick(std::integral_constant<int, 12>{}) : pick(std::integral_constant<int, 4>{});
+    const int block = deep ? 12 * 64 : kWg;
+    // two workgroups (eight waves) per CU, or one of twelve waves; a multiple of the 8 XCDs
+    const uint32_t per_launch = (uint32_t)std::max(8, cus * (deep ? 1 : 2) / 8 * 8);
+    const uint32_t grid = std::min(std::min(persistent_grid(kern, block), per_launch), (tiles + 7) / 8 * 8);
     if (grid == 0) return STARK_QMM_DEVICE_FAILURE;
     Schedule sched;
     const stark_qmm_status st = schedule_for(sorted.data(), count, grid, &sched, stream, kTR);
     if (st != STARK_QMM_OK) return st;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(kWg), 0, stream, batch, sched);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(block), 0, stream, batch, sched);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
 }
