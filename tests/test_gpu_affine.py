@@ -322,6 +322,9 @@ def test_decode_stream_kernel_d_ops_on_shifted_tile(qmm, oracle):
     """N=40: the last 16-row tile overlaps the previous one; accumulate must add once."""
     run_case(qmm, oracle, m=1, n=40, k=4096, ab_scale=0.5, accumulate=True, with_bias=True, d_dt=H.F32, seed=18)
     run_case(qmm, oracle, m=1, n=40, k=8192, bits=8, accumulate=True, soft_cap=2.0, d_dt=H.BF16, seed=19)
+    # 12288-deep launch with fewer tiles than CUs: the twelve-wave workgroups
+    run_case(qmm, oracle, m=1, n=40, k=12288, ab_scale=0.5, accumulate=True, with_bias=True, d_dt=H.F32, seed=20)
+    run_case(qmm, oracle, m=1, n=4096, k=12288, correction=0, signed=True, quantizer=False, seed=21)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
