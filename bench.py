@@ -1,6 +1,6 @@
 """Benchmark of the quantized matvec hot path on one MI355X.
 
-Workload: the Qwen3-8B per-layer 4-bit decode matvec set
+Workload (config 1, the headline): the Qwen3-8B per-layer 4-bit decode matvec set
     q 4096->4096, k/v 4096->1024, o 4096->4096, gate/up 4096->12288, down 12288->4096
 MLX-affine W4, group 64, bf16 scale/bias planes in the converter's group-output
 layout, bf16 activations N(0,1), M=1. One step = one pass over the set, issued
@@ -38,7 +38,7 @@ SEED = 20261201
 
 
 def quantize_gpu(w, group=GROUP):
-    """BASELINE rule on the GPU (data generation only): per group
+    """MLX affine quantization on the GPU (data generation only): per group
     scale=(max-min)/15, bias=min as bf16; q=clamp(round((w-bias)/scale)).
     Returns (codes u8 [N, K/2], scales/biases int16 bits [G, N] group-output)."""
     import torch
@@ -56,7 +56,7 @@ def quantize_gpu(w, group=GROUP):
 
 
 def quantize_gpu_bits(torch, w, bits, group=GROUP):
-    """MLX affine at `bits` (4 or 8) by the BASELINE rule: scale=(max-min)/(2^bits-1),
+    """MLX affine at `bits` (4 or 8): scale=(max-min)/(2^bits-1),
     bias=min as bf16; codes little-endian (low nibble first for 4-bit)."""
     if bits == 4:
         return quantize_gpu(w, group)
@@ -318,7 +318,7 @@ def config1(args, torch, Q):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: random-init N(0,0.02) weights quantized W4 g64 (BASELINE rule), bf16 N(0,1) activations",
+        "data": "synthetic: random-init N(0,0.02) weights quantized W4 g64 (MLX affine rule), bf16 N(0,1) activations",
         "config": {
             "workload": "Qwen3-8B layer matvec set q,k,v,o,gate,up,down; MLX-affine W4 g64 bf16 planes; M=1; "
                         f"{args.copies} rotating layer copies; one stark_qmm_encode_many launch per step",
@@ -526,7 +526,7 @@ def config3(args, torch, Q):
         print(json.dumps({"metric": "Qwen3-30B-A3B MoE layer decode HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
                           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-                          "data": "synthetic: N(0,0.02) weights W4 g64 (BASELINE rule), N(0,1) hidden states",
+                          "data": "synthetic: N(0,0.02) weights W4 g64 (MLX affine rule), N(0,1) hidden states",
                           "config": {"workload": f"config 3: router + routed experts, tokens={T}, E={E}, top-{A}, "
                                                  f"H={Hm}, I={I}, {copies} rotating layer copies",
                                      "unique_experts": u, "bytes_per_step": int(nbytes),
@@ -564,7 +564,7 @@ def config4(args, torch, Q):
     print(json.dumps({"metric": "Qwen3-8B W4 prefill dequant-GEMM TFLOP/s", "value": round(tf, 1), "unit": "TFLOP/s",
                       "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
                       "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-                      "data": "synthetic: N(0,0.02) weights W4 g64 (BASELINE rule), N(0,1) bf16 activations",
+                      "data": "synthetic: N(0,0.02) weights W4 g64 (MLX affine rule), N(0,1) bf16 activations",
                       "config": {"workload": f"config 4 prefill: M={Mtok} through q,k,v,o,gate,up,down (one layer)",
                                  "flops_per_step": flops, "prefill_tokens_per_s_36_layers":
                                      round(Mtok * 1000.0 / (ms * LAYERS), 1)},

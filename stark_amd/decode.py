@@ -1,4 +1,4 @@
-"""End-to-end decode stand-in for BASELINE config 4: a random-init
+"""End-to-end decode stand-in for the benchmark's config 4 (Qwen3-8B greedy decode): a random-init
 Qwen3-architecture decoder whose every weight product runs through the
 quantized matrix-product library (libstark_qmm: 4-bit MLX-affine layer
 projections, an 8-bit lm_head), with the decode-step kernels of
@@ -69,7 +69,7 @@ class Qwen3Config:
 
 
 def quantize_affine_gpu(w: torch.Tensor, bits: int = 4, group: int = 64):
-    """MLX affine by BASELINE's rule: per group scale = (max - min)/(2^bits - 1)
+    """MLX affine quantization: per group scale = (max - min)/(2^bits - 1)
     and bias = min as bf16, q = clamp(round((w - bias)/scale)); codes
     little-endian (low nibble first for 4-bit); planes in the converter's
     group-output layout [G][N] (N % 4 == 0). Returns (codes u8, scales, biases)

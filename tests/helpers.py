@@ -32,7 +32,7 @@ def load(O, x, dt):
 
 def affine_weights(O, rng, n, k, bits=4, gs=64, layout=0, correction=1, w_dt=BF16, quantizer=True):
     """Returns dict(codes, scales, corr, zos/zgs...) as storage arrays. With
-    quantizer=True weights are N(0, 0.02) quantized per BASELINE's rule;
+    quantizer=True weights are N(0, 0.02) quantized MLX-affine (scale = (max-min)/(2^bits-1), bias = min);
     otherwise codes/scales/biases are drawn like the reference's QuantInput
     (unit/common/matmul/quant.rs:132-186)."""
     G = k // gs

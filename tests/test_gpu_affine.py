@@ -69,7 +69,7 @@ def run_case(Q, O, *, m, n, k, bits=4, gs=64, layout=0, correction=1, w_dt=H.BF1
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("d_dt", [H.BF16, H.F32])
 def test_config0_w4_matvec(qmm, oracle, layout, d_dt):
-    """N=3072, K=1024, W4 g64, M=1."""
+    """Benchmark config 0 (the reference's CPU-runnable case): N=3072, K=1024, W4 g64, M=1."""
     run_case(qmm, oracle, m=1, n=3072, k=1024, layout=layout, d_dt=d_dt, seed=1)
 
 
