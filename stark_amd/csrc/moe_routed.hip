@@ -22,6 +22,7 @@
 // a route; each output value of the matrix-core tile depends on its own
 // activation row alone.
 #include <cmath>
+#include <cstdlib>
 #include <mutex>
 
 #include "mfma_tile.h"
@@ -338,6 +339,124 @@ __global__ __launch_bounds__(kWg) void moe_down_mfma(GroupedLaunch launch) {
     }
 }
 
+// ---- 1+2+3 fused for one token (rows == 1, up to kOneTokenExperts experts):
+// every workgroup routes the token itself -- phases a-d of moe_route_compact
+// restricted to one row, in the same operations, so the ids and weights are
+// the same bits -- files route r as its own one-route slot r (one token gives
+// an expert at most one route, and each route's product depends on its own
+// activation row alone, so a slot per route computes what the counting sort's
+// slots compute), and then computes its (slot, tile) item of the up product.
+// Workgroup 0 also writes the ids, the weights and the class-0 slot table that
+// the down product and the rank accumulation read. This takes the separate
+// route launch off the one-token chain.
+constexpr uint32_t kOneTokenExperts = 256;
+
+struct RouteOneArgs {
+    const float* logits;
+    const float* gains;
+    uint32_t experts, active, round_weights, round_logits, adjust, sort_ids;
+    uint32_t* ids;
+    float* weights;
+    uint32_t* table;
+    uint32_t* header;
+};
+
+template <int GS, bool SIGNED, int P1>
+__global__ __launch_bounds__(kWg) void moe_route_up_one(GroupedLaunch launch, RouteOneArgs ra) {
+    (void)launch;
+    __shared__ MfmaLds<1, 1, GS, 4, P1> lds;
+    __shared__ uint64_t keys[kOneTokenExperts];
+    __shared__ uint32_t rid[32], sid[32];
+    __shared__ float rmax, rden;
+    __shared__ uint32_t rbad;
+    const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t E = ra.experts, A = ra.active;
+    // a. keys (bf16-rounded logits if asked) and the finite flag
+    if (tid == 0) rbad = 0;
+    if (tid < 32) rid[tid] = 0;
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += kWg) {
+        float x = ra.logits[e];
+        if (ra.round_logits) x = route_round_bf16(x);
+        keys[e] = route_key(x, e);
+        if (!__builtin_isfinite(x)) rbad = 1;
+    }
+    __syncthreads();
+    // b. max and den (wave 0, as one row of moe_route_compact)
+    if (wave == 0) {
+        float mx = -INFINITY;
+        for (uint32_t e = lane; e < E; e += 64) mx = fmaxf(mx, route_key_value(keys[e]));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float den = 0.0f;
+        for (uint32_t e = lane; e < E; e += 64) den += expf(route_key_value(keys[e]) - mx);
+        den = wave_sum(den);
+        if (lane == 0) {
+            rmax = mx;
+            rden = den;
+        }
+    }
+    // c. ranks: #{e' : key(e') > key(e)}
+    for (uint32_t e = tid; e < E; e += kWg) {
+        const uint64_t k = keys[e];
+        uint32_t rank = 0;
+        for (uint32_t f = 0; f < E; ++f) rank += keys[f] > k ? 1u : 0u;
+        if (rank < A) rid[rank] = e;
+    }
+    __syncthreads();
+    // d. weights in rank order, renormalised; gains and the stable id sort
+    if (wave == 0) {
+        const bool valid = rbad == 0;
+        const uint32_t my_id = lane < A ? rid[lane] : 0u;
+        const float my_v = lane < A && my_id < E ? route_key_value(keys[my_id]) : 0.0f;
+        const float score = lane < A ? expf(my_v - rmax) / rden : 0.0f;
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < A; ++r) sum += __shfl(score, r, 64);
+        float w = score / sum;
+        if (ra.round_weights) w = route_round_bf16(w);
+        const uint32_t id = valid ? my_id : 0u;
+        w = valid ? w : __builtin_nanf("");
+        uint32_t pos = lane;
+        if (ra.adjust) {
+            w = id < E ? w * (ra.gains ? ra.gains[id] : 1.0f) : __builtin_nanf("");
+            if (ra.sort_ids) {
+                pos = 0;
+                for (uint32_t r = 0; r < A; ++r) {
+                    const uint32_t o = __shfl(id, r, 64);
+                    pos += (o < id || (o == id && r < lane)) ? 1u : 0u;
+                }
+            }
+        }
+        if (lane < A) {
+            sid[pos] = id;
+            if (blockIdx.x == 0) {
+                ra.ids[pos] = id;
+                ra.weights[pos] = w;
+                uint32_t* rec = ra.table + (size_t)pos * kRecWords;
+                rec[0] = id < E ? id : 0u;  // out-of-range ids read expert 0's rows (moe.rs:87-107)
+                rec[1] = 1;
+                rec[2] = pos;
+            }
+        }
+        if (blockIdx.x == 0 && lane < kClasses) ra.header[lane] = lane == 0 ? A : 0u;
+    }
+    __syncthreads();
+    // the item: route (slot) and tile of 8 value rows
+    const uint32_t H = L->hidden, model = L->model;
+    const uint32_t slot = blockIdx.x / L->tiles, t = blockIdx.x % L->tiles;
+    const uint32_t e = sid[slot] < E ? sid[slot] : 0u;
+    const uint32_t nA = e * 2 * H + 8 * t, nB = nA + H;
+    mfma_tile<1, 1, GS, 4, SIGNED, P1>(L->op, plane_flags(L->op), nA, nB, 1, [&](uint32_t) { return (size_t)0; }, lds);
+    (void)model;
+    if (threadIdx.x < 8) {
+        const uint32_t i = threadIdx.x;
+        const float v = (lds.red[0][0][i] + lds.red[1][0][i]) + (lds.red[2][0][i] + lds.red[3][0][i]);
+        const float g = (lds.red[0][0][8 + i] + lds.red[1][0][8 + i]) + (lds.red[2][0][8 + i] + lds.red[3][0][8 + i]);
+        L->out[(size_t)slot * H + 8 * t + i] = gated_silu(v, g);
+    }
+}
+
 // ---- 5. accumulation over ranks in order (moe.rs:109-145 applied rank 0..k-1).
 __global__ void moe_accumulate_ranks(const uint16_t* proj, const float* weights, uint16_t* output, uint32_t model,
                                      uint32_t active, uint32_t round_product, uint32_t round_accumulator) {
@@ -389,6 +508,20 @@ void* pick_class(int cls, uint32_t max_count, uint32_t gs, bool sg, uint32_t k) 
     if (max_count <= 4) return pick<K, 4, 1, 2048>(gs, sg);
     if (max_count <= 8) return pick<K, 8, 1, 2048>(gs, sg);
     return pick<K, 8, 2, 2048>(gs, sg);
+}
+
+// The one-token fused kernel of a group size and signedness (the one-route
+// tile shape, pass length as pick_class takes for class 0).
+void* pick_route_up_one(uint32_t gs, bool sg, uint32_t k) {
+#define QMM_RU(G, S, P) (void*)&moe_route_up_one<G, S, P>
+    const bool short_k = k <= 1024;
+    if (gs == 32) return short_k ? (sg ? QMM_RU(32, true, 1024) : QMM_RU(32, false, 1024))
+                                 : (sg ? QMM_RU(32, true, 2048) : QMM_RU(32, false, 2048));
+    if (gs == 64) return short_k ? (sg ? QMM_RU(64, true, 1024) : QMM_RU(64, false, 1024))
+                                 : (sg ? QMM_RU(64, true, 2048) : QMM_RU(64, false, 2048));
+    return short_k ? (sg ? QMM_RU(128, true, 1024) : QMM_RU(128, false, 1024))
+                   : (sg ? QMM_RU(128, true, 2048) : QMM_RU(128, false, 2048));
+#undef QMM_RU
 }
 
 // Largest number of slots a class can hold: an expert receives at most one
@@ -497,7 +630,29 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
     const bool adjust = a->expert_scales || a->sort_expert_ids;
     const uint32_t sort = a->expert_scales ? a->sort_expert_ids : 1;
     const uint64_t nkeys = (uint64_t)R * E;
-    if (Lw.routes <= kFusedRoutes && R <= kFusedRows && nkeys <= kFusedKeys && nkeys * E <= kFusedCompares) {
+    const bool sg = a->up.signed_codes != 0;
+    // one token: route, slots and the up product in one launch
+    // (STARK_QMM_SEPARATE_ROUTE=1 in the environment keeps the separate route
+    // launch: a diagnostic, and the tests' way to compare the two paths)
+    const char* sep = std::getenv("STARK_QMM_SEPARATE_ROUTE");
+    const bool one = R == 1 && E <= kOneTokenExperts && !(sep && sep[0] == '1');
+    if (one) {
+        RouteOneArgs ra{a->router_logits, a->expert_scales, E, A, a->round_weights_bf16, a->round_logits_bf16,
+                        (uint32_t)adjust, sort, ids, weights, table, header};
+        GroupedLaunch g{};
+        g.op = bank_op(a->up, E * 2 * H, model, a->input);
+        g.header = header;
+        g.table = table;
+        g.out = act;
+        g.tiles = H / 8;
+        g.active = A;
+        g.hidden = H;
+        g.model = model;
+        g.cls = 0;
+        void* fn = pick_route_up_one(g.op.group_size, sg, model);
+        void* argv[] = {&g, &ra};
+        QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(A * g.tiles), dim3(kWg), argv, 0, stream));
+    } else if (Lw.routes <= kFusedRoutes && R <= kFusedRows && nkeys <= kFusedKeys && nkeys * E <= kFusedCompares) {
         hipLaunchKernelGGL(moe_route_compact, dim3(1), dim3(1024), nkeys * 8, stream, a->router_logits, R, E, A,
                            a->round_weights_bf16, a->round_logits_bf16, a->expert_scales, (uint32_t)adjust, sort,
                            Lw.max_slots, ids, weights, sorted, table, header);
@@ -513,10 +668,10 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
                            table, header);
         QMM_HIP_CHECK(hipGetLastError());
     }
-    // 3./4. grouped products, one launch per route-count class in use
-    const bool sg = a->up.signed_codes != 0;
+    // 3./4. grouped products, one launch per route-count class in use (the
+    // one-token path has run the up product already)
     const int top = (int)count_class(max_count);
-    for (int pass = 0; pass < 2; ++pass) {
+    for (int pass = one ? 1 : 0; pass < 2; ++pass) {
         GroupedLaunch g{};
         const bool up = pass == 0;
         g.op = up ? bank_op(a->up, E * 2 * H, model, a->input) : bank_op(a->down, E * model, H, act);

@@ -1,5 +1,7 @@
 """GPU parity of the MoE kernels (moe.rs:24-184 restated in the oracle) and of
 the fused routed-experts pipeline (routed.rs:154-257) through the C ABI."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -68,14 +70,25 @@ def test_gather_and_accumulate_exact(qmm, oracle):
         assert np.array_equal(H.from_dev(do, np.uint16), out)
 
 
-def routed_check(qmm, O, c, **flags):
+def routed_want(O, c, **flags):
     R, M, Hd, E, A = c["rows"], c["model"], c["hidden"], c["experts"], c["active"]
-    want = O.bf16_to_f32(O.routed_experts(c["x"], c["logits"], c["up"], c["down"], R, M, Hd, E, A,
+    return O.bf16_to_f32(O.routed_experts(c["x"], c["logits"], c["up"], c["down"], R, M, Hd, E, A,
                                           expert_scales=c["scales"], layout=c["layout"], group=c["group"],
                                           round_logits=flags.get("rl", False), round_weights=flags.get("rw", False),
                                           round_products=flags.get("rp", False),
                                           round_accumulator=flags.get("ra", False),
                                           sort_ids=flags.get("si", False)))
+
+
+def routed_check(qmm, O, c, workspace=None, **flags):
+    want = routed_want(O, c, **flags)
+    got = routed_run(qmm, c, workspace, **flags)
+    check_routed(O, c, got, want, flags)
+    return got, want
+
+
+def routed_run(qmm, c, workspace=None, **flags):
+    R, M, Hd, E, A = c["rows"], c["model"], c["hidden"], c["experts"], c["active"]
     corr = qmm.BIASES if c["up"]["biases"] is not None else qmm.SYMMETRIC
 
     def qb(b, rows, cols):
@@ -89,11 +102,9 @@ def routed_check(qmm, O, c, **flags):
                              expert_scales=None if c["scales"] is None else H.to_dev(c["scales"]),
                              round_logits=flags.get("rl", False), round_weights=flags.get("rw", False),
                              round_products=flags.get("rp", False), round_accumulator=flags.get("ra", False),
-                             sort_expert_ids=flags.get("si", False))
+                             sort_expert_ids=flags.get("si", False), workspace=workspace)
     torch.cuda.synchronize()
-    got = O.bf16_to_f32(H.from_dev(out.view(torch.int16), np.uint16))
-    check_routed(O, c, got, want, flags)
-    return got, want
+    return (H.from_dev(out.view(torch.int16), np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
 def _dequant4(O, bank, r0, rows, cols, total_rows, layout, group):
@@ -199,6 +210,81 @@ def test_routed_experts_qwen3_moe_geometry(qmm, oracle, rows):
     the K=2048 grouped up kernels of every route-count class run."""
     c = MC.case(oracle, 9 + rows, rows, model=2048, hidden=768, experts=128, active=8)
     routed_check(qmm, oracle, c)
+
+
+def _workspace_routes(oracle, c, ws, flags):
+    """(ids, weights) the call left at the start of its workspace, and the
+    oracle's route (+ adjust, as routed.rs:188-209 applies it) of the same logits."""
+    R, E, A = c["rows"], c["experts"], c["active"]
+    n = R * A
+    raw = ws.cpu().numpy()
+    ids = raw[: 4 * n].view(np.uint32)
+    w = raw[(4 * n + 255) // 256 * 256:][: 4 * n].view(np.float32)
+    want_ids, want_w = oracle.moe_route(c["logits"], R, E, A, flags.get("rw", False), flags.get("rl", False))
+    gains = c["scales"]
+    if gains is not None or flags.get("si", False):
+        g = gains if gains is not None else np.ones(E, np.float32)
+        oracle.moe_adjust_routes(want_ids, want_w, g, R, E, A, flags.get("si", False) if gains is not None else True)
+    return ids, w, want_ids, want_w
+
+
+@pytest.mark.parametrize("experts,active,flags", [(128, 8, {}), (256, 8, dict(si=True)),
+                                                  (64, 4, dict(rl=True, rp=True)), (16, 4, dict(si=True)),
+                                                  (256, 8, dict(rw=True, ra=True)), (257, 8, {})])
+def test_routed_experts_one_token(qmm, oracle, experts, active, flags):
+    """One token (E <= 256) routes inside the up launch (every workgroup ranks
+    the token's logits itself; workgroup 0 files the slots). Its ids, weights
+    and outputs are the same bits as the separate route launch + compaction
+    gives, the ids equal the oracle's route + adjust, the weights meet the
+    route kernels' bar and the outputs the routed bar. With bf16-rounded
+    weights a last-bit difference of expf (the device's against the oracle's
+    libm) can move a weight by one bf16 ulp, which the output bar does not
+    cover; there the output is held to the separate path only. E = 257 takes
+    the separate route launch."""
+    c = MC.case(oracle, 700 + experts + active, 1, model=1024, hidden=256, experts=experts, active=active,
+                gains=bool(flags.get("si")) and experts != 16)
+    c["logits"][: experts // 4] = c["logits"][experts // 4: experts // 2]  # exact ties: the lower id wins
+    need = qmm.routed_experts_workspace_size(1, 1024, 256, experts, active)
+    runs = []
+    for separate in (False, True):  # the fused launch, then the separate route launch + compaction
+        if separate:
+            os.environ["STARK_QMM_SEPARATE_ROUTE"] = "1"
+        try:
+            ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+            out = routed_run(qmm, c, ws, **flags)
+        finally:
+            os.environ.pop("STARK_QMM_SEPARATE_ROUTE", None)
+        runs.append((out, ws))
+    (got, ws), (got2, ws2) = runs
+    ids, w, want_ids, want_w = _workspace_routes(oracle, c, ws, flags)
+    ids2, w2, _, _ = _workspace_routes(oracle, c, ws2, flags)
+    # both paths give the same bits
+    assert np.array_equal(ids, ids2) and np.array_equal(w.view(np.uint32), w2.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), got2.view(np.uint32))
+    # and the oracle's routes, weights and outputs
+    assert np.array_equal(ids, want_ids)
+    rtol = 2.0 ** -7 if flags.get("rw") else 4e-7 * 8
+    assert np.allclose(w, want_w, rtol=rtol, atol=0)
+    if not flags.get("rw"):
+        check_routed(oracle, c, got, routed_want(oracle, c, **flags), flags)
+
+
+def test_routed_experts_one_token_non_finite_logit(qmm, oracle):
+    """A non-finite logit: every route of the token reads expert 0 with a NaN
+    weight (moe.rs:52-84), in the fused one-token launch as in the route kernels."""
+    c = MC.case(oracle, 812, 1, model=256, hidden=128, experts=32, active=4)
+    c["logits"][5] = np.nan
+    b = lambda bank, rows, cols: qmm.QuantizedB(
+        codes=H.to_dev(bank["codes"]), scales=H.to_dev(bank["scales"]), correction_data=H.to_dev(bank["biases"]),
+        params=qmm.QuantParams(c["layout"], rows, cols // c["group"]))
+    need = qmm.routed_experts_workspace_size(1, 256, 128, 32, 4)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    qmm.routed_experts(H.to_dev(c["x"]), H.to_dev(c["logits"]), b(c["up"], 32 * 2 * 128, 256), b(c["down"], 32 * 256, 128),
+                       1, 256, 128, 32, 4, workspace=ws)
+    torch.cuda.synchronize()
+    ids, w, want_ids, want_w = _workspace_routes(oracle, c, ws, {})
+    assert np.array_equal(ids, want_ids) and not ids.any()
+    assert np.isnan(w).all() and np.isnan(want_w).all()
 
 
 def test_routed_experts_rejections(qmm, oracle):
