@@ -234,8 +234,9 @@ __global__ __launch_bounds__(64 * G) void attn_partial_kernel(const uint16_t* q,
 }
 
 // Combine the chunks of each query head: out = sum_c o_c e^(m_c - m) / sum_c l_c e^(m_c - m).
-// The chunk maxima and sums are read in parallel first; the weighted sum of
-// the partial outputs then issues its loads eight chunks at a time.
+// The chunk maxima and sums are read in parallel first (the first 128 with
+// the first partial outputs, before the position is known); the weighted sum
+// of the remaining partial outputs issues its loads eight chunks at a time.
 __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const float* pml, uint16_t* out,
                                                           const int32_t* pos_ptr, uint32_t nchunks, uint32_t cap) {
     __shared__ float fs[kMaxChunks];
@@ -249,11 +250,13 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
     float pre[kPre];
 #pragma unroll
     for (uint32_t j = 0; j < kPre; ++j) pre[j] = j < nchunks ? col[(size_t)j * kHd] : 0.0f;
+    // this thread's first chunk statistics, likewise before the position is known
+    const float2* ml = (const float2*)pml + (size_t)h * nchunks;
+    const float2 ml0 = d < nchunks ? ml[d] : float2{0.0f, 0.0f};
     const uint32_t len = min((uint32_t)*pos_ptr + 1, cap);
     const uint32_t nc = min(nchunks, (len + kChunk - 1) / kChunk);
-    const float2* ml = (const float2*)pml + (size_t)h * nchunks;
-    float mx = -INFINITY;
-    for (uint32_t c = d; c < nc; c += 128) mx = fmaxf(mx, ml[c].x);
+    float mx = d < nc ? ml0.x : -INFINITY;
+    for (uint32_t c = d + 128; c < nc; c += 128) mx = fmaxf(mx, ml[c].x);
     mx = wave_max(mx);
     if ((d & 63) == 0) red[d >> 6] = mx;
     __syncthreads();
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
     __syncthreads();
     float l = 0.0f;
     for (uint32_t c = d; c < nc; c += 128) {
-        const float2 v = ml[c];
+        const float2 v = c == d ? ml0 : ml[c];
         const float f = __expf(v.x - m);
         fs[c] = f;
         l = fmaf(v.y, f, l);
