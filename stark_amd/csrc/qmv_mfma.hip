@@ -445,15 +445,32 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
         return min((e & 0xffffffu) * kTR, op.n - kTR);
     };
 
-    // RMS-norm prologue: the row's first 8192 values are loaded before the
-    // first unit's loads (so that waiting for them waits for nothing else) and
-    // summed after those are issued
-    u32x4 q4[4];
+    // RMS-norm prologue. The sum of squares runs in chunk-major order: the
+    // first four waves' lane l sums, for chunks c = wave, wave + 4, ... (1024
+    // values each), the 8-value vectors 128c + l and 128c + 64 + l -- the two
+    // vectors a wave stages of its chunk -- then the wave sums (xor butterfly)
+    // and the four waves in order (the decode loop's RMS-norm kernel sums in
+    // the same order). With K = 4096 and four waves every wave computes all
+    // four waves' sums itself (eight vectors per lane, L2 hits after the
+    // first), so that no wave waits for another's loads; otherwise the row's
+    // first two chunks per wave are loaded before the first unit's loads (so
+    // that waiting for them waits for nothing else), summed after those are
+    // issued and combined through LDS at the list barrier.
+    u32x4 q4[4], q8[8];
     const AffineOp& o0 = kb_->op[((cu32*)sched.tiles)[lo] >> 24];
     const __amdgpu_buffer_rsrc_t x0r = rsrc(o0.x, o0.k * 2);
+    const bool ss_from_stage = WV == 4 && o0.k == 4 * kUnitK;
+    const auto ss_offset = [&](uint32_t c, int half) {  // byte offset of vector 128c + 64 half + lane
+        return wave < 4 ? (c * kUnitK + 512 * half + lane * 8) * 2 : OOB;
+    };
     if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM) {
+        if (ss_from_stage) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, tid < (uint32_t)kWg ? (tid + j * kWg) * 16 : OOB);
+            for (int j = 0; j < 8; ++j) q8[j] = buf_load(x0r, ((j >> 1) * kUnitK + 512 * (j & 1) + lane * 8) * 2);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, ss_offset(wave + 4 * (j >> 1), j & 1));
+        }
     }
 
     u32x4 ring[8];
@@ -495,25 +512,46 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
 #pragma unroll
         for (int s = 0; s < 8; ++s) ring[s] = buf_load<kBufNt>(cr, vo, step_soff(*opp, s));
     }
-    if (PRO == STARK_QMM_PROLOGUE_RMS_NORM && wave < 4) {
-        // sum of squares by the first 256 threads: thread t takes 8-value
-        // vectors t, t + 256, ... in order, then the wave sums (xor butterfly)
-        // and the four waves in order; loads past the row read zero and add
-        // nothing
-        float ss = 0.0f;
-        const uint32_t nv = o0.k / 8;
-        for (uint32_t v0 = 0;;) {
+    float inv = 0.0f;
+    if (PRO == STARK_QMM_PROLOGUE_RMS_NORM && ss_from_stage) {
+        float p[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+        for (int w = 0; w < 4; ++w) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const float a = __uint_as_float(q4[j][q] << 16), b = __uint_as_float(q4[j][q] & 0xffff0000u);
+                    const float a = __uint_as_float(q8[2 * w + h][q] << 16);
+                    const float b = __uint_as_float(q8[2 * w + h][q] & 0xffff0000u);
                     ss = fmaf(a, a, fmaf(b, b, ss));
                 }
-            v0 += 4 * kWg;
-            if (v0 >= nv) break;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, (v0 + tid + j * kWg) * 16);
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            p[w] = ss;
+        }
+        inv = 1.0f / sqrtf((p[0] + p[1] + p[2] + p[3]) / (float)o0.k + kb_->pro_eps);
+    }
+    if (PRO == STARK_QMM_PROLOGUE_RMS_NORM && !ss_from_stage && wave < 4) {
+        // (loads past the row read zero and add nothing)
+        float ss = 0.0f;
+        const auto sq = [&](const u32x4& u) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float a = __uint_as_float(u[q] << 16), b = __uint_as_float(u[q] & 0xffff0000u);
+                ss = fmaf(a, a, fmaf(b, b, ss));
+            }
+        };
+        {
+            const uint32_t nch = o0.k / kUnitK;
+            for (uint32_t c = wave;;) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sq(q4[j]);
+                c += 8;
+                if (c >= nch) break;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) q4[j] = buf_load(x0r, ss_offset(c + 4 * (j >> 1), j & 1));
+            }
         }
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
@@ -521,8 +559,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
     }
     if (tid < (uint32_t)kListLds) lds.list[tid] = list_v;
     lds_barrier();
-    float inv = 0.0f;
-    if constexpr (PRO == STARK_QMM_PROLOGUE_RMS_NORM)
+    if (PRO == STARK_QMM_PROLOGUE_RMS_NORM && !ss_from_stage)
         inv = 1.0f / sqrtf((lds.ssq[0] + lds.ssq[1] + lds.ssq[2] + lds.ssq[3]) / (float)opp->k + kb_->pro_eps);
     uint32_t tg0 = ~0u, tg1 = ~0u, tg2 = ~0u;  // (op << 16 | chunk) held by each activation region
     const auto tag_of = [&](uint32_t rg) { return rg == 0 ? tg0 : rg == 1 ? tg1 : tg2; };

@@ -70,19 +70,29 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // out = x * rsqrt(mean(x^2) + eps) * w, one row of n (n % 256 == 0), 256 threads;
 // the bf16 roundings on v_cvt_pk_bf16_f32, as the products' RMS-norm prologue.
-// Every load of a thread is a 16-byte vector issued before the first use (the
-// row is read once; rows up to 8192 stay in registers for the second pass).
+// Thread t = 64 w + l owns the 8-value vectors 128c + l and 128c + 64 + l of
+// the 1024-value chunks c = w, w + 4, ... (chunk-major: the order in which
+// the products' RMS-norm prologue sums the row, so that both compute the same
+// inverse norm), summed in that order, then the wave sums (xor butterfly) and
+// the four waves in order; rows that are not whole chunks take vectors t,
+// t + 256, ... instead. Every load of a thread is a 16-byte vector issued
+// before the first use (rows up to 8192 stay in registers for the second pass).
 __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out,
                                                        uint32_t n, float eps) {
     constexpr int kKeep = 4;  // vectors of 8 values kept per thread
     __shared__ float part[4];
     const uint32_t t = threadIdx.x, nv = n / 8;
+    const bool chunked = n % 1024 == 0;
+    // j-th vector of this thread
+    const auto vec = [&](uint32_t j) -> uint32_t {
+        return chunked ? 128 * ((t >> 6) + 4 * (j >> 1)) + 64 * (j & 1) + (t & 63) : t + 256 * j;
+    };
     const uint4* xv = (const uint4*)x;
     uint4 keep[kKeep], wkeep[kKeep];  // the weights are loaded with x: one memory round trip
 #pragma unroll
-    for (int j = 0; j < kKeep; ++j) keep[j] = t + j * 256 < nv ? xv[t + j * 256] : uint4{0, 0, 0, 0};
+    for (int j = 0; j < kKeep; ++j) keep[j] = vec(j) < nv ? xv[vec(j)] : uint4{0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < kKeep; ++j) wkeep[j] = t + j * 256 < nv ? ((const uint4*)w)[t + j * 256] : uint4{0, 0, 0, 0};
+    for (int j = 0; j < kKeep; ++j) wkeep[j] = vec(j) < nv ? ((const uint4*)w)[vec(j)] : uint4{0, 0, 0, 0};
     float ss = 0.0f;
     const auto sq = [&](const uint4& u) {
         const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
@@ -94,7 +104,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
     };
 #pragma unroll
     for (int j = 0; j < kKeep; ++j) sq(keep[j]);
-    for (uint32_t i = t + kKeep * 256; i < nv; i += 256) sq(xv[i]);
+    for (uint32_t j = kKeep; vec(j) < nv; ++j) sq(xv[vec(j)]);
     ss = wave_sum(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
     __syncthreads();
@@ -113,8 +123,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
     };
 #pragma unroll
     for (int j = 0; j < kKeep; ++j)
-        if (t + j * 256 < nv) emit(t + j * 256, keep[j], wkeep[j]);
-    for (uint32_t i = t + kKeep * 256; i < nv; i += 256) emit(i, xv[i], ((const uint4*)w)[i]);
+        if (vec(j) < nv) emit(vec(j), keep[j], wkeep[j]);
+    for (uint32_t j = kKeep; vec(j) < nv; ++j) emit(vec(j), xv[vec(j)], ((const uint4*)w)[vec(j)]);
 }
 
 // Per-head RMSNorm of q and k, rotate-half RoPE at *pos, and the k/v write
