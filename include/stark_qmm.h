@@ -188,8 +188,9 @@ STARK_QMM_API stark_qmm_status stark_qmm_encode(stark_qmm_kernel* kernel, const 
 /* Independent products with one submission, in the manner of the hybrid
  * engine's Weights::matvec_many (src/engine/hybrid/weights.rs:1323-1388): every
  * args[i] is validated as stark_qmm_encode would, then all eligible GEMV
- * products share one launch per (bits, M class). Outputs must not alias inputs
- * of other entries. */
+ * products share one launch per (bits, M class) and the dequant-GEMM products
+ * (M > 16) one per (bits, signed codes, correction, plane type). Outputs must
+ * not alias inputs or outputs of other entries. */
 STARK_QMM_API stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kernel, const stark_qmm_args* args, uint32_t count,
                                        void* stream);
 

@@ -216,6 +216,26 @@ stark_qmm_status encode_product(stark_qmm_kernel* kr, const stark_qmm_args* args
     return launch_affine_generic(op, bits, stream);
 }
 
+// The int8-activation GEMM operands of args when the product takes that grid
+// with the same validation as encode_product (else false: the entry then
+// goes through stark_qmm_encode, which reports any error).
+bool a8_gemm_entry(const stark_qmm_kernel* kr, const stark_qmm_args* a, AffineOp* op, A8Operand* q, int* bits) {
+    const stark_qmm_b& b = a->b;
+    if (a->a_kind != STARK_QMM_A_INT8_SYMMETRIC || a->a_code_layout > STARK_QMM_CODES_GROUPED_BY_NIBBLE || !b.codes ||
+        a->d_ops.rht_factors || b.params.materialize_affine_input_sum || a->gather_indices || a->m <= 16 || a->n == 0)
+        return false;
+    const uint32_t ag = a->a_scale_group_size, gs = b.group_size;
+    if (!(ag == 32 || ag == 64 || ag == 128) || a->k % ag != 0 || !(gs == 32 || gs == 64 || gs == 128) ||
+        !(b.mode == STARK_QMM_MODE_U4 || b.mode == STARK_QMM_MODE_U8))
+        return false;
+    if (build_affine_op(kr, b, a->m, a->n, a->k, nullptr, a->d, a->d_ops, nullptr, op, bits) != STARK_QMM_OK)
+        return false;
+    if (!a->d || (a->k && (!a->a || !a->a_scales))) return false;
+    *q = A8Operand{(const int8_t*)a->a, a->a_scales, a->a_scale_group_size,
+                   a->a_code_layout == STARK_QMM_CODES_GROUPED_BY_NIBBLE ? 1u : 0u};
+    return a8_gemm_eligible(*op, *q, *bits);
+}
+
 }  // namespace
 
 extern "C" {
@@ -241,11 +261,27 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
     if (!kr || (!args && count)) return STARK_QMM_INVALID_ARGUMENT;
     hipStream_t stream = (hipStream_t)stream_ptr;
     std::vector<AffineOp> fast4, fast8;
+    // prefill-sized products by (bits, signed codes, biases, bf16 planes): one grid each
+    std::vector<AffineOp> gemm[2][2][2][2];
+    // int8-activation prefill products by grid class
+    std::vector<AffineOp> a8_ops[16];
+    std::vector<A8Operand> a8_as[16];
     std::vector<size_t> rest;
     const size_t xsz = kr->x_dt == STARK_QMM_F32 ? 4 : 2;
     for (uint32_t i = 0; i < count; ++i) {
         const stark_qmm_args* a = &args[i];
         if (a->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
+        {
+            AffineOp op;
+            A8Operand q;
+            int bits;
+            if (a8_gemm_entry(kr, a, &op, &q, &bits)) {
+                const uint32_t c = a8_gemm_class(op, q, bits);
+                a8_ops[c].push_back(op);
+                a8_as[c].push_back(q);
+                continue;
+            }
+        }
         if (a->d_ops.rht_factors || a->a_kind != STARK_QMM_A_FULL_PRECISION || !a->b.codes || a->b.params.materialize_affine_input_sum || a->m == 0 || a->n == 0) {
             rest.push_back(i);
             continue;
@@ -256,7 +292,10 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
         stark_qmm_status st = build_affine_op(kr, a->b, a->m, a->n, a->k, x, a->d, a->d_ops, a->gather_indices, &op, &bits);
         if (st != STARK_QMM_OK) return st;
         if (!a->d || (!x && a->k)) return STARK_QMM_INVALID_ARGUMENT;
-        if (!affine_fast_eligible(op, bits) || op.gather || (op.m > 16 && !kr->reference_accumulation)) {
+        if (op.m > 16 && !kr->reference_accumulation && gemm_eligible(op, bits)) {
+            gemm[bits == 8][(op.flags & FLAG_SIGNED) != 0][op.corr_kind == STARK_QMM_CORRECTION_BIASES]
+                [op.w_dt == STARK_QMM_BF16].push_back(op);
+        } else if (!affine_fast_eligible(op, bits) || op.gather || (op.m > 16 && !kr->reference_accumulation)) {
             rest.push_back(i);
         } else if (bits == 4) {
             fast4.push_back(op);
@@ -274,6 +313,22 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
         st = launch_affine_gemv(many.data(), (uint32_t)many.size(), bits, stream);
         if (st != STARK_QMM_OK) return st;
     }
+    for (int b8 = 0; b8 < 2; ++b8)
+        for (auto& a : gemm[b8])
+            for (auto& c : a)
+                for (auto& v : c)
+                    for (size_t s = 0; s < v.size(); s += kMaxBatchOps) {
+                        const uint32_t n = (uint32_t)std::min<size_t>(kMaxBatchOps, v.size() - s);
+                        const stark_qmm_status st = launch_affine_gemm_group(v.data() + s, n, b8 ? 8 : 4, stream);
+                        if (st != STARK_QMM_OK) return st;
+                    }
+    for (uint32_t c = 0; c < 16; ++c)
+        for (size_t s = 0; s < a8_ops[c].size(); s += kMaxBatchOps) {
+            const uint32_t n = (uint32_t)std::min<size_t>(kMaxBatchOps, a8_ops[c].size() - s);
+            const stark_qmm_status st =
+                launch_affine_a8_gemm_group(a8_ops[c].data() + s, a8_as[c].data() + s, n, (c & 8) ? 8 : 4, stream);
+            if (st != STARK_QMM_OK) return st;
+        }
     for (size_t i : rest) {
         stark_qmm_status st = stark_qmm_encode(kr, &args[i], stream_ptr);
         if (st != STARK_QMM_OK) return st;

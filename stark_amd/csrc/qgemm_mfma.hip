@@ -38,14 +38,15 @@ __device__ __forceinline__ float plane_f32(const void* p, size_t i) {
     return BF ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
 }
 
+// Output tile (bx, by) of one product: columns 128 bx.., rows 128 by...
 // BITS: 4 or 8. CORR: 0 symmetric, 1 biases. BF: bf16 (else f16) planes.
 template <int BITS, int CORR, bool SIGNED, bool BF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
+__device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint32_t by) {
     __shared__ GemmLds lds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t M = op.m, N = op.n, K = op.k;
-    const uint32_t m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const uint32_t m0 = by * kBM, n0 = bx * kBN;
     const size_t row_bytes = (size_t)K * BITS / 8;
     const uint16_t* X = (const uint16_t*)op.x;
 
@@ -203,6 +204,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
             }
 }
 
+template <int BITS, int CORR, bool SIGNED, bool BF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
+    gemm_tile<BITS, CORR, SIGNED, BF>(op, blockIdx.x, blockIdx.y);
+}
+
+__host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o) {
+    return ((o.n + kBN - 1) / kBN) * ((o.m + kBM - 1) / kBM);
+}
+
+// Several products in one grid (ops of one template class): the tiles of op
+// i follow those of op i - 1, each op's row-major over (row block, column
+// block), so that the column blocks that share a weight tile keep one XCD
+// while the op's column-block count is a multiple of 8. Ops come longest K
+// first, so the costliest tiles are dispatched first.
+template <int BITS, int CORR, bool SIGNED, bool BF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
+    (void)batch;
+    const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t t = blockIdx.x, i = 0;
+    for (; i + 1 < kb->count; ++i) {
+        const uint32_t nt = gemm_tiles(kb->op[i]);
+        if (t < nt) break;
+        t -= nt;
+    }
+    const AffineOp& op = kb->op[i];
+    const uint32_t gx = (op.n + kBN - 1) / kBN;
+    gemm_tile<BITS, CORR, SIGNED, BF>(op, t % gx, t / gx);
+}
+
 }  // namespace
 
 bool gemm_eligible(const AffineOp& o, int bits) {
@@ -236,6 +266,52 @@ stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t st
     }
 #undef QMM_G_BITS
 #undef QMM_G
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
+
+}  // namespace qmm
+
+namespace qmm {
+
+// ops: gemm_eligible, M > 16, of one (bits, signedness, correction, plane
+// type) class; at most kMaxBatchOps.
+stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream) {
+    if (count == 0) return STARK_QMM_OK;
+    if (count == 1) return launch_affine_gemm(ops[0], bits, stream);
+    if (count > (uint32_t)kMaxBatchOps) return STARK_QMM_UNSUPPORTED;
+    std::vector<AffineOp> sorted(ops, ops + count);
+    std::stable_sort(sorted.begin(), sorted.end(), [](const AffineOp& a, const AffineOp& b) { return a.k > b.k; });
+    AffineBatch batch{};
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        batch.op[i] = sorted[i];
+        tiles += gemm_tiles(sorted[i]);
+    }
+    batch.count = count;
+    batch.total = (uint32_t)tiles;
+    if (tiles == 0) return STARK_QMM_OK;
+    if (tiles > 0x7fffffffu) return STARK_QMM_UNSUPPORTED;
+    const AffineOp& op = sorted[0];
+    const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
+    const bool bf = op.w_dt == STARK_QMM_BF16;
+    const dim3 grid((uint32_t)tiles);
+#define QMM_GG(B, C, S, F) hipLaunchKernelGGL((qgemm_group<B, C, S, F>), grid, dim3(256), 0, stream, batch)
+#define QMM_GG_BITS(B)                                                                 \
+    if (bi) {                                                                          \
+        if (sg) { if (bf) QMM_GG(B, 1, true, true); else QMM_GG(B, 1, true, false); } \
+        else { if (bf) QMM_GG(B, 1, false, true); else QMM_GG(B, 1, false, false); }  \
+    } else {                                                                           \
+        if (sg) { if (bf) QMM_GG(B, 0, true, true); else QMM_GG(B, 0, true, false); } \
+        else { if (bf) QMM_GG(B, 0, false, true); else QMM_GG(B, 0, false, false); }  \
+    }
+    if (bits == 4) {
+        QMM_GG_BITS(4)
+    } else {
+        QMM_GG_BITS(8)
+    }
+#undef QMM_GG_BITS
+#undef QMM_GG
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
 }

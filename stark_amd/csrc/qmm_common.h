@@ -231,6 +231,7 @@ stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stre
 // Prefill dequant-GEMM on the matrix cores for M > 16 (qgemm_mfma.hip).
 bool gemm_eligible(const AffineOp& op, int bits);
 stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t stream);
+stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream);
 // Route adjustment with optional gains (moe.hip).
 stark_qmm_status launch_moe_adjust(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
                                    uint32_t experts, uint32_t active, uint32_t sort_ids, hipStream_t stream);
@@ -291,6 +292,16 @@ struct A8Operand {
     uint32_t grouped;      // Int8CodeLayout::GroupedByNibble
 };
 stark_qmm_status launch_affine_a8(const AffineOp& op, const A8Operand& a, int bits, hipStream_t stream);
+// int8-activation products of one grid (prefill sizes)
+struct A8Batch {
+    AffineOp op[kMaxBatchOps];
+    A8Operand a[kMaxBatchOps];
+    uint32_t count;
+};
+bool a8_gemm_eligible(const AffineOp& op, const A8Operand& a, int bits);
+uint32_t a8_gemm_class(const AffineOp& op, const A8Operand& a, int bits);
+stark_qmm_status launch_affine_a8_gemm_group(const AffineOp* ops, const A8Operand* as, uint32_t count, int bits,
+                                             hipStream_t stream);
 
 // Largest M the GEMV kernel handles in one weight pass.
 constexpr uint32_t kGemvMaxM = 2;

@@ -202,14 +202,15 @@ __device__ __forceinline__ u32x4 a8_load16(__amdgpu_buffer_rsrc_t r, uint32_t of
 }
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Output tile (bx, by) of one product: columns kGB bx.., rows kGB by...
 template <int BITS, int G, bool SIGNED, bool GROUPED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_A8_WPE))) void qgemm_a8(AffineOp op, A8Operand a) {
+__device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, uint32_t bx, uint32_t by) {
     __shared__ A8GemmLds lds;
     constexpr int NCH = kGK / G;  // flush chunks per step
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t M = op.m, N = op.n, K = op.k, GA = K / a.group;
-    const uint32_t m0 = blockIdx.y * kGB, n0 = blockIdx.x * kGB;
+    const uint32_t m0 = by * kGB, n0 = bx * kGB;
     const size_t wrow = (size_t)K * BITS / 8;
 
     // staging roles: activation rows ar and 64 + ar, 16 bytes at aq * 16;
@@ -399,6 +400,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_A8_WPE)
             }
 }
 
+template <int BITS, int G, bool SIGNED, bool GROUPED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_A8_WPE))) void qgemm_a8(AffineOp op, A8Operand a) {
+    a8_tile<BITS, G, SIGNED, GROUPED>(op, a, blockIdx.x, blockIdx.y);
+}
+
+__host__ __device__ inline uint32_t a8_tiles(const AffineOp& o) {
+    return ((o.n + kGB - 1) / kGB) * ((o.m + kGB - 1) / kGB);
+}
+
+// Several products in one grid (one template class), as qgemm_group: op i's
+// tiles follow op i - 1's, row-major over (row block, column block).
+template <int BITS, int G, bool SIGNED, bool GROUPED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_A8_WPE))) void qgemm_a8_group(A8Batch batch) {
+    (void)batch;
+    const A8Batch* kb = (const A8Batch*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t t = blockIdx.x, i = 0;
+    for (; i + 1 < kb->count; ++i) {
+        const uint32_t nt = a8_tiles(kb->op[i]);
+        if (t < nt) break;
+        t -= nt;
+    }
+    const AffineOp& op = kb->op[i];
+    const uint32_t gx = (op.n + kGB - 1) / kGB;
+    a8_tile<BITS, G, SIGNED, GROUPED>(op, kb->a[i], t % gx, t / gx);
+}
+
+template <int BITS, int G>
+void launch_gemm_a8_group(const A8Batch& b, uint32_t tiles, hipStream_t stream) {
+    const bool sg = (b.op[0].flags & FLAG_SIGNED) != 0, gr = b.a[0].grouped != 0;
+    const dim3 grid(tiles);
+    if (sg && gr)
+        hipLaunchKernelGGL((qgemm_a8_group<BITS, G, true, true>), grid, dim3(256), 0, stream, b);
+    else if (sg)
+        hipLaunchKernelGGL((qgemm_a8_group<BITS, G, true, false>), grid, dim3(256), 0, stream, b);
+    else if (gr)
+        hipLaunchKernelGGL((qgemm_a8_group<BITS, G, false, true>), grid, dim3(256), 0, stream, b);
+    else
+        hipLaunchKernelGGL((qgemm_a8_group<BITS, G, false, false>), grid, dim3(256), 0, stream, b);
+}
+
 template <int BITS, int G>
 void launch_gemm_a8(const AffineOp& op, const A8Operand& a, hipStream_t stream) {
     const dim3 grid((op.n + kGB - 1) / kGB, (op.m + kGB - 1) / kGB);
@@ -415,12 +456,54 @@ void launch_gemm_a8(const AffineOp& op, const A8Operand& a, hipStream_t stream) 
 
 }  // namespace
 
+// Prefill sizes take the int8 GEMM on the matrix cores.
+bool a8_gemm_eligible(const AffineOp& op, const A8Operand& a, int bits) {
+    return op.m > 16 && !op.gather && op.k % kGK == 0 && (((uintptr_t)op.codes | (uintptr_t)a.codes) & 15) == 0 &&
+           op.corr_kind != STARK_QMM_CORRECTION_ZERO_POINTS && op.w_dt != STARK_QMM_F32 &&
+           (uint64_t)op.m * op.k < (1ull << 31) && (uint64_t)op.n * op.k * bits / 8 < (1ull << 31);
+}
+
+// Grid class of an a8_gemm_eligible product: (bits, flush group 32, signed codes, grouped activation codes).
+uint32_t a8_gemm_class(const AffineOp& op, const A8Operand& a, int bits) {
+    return (bits == 8 ? 8u : 0u) | (a.group == 32 || op.group_size == 32 ? 4u : 0u) |
+           ((op.flags & FLAG_SIGNED) ? 2u : 0u) | (a.grouped ? 1u : 0u);
+}
+
+stark_qmm_status launch_affine_a8_gemm_group(const AffineOp* ops, const A8Operand* as, uint32_t count, int bits,
+                                             hipStream_t stream) {
+    if (count == 0) return STARK_QMM_OK;
+    if (count == 1) return launch_affine_a8(ops[0], as[0], bits, stream);
+    if (count > (uint32_t)kMaxBatchOps) return STARK_QMM_UNSUPPORTED;
+    std::vector<uint32_t> idx(count);
+    for (uint32_t i = 0; i < count; ++i) idx[i] = i;
+    std::stable_sort(idx.begin(), idx.end(), [&](uint32_t x, uint32_t y) { return ops[x].k > ops[y].k; });
+    A8Batch b{};
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        b.op[i] = ops[idx[i]];
+        b.a[i] = as[idx[i]];
+        tiles += a8_tiles(b.op[i]);
+    }
+    b.count = count;
+    if (tiles == 0) return STARK_QMM_OK;
+    if (tiles > 0x7fffffffu) return STARK_QMM_UNSUPPORTED;
+    const bool g32 = (a8_gemm_class(b.op[0], b.a[0], bits) & 4u) != 0;
+    if (bits == 4 && g32)
+        launch_gemm_a8_group<4, 32>(b, (uint32_t)tiles, stream);
+    else if (bits == 4)
+        launch_gemm_a8_group<4, 64>(b, (uint32_t)tiles, stream);
+    else if (g32)
+        launch_gemm_a8_group<8, 32>(b, (uint32_t)tiles, stream);
+    else
+        launch_gemm_a8_group<8, 64>(b, (uint32_t)tiles, stream);
+    QMM_HIP_CHECK(hipGetLastError());
+    return STARK_QMM_OK;
+}
+
 stark_qmm_status launch_affine_a8(const AffineOp& op, const A8Operand& a, int bits, hipStream_t stream) {
     if (op.m == 0 || op.n == 0) return STARK_QMM_OK;
     // prefill sizes: the int8 GEMM on the matrix cores
-    if (op.m > 16 && !op.gather && op.k % kGK == 0 && (((uintptr_t)op.codes | (uintptr_t)a.codes) & 15) == 0 &&
-        op.corr_kind != STARK_QMM_CORRECTION_ZERO_POINTS && op.w_dt != STARK_QMM_F32 &&
-        (uint64_t)op.m * op.k < (1ull << 31) && (uint64_t)op.n * op.k * bits / 8 < (1ull << 31)) {
+    if (a8_gemm_eligible(op, a, bits)) {
         const bool g32 = a.group == 32 || op.group_size == 32;
         if (bits == 4 && g32)
             launch_gemm_a8<4, 32>(op, a, stream);

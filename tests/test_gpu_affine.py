@@ -609,3 +609,52 @@ def test_prefill_gemm_d_ops_and_reference_mode(qmm, oracle):
             check(got, want, mag=mag * 0.5 + 4.0, label="reference mode")
         else:
             assert np.all(np.abs(got - want) <= 0.05 * np.abs(want) + 0.4)
+
+
+def test_prefill_gemm_batch_matches_single(qmm, oracle):
+    """stark_qmm_encode_many with M > 16 products: one dequant-GEMM grid per
+    (bits, signed codes, correction, plane type) class, ops longest K first,
+    gives the bits of one launch per product (the same tile code, found by
+    block index). Ragged M, N and K, both layouts, 4- and 8-bit, both
+    corrections, signed codes, and the D-ops on one entry."""
+    rng = np.random.default_rng(77)
+    kern = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    # (m, n, k, bits, layout, correction, signed, d-ops)
+    specs = [(200, 300, 512, 4, 1, 1, False, False), (40, 1024, 1536, 4, 0, 1, False, True),
+             (130, 96, 256, 4, 1, 1, False, False), (17, 136, 320, 8, 0, 1, False, False),
+             (300, 256, 1024, 8, 1, 1, False, False), (64, 64, 512, 4, 1, 0, True, False),
+             (72, 520, 192, 4, 0, 0, True, False), (256, 128, 2048, 4, 1, 1, False, False)]
+    made = []
+    for m, n, kk, bits, layout, corr, signed, dops in specs:
+        W = H.affine_weights(oracle, rng, n, kk, bits, 64, layout, corr, H.BF16, quantizer=False)
+        x = H.to_dev(H.activations(oracle, rng, m, kk))
+        prior = H.to_dev(oracle.f32_to_bf16(rng.normal(0, 1, m * n).astype(np.float32))) if dops else None
+        bias = H.to_dev(oracle.f32_to_bf16(rng.normal(0, 0.5, n).astype(np.float32))) if dops else None
+        made.append((m, n, kk, bits, layout, corr, signed, W, x, prior, bias))
+
+    def args(m, n, kk, bits, layout, corr, signed, W, x, prior, bias):
+        d = prior.clone() if prior is not None else torch_empty(m * n, H.BF16)
+        return qmm.MatmulArguments(
+            a=x, m=m, n=n, k=kk, d=d,
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(layout, n, kk // 64), mode=qmm.MODE_U4 if bits == 4 else qmm.MODE_U8,
+                             correction=corr, signed_codes=signed,
+                             correction_data=None if W["corr"] is None else H.to_dev(W["corr"])),
+            d_transform=qmm.MatmulDOps(ab_scale=0.75, accumulate=True, bias=bias) if prior is not None else qmm.MatmulDOps())
+    many = [args(*t) for t in made]
+    kern.encode_many(many)
+    single = [args(*t) for t in made]
+    for a in single:
+        kern.encode(a)
+    torch.cuda.synchronize()
+    for a, b, t in zip(many, single, made):
+        assert torch.equal(a.d, b.d), f"batched and single differ for m={t[0]} n={t[1]} k={t[2]} bits={t[3]}"
+    # and the batch against the f64 product of the bf16-effective weights
+    for a, t in zip(many, made):
+        m, n, kk, bits, layout, corr, signed, W, x, prior, bias = t
+        if prior is not None:
+            continue
+        got = H.load(oracle, H.from_dev(a.d, np.uint16), H.BF16)
+        want, mag = bf16_effective_reference(oracle, W, H.from_dev(x, np.uint16), m, n, kk, bits, 64, layout, corr,
+                                             H.BF16, signed)
+        check(got, want.ravel(), mag=mag.ravel(), label=f"batched gemm m{m} n{n} k{kk} b{bits}")

@@ -453,3 +453,43 @@ def test_a8_prefill_full_width(qmm, oracle):
     mag = H.dequant_magnitude(oracle, w["codes"], w["scales"], w["corr"], n, k, 4, wg, 0, 1, BF16, xf.ravel(), F32,
                               len(rows))
     check(got[rows].ravel(), want, mag=mag, label="a8 prefill full width")
+
+
+def test_a8_prefill_batch_matches_single(qmm, oracle):
+    """stark_qmm_encode_many with int8-activation products of M > 16: one GEMM
+    grid per (bits, flush group, signed codes, code layout) class, each entry
+    with its own activations, gives the bits of one launch per product.
+    Ragged M, N and K; the D-ops on one entry; entries of three classes."""
+    rng = np.random.default_rng(55)
+    kern = qmm.MatmulKernel(BF16, BF16, BF16)
+    # (m, n, k, bits, wg, ag, grouped, d-ops)
+    specs = [(40, 136, 512, 4, 64, 128, True, False), (130, 96, 1024, 4, 64, 64, True, True),
+             (300, 256, 256, 4, 64, 128, True, False), (17, 64, 384, 8, 64, 64, False, False),
+             (64, 200, 512, 8, 64, 128, False, False), (33, 520, 256, 4, 64, 128, True, False)]
+    made = []
+    for m, n, k, bits, wg, ag, grouped, dops in specs:
+        w = H.affine_weights(oracle, rng, n, k, bits=bits, gs=wg)
+        q, sc = _a8_inputs(oracle, rng, m, k, ag, grouped)
+        prior = H.to_dev(oracle.f32_to_bf16(rng.normal(0, 1, m * n).astype(np.float32))) if dops else None
+        bias = H.to_dev(oracle.f32_to_bf16(rng.normal(0, 0.2, n).astype(np.float32))) if dops else None
+        made.append((m, n, k, bits, wg, ag, grouped, w, H.to_dev(q), H.to_dev(sc), prior, bias))
+
+    def args(m, n, k, bits, wg, ag, grouped, w, q, sc, prior, bias):
+        b = qmm.QuantizedB(codes=H.to_dev(w["codes"]), scales=H.to_dev(w["scales"]),
+                           params=qmm.QuantParams(layout=0, row_count=n, group_count=k // wg),
+                           mode=qmm.MODE_U4 if bits == 4 else qmm.MODE_U8, group_size=wg, correction=qmm.BIASES,
+                           correction_data=H.to_dev(w["corr"]))
+        A = qmm.Int8SymmetricA(values=q, scales=sc, scale_group_size=ag,
+                               code_layout=qmm.GROUPED_BY_NIBBLE if grouped else qmm.SEQUENTIAL)
+        d = prior.clone() if prior is not None else _dev_empty(m * n, torch.int16)
+        dops = qmm.MatmulDOps(ab_scale=0.5, accumulate=True, bias=bias) if prior is not None else qmm.MatmulDOps()
+        return qmm.MatmulArguments(a=A, b=b, d=d, m=m, n=n, k=k, d_transform=dops)
+    many = [args(*t) for t in made]
+    kern.encode_many(many)
+    single = [args(*t) for t in made]
+    for a in single:
+        kern.encode(a)
+    torch.cuda.synchronize()
+    for a, b, t in zip(many, single, made):
+        assert torch.equal(a.d, b.d), f"batched and single differ for m={t[0]} n={t[1]} k={t[2]} bits={t[3]}"
+    assert any(bool((a.d != 0).any()) for a in many)
