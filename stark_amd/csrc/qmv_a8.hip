@@ -175,11 +175,16 @@ __global__ __launch_bounds__(256) void qmv_a8_generic(AffineOp op, A8Operand a, 
 #endif
 constexpr int kGB = 128;         // tile rows (M) and columns (N)
 constexpr int kGK = 64;          // k per step
-constexpr int kGRow = kGK + 16;  // LDS row bytes: the 80-byte stride spreads a 16-row read over the banks
+// LDS rows of 64 int8 codes (4 chunks of 16 bytes), chunk c of row r stored
+// at chunk c ^ ((r >> 1) & 3): any 8 consecutive lanes moving 16 bytes each
+// then cover the 32 banks once -- the MFMA operand reads (rows r..r+7, one
+// chunk), the activation stores (2 rows x 4 chunks) and the 4-bit weight
+// stores (4 rows x 2 chunks).
+__device__ __forceinline__ uint32_t swz8(uint32_t r, uint32_t c) { return c ^ ((r >> 1) & 3); }
 
 struct A8GemmLds {
-    u32x4 a[2][kGB][kGRow / 16];  // int8 codes, 16 per element
-    u32x4 b[2][kGB][kGRow / 16];
+    u32x4 a[2][kGB][kGK / 16];  // int8 codes, 16 per element
+    u32x4 b[2][kGB][kGK / 16];
     float sa[2][2][kGB];  // [buf][chunk][row] activation scale
     float ua[2][2][kGB];  // [buf][chunk][row] activation scale * chunk sum of codes
     float ws[2][2][kGB];  // [buf][chunk][col] weight scale
@@ -261,7 +266,7 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t r = ar + 64 * h;
-            lds.a[buf][r][aq] = st.xa[h];
+            lds.a[buf][r][swz8(r, aq)] = st.xa[h];
             int sum = 0;
 #pragma unroll
             for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_sdot4((int)st.xa[h][t], 0x01010101, sum, false);
@@ -284,8 +289,8 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
                 out[2 * t] = GROUPED ? lo : __builtin_amdgcn_perm(hi, lo, 0x05010400u);
                 out[2 * t + 1] = GROUPED ? hi : __builtin_amdgcn_perm(hi, lo, 0x07030602u);
             }
-            lds.b[buf][r][off / 16] = u32x4{out[0], out[1], out[2], out[3]};
-            lds.b[buf][r][off / 16 + 1] = u32x4{out[4], out[5], out[6], out[7]};
+            lds.b[buf][r][swz8(r, off / 16)] = u32x4{out[0], out[1], out[2], out[3]};
+            lds.b[buf][r][swz8(r, off / 16 + 1)] = u32x4{out[4], out[5], out[6], out[7]};
         } else {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -299,7 +304,7 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
                     const uint32_t o1 = __builtin_amdgcn_perm(w[3], w[2], 0x07050301u);
                     w = u32x4{e0, o0, e1, o1};
                 }
-                lds.b[buf][ar + 64 * h][aq] = w;
+                lds.b[buf][ar + 64 * h][swz8(ar + 64 * h, aq)] = w;
             }
         }
         if (tid < kGB) {
@@ -335,11 +340,15 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
             }
             u32x4 bfr[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bfr[j] = lds.b[buf][wn * 64 + 16 * j + li][lq];
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t r = wn * 64 + 16 * j + li;
+                bfr[j] = lds.b[buf][r][swz8(r, lq)];
+            }
             i32x4_t cz = i32x4_t{0, 0, 0, 0};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                u32x4 af = lds.a[buf][wm * 64 + 16 * i + li][lq];
+                const uint32_t ra = wm * 64 + 16 * i + li;
+                u32x4 af = lds.a[buf][ra][swz8(ra, lq)];
                 // a 32-wide chunk keeps the activation bytes of its own half of
                 // the step (lanes 16 lq read bytes 16 lq ..), the other half zero
                 if (G == 32 && (lq >> 1) != (uint32_t)c) af = u32x4{0, 0, 0, 0};
