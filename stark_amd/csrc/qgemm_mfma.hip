@@ -39,10 +39,8 @@ struct GemmLds {
 };
 __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) { return c ^ (r & 7); }
 
-template <bool BF>
-__device__ __forceinline__ float plane_f32(const void* p, size_t i) {
-    const uint16_t h = ((const uint16_t*)p)[i];
-    return BF ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p, uint64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)min(bytes, (uint64_t)0x7fffffffu), 0x00020000);
 }
 
 // Output tile (bx, by) of one product: columns 128 bx.., rows 128 by...
@@ -54,8 +52,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t M = op.m, N = op.n, K = op.k;
     const uint32_t m0 = by * kBM, n0 = bx * kBN;
-    const size_t row_bytes = (size_t)K * BITS / 8;
-    const uint16_t* X = (const uint16_t*)op.x;
+    const uint32_t row_bytes = K * BITS / 8;
 
     // ---- per-thread load assignment
     // X tile [128][64] bf16: 4 x 16 B per thread (row v / 8, column 8 * (v % 8)).
@@ -70,24 +67,46 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         float ws[WPASS], wb[WPASS];
     };
 
+    // Buffer loads with per-thread offsets fixed here (the step adds k0):
+    // X rows past M and W rows past N lie past their resources and read
+    // zeros (with no branch around the load); a W row past N takes its plane
+    // entries from row N - 1 (its outputs are never stored). The plane group
+    // of a thread's codes is k0 / gs + (its offset in the step) / gs: group
+    // sizes are 32, 64 or 128 and k0 a multiple of 64.
+    const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(op.x, (uint64_t)M * K * 2);
+    const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(op.codes, (uint64_t)N * row_bytes);
+    const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(op.scales, 0x7fffffffu);
+    const __amdgpu_buffer_rsrc_t rb = gemm_rsrc(op.corr, 0x7fffffffu);
+    const uint32_t lgs = 31 - __builtin_clz(op.group_size);
+    uint32_t xo[4], wo[WPASS], po[WPASS];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
+        xo[i] = ((m0 + r) * K + c) * 2;
+    }
+#pragma unroll
+    for (int p = 0; p < WPASS; ++p) {
+        const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
+        const uint32_t n = n0 + r;
+        wo[p] = n * row_bytes + part * WPT * BITS / 8;
+        po[p] = (min(n, N - 1) * op.os + ((part * WPT) >> lgs) * op.gs) * 2;
+    }
     auto load_step = [&](Stage& st, uint32_t k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
-            const uint32_t m = m0 + r;
-            st.xa[i] = m < M ? *(const u32x4*)(X + (size_t)m * K + k0 + c) : u32x4{0, 0, 0, 0};
-        }
+        for (int i = 0; i < 4; ++i)
+            st.xa[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[i] + k0 * 2, 0, 0));
+        const uint32_t pg = (k0 >> lgs) * op.gs * 2;  // bytes of the step's first plane group
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
-            const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
-            const uint32_t n = n0 + r;
-            const bool ok = r < (uint32_t)kBN && n < N;
-            const uint32_t kk = k0 + part * WPT;  // first k of this thread's codes
-            const uint8_t* src = op.codes + (size_t)(ok ? n : 0) * row_bytes + (size_t)kk * BITS / 8;
-            st.wc[p] = ok ? __builtin_nontemporal_load((const u32x4*)src) : u32x4{0, 0, 0, 0};
-            const size_t si = (size_t)(ok ? n : 0) * op.os + (size_t)(kk / op.group_size) * op.gs;
-            st.ws[p] = ok ? plane_f32<BF>(op.scales, si) : 0.0f;
-            st.wb[p] = ok && CORR == 1 ? plane_f32<BF>(op.corr, si) : 0.0f;
+            st.wc[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo[p] + k0 * BITS / 8, 0, 2));
+            const uint32_t hs = __builtin_amdgcn_raw_buffer_load_b16(rs, po[p], pg, 0);
+            st.ws[p] = BF ? bf16_bits_to_f32(hs) : f16_bits_to_f32(hs);
+            if (CORR == 1) {
+                const uint32_t hb = __builtin_amdgcn_raw_buffer_load_b16(rb, po[p], pg, 0);
+                st.wb[p] = BF ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+            } else {
+                st.wb[p] = 0.0f;
+            }
         }
     };
     // X to LDS as is; W dequantised: w = s*q + bias_term (exact in f32: bf16/f16
@@ -255,6 +274,9 @@ bool gemm_eligible(const AffineOp& o, int bits) {
     if (!(o.corr_kind == STARK_QMM_CORRECTION_BIASES || o.corr_kind == STARK_QMM_CORRECTION_SYMMETRIC)) return false;
     if (o.group_size != 32 && o.group_size != 64 && o.group_size != 128) return false;
     if (o.k == 0 || o.k % kBK) return false;
+    // 32-bit buffer offsets (with a tile of rows to spare)
+    if ((uint64_t)(o.m + kBM) * o.k * 2 >= (1ull << 31) || (uint64_t)(o.n + kBN) * o.k * bits / 8 >= (1ull << 31))
+        return false;
     return (((uintptr_t)o.codes | (uintptr_t)o.x) & 15) == 0;
 }
 
