@@ -120,6 +120,10 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
             const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
+            // (never true with 256 threads; the compiler cannot tell, and the
+            // branch keeps the dequantisation below the MFMA block in its
+            // schedule: removing it measured 746 vs 791-797 TFLOP/s, a
+            // sched_barrier in its place 712-721)
             if (r >= (uint32_t)kBN) continue;
             const float s = st.ws[p];
             // bias term: biases, or -s * 2^(bits-1) for the symmetric correction
