@@ -7,7 +7,7 @@
 // threadgroup memory in the activation type and multiplies there; the CPU
 // twin of that rounding is reference_affine_linear_bf16
 // (backends/cpu/kernel/matmul/vision.rs:249-336): w = bf16_rne(f32(q)*s + b).
-// Here: a workgroup (4 waves) owns a 128x128 output tile; per 64-wide K step
+// Here: a workgroup (8 waves) owns a 256x128 output tile; per 64-wide K step
 // the X tile is staged in LDS as is and the W tile is dequantised into LDS as
 // bf16 (w = s*q + bias_term rounded to nearest even), double-buffered so the
 // next step's global loads overlap the current step's v_mfma_f32_16x16x32_bf16
@@ -24,7 +24,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kBM = 256, kBN = 128, kBK = 64;
+constexpr int kThreads = 512;
 
 // LDS tiles: rows of 64 bf16 (128 bytes, 8 chunks of 16 bytes), chunk c of
 // row r stored at chunk c ^ (r & 7). Every access here moves 16 bytes per
@@ -43,7 +44,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p, uint6
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)min(bytes, (uint64_t)0x7fffffffu), 0x00020000);
 }
 
-// Output tile (bx, by) of one product: columns 128 bx.., rows 128 by...
+// Output tile (bx, by) of one product: columns 128 bx.., rows 256 by...
 // BITS: 4 or 8. CORR: 0 symmetric, 1 biases. BF: bf16 (else f16) planes.
 template <int BITS, int CORR, bool SIGNED, bool BF>
 __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint32_t by) {
@@ -55,15 +56,19 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     const uint32_t row_bytes = K * BITS / 8;
 
     // ---- per-thread load assignment
-    // X tile [128][64] bf16: 4 x 16 B per thread (row v / 8, column 8 * (v % 8)).
-    // W tile: 128 rows x (64*BITS/8) bytes. 4-bit: 2 threads per row (32 codes
-    // each); 8-bit: 4 threads per row (16 codes each), two passes of 64 rows.
-    constexpr int WPT = BITS == 4 ? 32 : 16;        // codes per thread per pass
+    // X tile [256][64] bf16: 4 x 16 B per thread (row v / 8, column 8 * (v % 8)).
+    // W tile: 128 rows x (64*BITS/8) bytes, 4 threads per row, 16 codes each
+    // (8 bytes of 4-bit codes, 16 of 8-bit). Each dequantised weight serves the
+    // tile's 256 rows: against 128x128 tiles of four waves (two workgroups per
+    // CU), half the dequantisation per MFMA, 869-871 vs 792-795 TFLOP/s on the
+    // Qwen3-8B prefill set.
+    constexpr int WPT = 16;        // codes per thread per pass
     constexpr int TPR = kBK / WPT;                  // threads per row
-    constexpr int WPASS = (kBN * TPR + 255) / 256;  // passes over the rows
+    constexpr int WPASS = 1;  // passes over the rows
+    constexpr int WW = WPT * BITS / 32;  // code words per thread
     struct Stage {
         u32x4 xa[4];
-        u32x4 wc[WPASS];
+        uint32_t wc[WPASS][4];
         float ws[WPASS], wb[WPASS];
     };
 
@@ -81,12 +86,12 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     uint32_t xo[4], wo[WPASS], po[WPASS];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
+        const uint32_t v = tid + kThreads * i, r = v / 8, c = (v % 8) * 8;
         xo[i] = ((m0 + r) * K + c) * 2;
     }
 #pragma unroll
     for (int p = 0; p < WPASS; ++p) {
-        const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
+        const uint32_t v = tid + kThreads * p, r = v / TPR, part = v % TPR;
         const uint32_t n = n0 + r;
         wo[p] = n * row_bytes + part * WPT * BITS / 8;
         po[p] = (min(n, N - 1) * op.os + ((part * WPT) >> lgs) * op.gs) * 2;
@@ -98,7 +103,14 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         const uint32_t pg = (k0 >> lgs) * op.gs * 2;  // bytes of the step's first plane group
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
-            st.wc[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo[p] + k0 * BITS / 8, 0, 2));
+            if constexpr (WW == 4) {
+                const u32x4 t = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo[p] + k0 * BITS / 8, 0, 2));
+                st.wc[p][0] = t[0]; st.wc[p][1] = t[1]; st.wc[p][2] = t[2]; st.wc[p][3] = t[3];
+            } else {
+                typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+                const u32x2v t = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rw, wo[p] + k0 * BITS / 8, 0, 2));
+                st.wc[p][0] = t[0]; st.wc[p][1] = t[1]; st.wc[p][2] = 0; st.wc[p][3] = 0;
+            }
             const uint32_t hs = __builtin_amdgcn_raw_buffer_load_b16(rs, po[p], pg, 0);
             st.ws[p] = BF ? bf16_bits_to_f32(hs) : f16_bits_to_f32(hs);
             if (CORR == 1) {
@@ -114,23 +126,23 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     auto store_step = [&](const Stage& st, int buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t v = tid + 256 * i, r = v / 8, c = (v % 8) * 8;
+            const uint32_t v = tid + kThreads * i, r = v / 8, c = (v % 8) * 8;
             lds.a[buf][r][swz(r, c / 8)] = st.xa[i];
         }
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
-            const uint32_t v = tid + 256 * p, r = v / TPR, part = v % TPR;
-            // (never true with 256 threads; the compiler cannot tell, and the
+            const uint32_t v = tid + kThreads * p, r = v / TPR, part = v % TPR;
+            // (never true with kThreads threads; the compiler cannot tell, and the
             // branch keeps the dequantisation below the MFMA block in its
             // schedule: removing it measured 746 vs 791-797 TFLOP/s, a
-            // sched_barrier in its place 712-721)
+            // sched_barrier in its place 712-721, with 128x128 tiles)
             if (r >= (uint32_t)kBN) continue;
             const float s = st.ws[p];
             // bias term: biases, or -s * 2^(bits-1) for the symmetric correction
             const float b = CORR == 1 ? st.wb[p] : -s * (float)(1 << (BITS - 1));
             uint32_t bytes[WPT / 4];  // code e of this thread sits in byte e % 4 of bytes[e / 4]
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
+            for (int d = 0; d < WW; ++d) {
                 uint32_t u = st.wc[p][d];
                 if (BITS == 4) {
                     if (SIGNED) u ^= 0x88888888u;
@@ -159,7 +171,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     };
 
     // wave (wm, wn) owns rows wm*64.., cols wn*64.. of the tile
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 1, wn = wave & 1;  // wm 0..3
     const uint32_t li = lane & 15, lk = (lane >> 4) * 8;
     f32x4 acc[4][4];
 #pragma unroll
@@ -241,7 +253,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
 }
 
 template <int BITS, int CORR, bool SIGNED, bool BF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
     gemm_tile<BITS, CORR, SIGNED, BF>(op, blockIdx.x, blockIdx.y);
 }
 
@@ -255,7 +267,7 @@ __host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o) {
 // while the op's column-block count is a multiple of 8. Ops come longest K
 // first, so the costliest tiles are dispatched first.
 template <int BITS, int CORR, bool SIGNED, bool BF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
     (void)batch;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
     uint32_t t = blockIdx.x, i = 0;
@@ -289,7 +301,7 @@ stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t st
     if (grid.x == 0 || grid.y == 0) return STARK_QMM_OK;
     const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     const bool bf = op.w_dt == STARK_QMM_BF16;
-#define QMM_G(B, C, S, F) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F>), grid, dim3(256), 0, stream, op)
+#define QMM_G(B, C, S, F) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F>), grid, dim3(kThreads), 0, stream, op)
 #define QMM_G_BITS(B)                                                      \
     if (bi) {                                                              \
         if (sg) { if (bf) QMM_G(B, 1, true, true); else QMM_G(B, 1, true, false); } \
@@ -335,7 +347,7 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
     const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     const bool bf = op.w_dt == STARK_QMM_BF16;
     const dim3 grid((uint32_t)tiles);
-#define QMM_GG(B, C, S, F) hipLaunchKernelGGL((qgemm_group<B, C, S, F>), grid, dim3(256), 0, stream, batch)
+#define QMM_GG(B, C, S, F) hipLaunchKernelGGL((qgemm_group<B, C, S, F>), grid, dim3(kThreads), 0, stream, batch)
 #define QMM_GG_BITS(B)                                                                 \
     if (bi) {                                                                          \
         if (sg) { if (bf) QMM_GG(B, 1, true, true); else QMM_GG(B, 1, true, false); } \
