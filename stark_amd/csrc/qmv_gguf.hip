@@ -212,13 +212,16 @@ struct GEngine {
                 w[tt][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(crs, vo, 0, kBufNt));
             }
         }
+        // activations: chunks past the rows, the pass or K read zeros from past the resource
+        const __amdgpu_buffer_rsrc_t xrs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)op.x, 0, (int)min((uint64_t)M * K * 4, (uint64_t)0x7fffffffu), 0x00020000);
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
             const uint32_t v = tid + i * kWg, r = v / (PASS / 8), c = v % (PASS / 8);
             const bool ok = v < (uint32_t)XV && r < M && c * 8 < kvals;
-            const float* src = (const float*)op.x + (ok ? (size_t)r * K + kbase + c * 8 : 0);
-            xa[i] = *(const u32x4*)src;
-            xb[i] = *(const u32x4*)(src + 4);
+            const uint32_t xo = ok ? (r * K + kbase + c * 8) * 4 : 0x80000000u;
+            xa[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
+            xb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16, 0, 0));
         }
     }
 
@@ -247,13 +250,12 @@ struct GEngine {
             // per-group exponent E (group_shift): the 4 chunks of a 32-value
             // group sit in consecutive lanes; Q4_K values 32..63 of every 64
             // meet the high nibbles (16 q) and are staged at x * 2^(E-4)
-            const int E = group_shift(group_max<4>(f32x8_exp_max(xa[i], xb[i])));
+            const uint32_t fe = f32x8_exp_max(xa[i], xb[i]);
+            const int E = group_shift(group_max<4>(fe));
             const int Es = (KIND == 12 && ((c * 8) & 32)) ? E - 4 : E;
             const float sc = pow2i(Es);
-            if (v < (uint32_t)XV && r < M && c * 8 < kvals) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(x[e]);
-            }
+            // a value is infinite or NaN exactly when its exponent field is 255
+            bad |= v < (uint32_t)XV && r < M && c * 8 < kvals && fe == 255u;
             // hi = bf16(x sc) = bf16(x) sc and lo = bf16(x sc - hi) through the
             // hardware round-to-nearest-even pack; sc is a power of two, so the
             // sums of the scaled parts times 1/sc are the sums of the parts
@@ -592,6 +594,7 @@ stark_qmm_status launch_class(int c, const GgufOp* ops, uint32_t count, uint32_t
 // matrix-core kernel: f32 activations, 16-byte aligned rows, at least one tile
 bool mfma_ok(const GgufOp& o) {
     if (((uintptr_t)o.blocks & 15) || ((uintptr_t)o.x & 15) || o.k % 256 || o.n < (uint32_t)kRows) return false;
+    if ((uint64_t)o.k * 8 * 4 >= (1ull << 31)) return false;  // 32-bit offsets into 8 activation rows
     return o.x_dt == STARK_QMM_F32;
 }
 

@@ -166,13 +166,31 @@ def test_affine_matvec(qmm, oracle, bits, group, sdt):
     check(out.cpu().numpy(), want, mag=mag, label=f"affine b{bits} g{group} dt{sdt}")
 
 
-def test_non_finite_input_is_rejected(qmm, oracle):
-    rng = np.random.default_rng(4)
-    blocks = _packed(oracle, rng, 8, 32, 256)
-    x = rng.normal(0, 1, 256).astype(np.float32)
-    x[77] = np.inf
-    op = qmm.MappedOperation(matrices=[qmm.MappedMatrix(codes=H.to_dev(blocks.ravel()))],
-                             inputs=torch.from_numpy(x).cuda(), rows=32, columns=256, format=("packed", 8))
-    with pytest.raises(qmm.MatmulError) as e:
+@pytest.mark.parametrize("kind", [8, 12])
+@pytest.mark.parametrize("m", [1, 8])
+def test_non_finite_input_is_rejected(qmm, oracle, kind, m):
+    """The reference's input finite check (weight_metal.rs:435-440) on the
+    matrix-core path: an infinity or NaN anywhere in any activation row is
+    rejected; the largest finite magnitudes are not."""
+    rng = np.random.default_rng(4 + kind + m)
+    n, k = 32, 512
+    blocks = _packed(oracle, rng, kind, n, k)
+    codes = H.to_dev(blocks.ravel())
+
+    def run(x):
+        op = qmm.MappedOperation(matrices=[qmm.MappedMatrix(codes=codes)] * m,
+                                 inputs=torch.from_numpy(x.ravel()).cuda(), rows=n, columns=k, format=("packed", kind))
         qmm.mapped_many([op])
-    assert e.value.status == qmm.INVALID_ARGUMENT
+        torch.cuda.synchronize()
+
+    for bad in (np.inf, -np.inf, np.nan):
+        for row, col in ((0, 0), (m - 1, 77), (m // 2, k - 1)):
+            x = rng.normal(0, 1, (m, k)).astype(np.float32)
+            x[row, col] = bad
+            with pytest.raises(qmm.MatmulError) as e:
+                run(x)
+            assert e.value.status == qmm.INVALID_ARGUMENT, (bad, row, col)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    x[0, 5] = np.finfo(np.float32).max
+    x[m - 1, k - 2] = -np.finfo(np.float32).max
+    run(x)  # finite: no error
