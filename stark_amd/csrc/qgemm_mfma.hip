@@ -234,6 +234,22 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     if (s < steps) compute(0);  // odd step count: the last step sits in buffer 0
 
     // ---- epilogue: C[i][j] of a 16x16 block sits in lane j + 16*(i/4), element i%4
+    // Full tiles with a plain bf16 store (no D-op past ab_scale): one row
+    // pointer per (i, e), the column blocks at fixed offsets from it.
+    if (!(op.flags & (FLAG_ACCUMULATE | FLAG_SOFT_CAP)) && !op.bias && op.d_dt == STARK_QMM_BF16 &&
+        m0 + kBM <= M && n0 + kBN <= N) {
+        uint16_t* const d = (uint16_t*)op.d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
+                uint16_t* const row = d + (size_t)m * N + n0 + wn * 64 + (lane & 15);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) row[16 * j] = f32_to_bf16_bits(op.ab_scale * acc[i][j][e]);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
