@@ -397,6 +397,21 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
         barrier();
     }
 
+    // full tiles with a plain bf16 store (no D-op past ab_scale): one row
+    // pointer per (i, e), the column blocks at fixed offsets from it
+    if (!(op.flags & (FLAG_ACCUMULATE | FLAG_SOFT_CAP)) && !op.bias && op.d_dt == STARK_QMM_BF16 &&
+        m0 + kGB <= M && n0 + kGB <= N) {
+        uint16_t* const d = (uint16_t*)op.d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint16_t* const row = d + (size_t)(m0 + wm * 64 + 16 * i + 4 * lq + e) * N + n0 + wn * 64 + li;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) row[16 * j] = f32_to_bf16_bits(op.ab_scale * acc[i][j][e]);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
