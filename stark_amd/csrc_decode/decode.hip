@@ -342,24 +342,30 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
     __shared__ __attribute__((aligned(16))) uint16_t qs[G][kHd];  // the rotated query, bf16
     __shared__ float ws[G][kChunk];
     const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63, h = t >> 6;
+    const uint32_t p0 = c * kChunk;
+    constexpr int kPer = (kVec + 64 * G - 1) / (64 * G);
+    // The chunk's K/V rows are loaded before the position is known (every
+    // row below the capacity is cache memory; rows past the context and the
+    // new position's stale row are loaded and not used), so the position's
+    // load and the rows' loads share one memory round trip.
+    uint4 kv[kPer], vv[kPer];
+    {
+        const uint4* kg = (const uint4*)(kcache + ((size_t)g * cap + p0) * kHd);
+        const uint4* vg = (const uint4*)(vcache + ((size_t)g * cap + p0) * kHd);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const uint32_t v = t + j * 64 * G, row = v / (kHd / 8);
+            const bool ok = v < (uint32_t)kVec && p0 + row < cap;
+            kv[j] = ok ? kg[v] : uint4{0, 0, 0, 0};
+            vv[j] = ok ? vg[v] : uint4{0, 0, 0, 0};
+        }
+    }
     const int32_t pos = *pos_ptr;
     const uint32_t len = min((uint32_t)pos + 1, cap);
-    const uint32_t p0 = c * kChunk;
     if (p0 >= len) return;  // chunk past the context
     const uint32_t np = min((uint32_t)kChunk, len - p0);
     const bool own_row = (uint32_t)pos < cap && (uint32_t)pos >= p0 && (uint32_t)pos < p0 + kChunk;
     {
-        constexpr int kPer = (kVec + 64 * G - 1) / (64 * G);
-        const uint4* kg = (const uint4*)(kcache + ((size_t)g * cap + p0) * kHd);
-        const uint4* vg = (const uint4*)(vcache + ((size_t)g * cap + p0) * kHd);
-        uint4 kv[kPer], vv[kPer];
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const uint32_t v = t + j * 64 * G, row = v / (kHd / 8);
-            const bool ok = v < (uint32_t)kVec && row < np && !(own_row && p0 + row == (uint32_t)pos);
-            kv[j] = ok ? kg[v] : uint4{0, 0, 0, 0};
-            vv[j] = ok ? vg[v] : uint4{0, 0, 0, 0};
-        }
         // query head g*G + h: norm + RoPE
         {
             const uint16_t* src = q + (size_t)(g * G + h) * kHd;
@@ -368,11 +374,13 @@ __global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, c
             qs[h][lane] = ra;
             qs[h][lane + 64] = rb;
         }
+        // rows of the context only (scores and PV read rows < np), and not
+        // the new position's row, which wave 0 alone writes below
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
-            const uint32_t v = t + j * 64 * G;
-            if (v < (uint32_t)kVec) {
-                const uint32_t row = v / (kHd / 8), col = (v % (kHd / 8)) * 4;
+            const uint32_t v = t + j * 64 * G, row = v / (kHd / 8);
+            if (v < (uint32_t)kVec && row < np && !(own_row && p0 + row == (uint32_t)pos)) {
+                const uint32_t col = (v % (kHd / 8)) * 4;
                 *(uint4*)&ks[row * kRowK + col] = kv[j];
                 *(uint4*)&vs[row * (kHd / 2) + col] = vv[j];
             }
