@@ -658,3 +658,40 @@ def test_prefill_gemm_batch_matches_single(qmm, oracle):
         want, mag = bf16_effective_reference(oracle, W, H.from_dev(x, np.uint16), m, n, kk, bits, 64, layout, corr,
                                              H.BF16, signed)
         check(got, want.ravel(), mag=mag.ravel(), label=f"batched gemm m{m} n{n} k{kk} b{bits}")
+
+
+@pytest.mark.parametrize("w_dt,gs", [(H.F16, 32), (H.F16, 128), (H.BF16, 128), (H.BF16, 32)])
+def test_prefill_gemm_batch_plane_types_and_groups(qmm, oracle, w_dt, gs):
+    """One-grid prefill batches with f16 or bf16 planes and group sizes 32 and
+    128 (the group of a thread's codes found from the step's k and its offset
+    in the step): the bits of one launch per product, and the bf16-effective
+    f64 product within the accumulation bar."""
+    rng = np.random.default_rng(gs * 3 + (w_dt == H.F16))
+    kern = qmm.MatmulKernel(w_dt, H.BF16, H.BF16)
+    specs = [(300, 260, 768, 4, 1, 1, False), (40, 128, 1024, 4, 0, 0, True), (257, 96, 384, 8, 1, 1, False)]
+    made = []
+    for m, n, kk, bits, layout, corr, signed in specs:
+        W = H.affine_weights(oracle, rng, n, kk, bits, gs, layout, corr, w_dt, quantizer=False)
+        x = H.to_dev(H.activations(oracle, rng, m, kk))
+        made.append((m, n, kk, bits, layout, corr, signed, W, x))
+
+    def args(m, n, kk, bits, layout, corr, signed, W, x):
+        return qmm.MatmulArguments(
+            a=x, m=m, n=n, k=kk, d=torch_empty(m * n, H.BF16),
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(layout, n, kk // gs), mode=qmm.MODE_U4 if bits == 4 else qmm.MODE_U8,
+                             group_size=gs, correction=corr, signed_codes=signed,
+                             correction_data=None if W["corr"] is None else H.to_dev(W["corr"])))
+    many = [args(*t) for t in made]
+    kern.encode_many(many)
+    single = [args(*t) for t in made]
+    for a in single:
+        kern.encode(a)
+    torch.cuda.synchronize()
+    for a, b, t in zip(many, single, made):
+        assert torch.equal(a.d, b.d), f"batched and single differ for m={t[0]} n={t[1]} k={t[2]}"
+        m, n, kk, bits, layout, corr, signed, W, x = t
+        got = H.load(oracle, H.from_dev(a.d, np.uint16), H.BF16)
+        want, mag = bf16_effective_reference(oracle, W, H.from_dev(x, np.uint16), m, n, kk, bits, gs, layout, corr,
+                                             w_dt, signed)
+        check(got, want.ravel(), mag=mag.ravel(), label=f"batched gemm gs{gs} m{m} n{n} k{kk} b{bits}")
