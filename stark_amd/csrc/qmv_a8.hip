@@ -186,9 +186,11 @@ struct A8GemmLds {
     u32x4 a[2][kGB][kGK / 16];  // int8 codes, 16 per element
     u32x4 b[2][kGB][kGK / 16];
     float sa[2][2][kGB];  // [buf][chunk][row] activation scale
-    float ua[2][2][kGB];  // [buf][chunk][row] activation scale * chunk sum of codes
+    // rings of 8 chunks; rows padded to 144 floats so that the four lane
+    // groups of a bias read (four slots) fall on disjoint banks
+    float ur[8][kGB + 16];  // [chunk % 8][row] activation scale * chunk sum of codes
     float ws[2][2][kGB];  // [buf][chunk][col] weight scale
-    float wb[2][2][kGB];  // [buf][chunk][col] bias term (8-bit: + 128 s)
+    float br[8][kGB + 16];  // [chunk % 8][col] bias term (8-bit: + 128 s)
 };
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -262,7 +264,8 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
             st.b[c] = __builtin_amdgcn_raw_buffer_load_b16(rpb, biased ? md * 2 : 0x80000000u, 0, 0);
         }
     };
-    auto store = [&](const Stage& st, int buf) {
+    // (st: the step whose chunks this stage holds)
+    auto store = [&](const Stage& st, int buf, uint32_t step) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t r = ar + 64 * h;
@@ -275,7 +278,7 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
             if (G == 64 ? aq == 0 : (aq & 1) == 0) {
                 const uint32_t c = G == 64 ? 0 : aq >> 1;
                 lds.sa[buf][c][r] = st.sa[h];
-                lds.ua[buf][c][r] = st.sa[h] * (float)sum;
+                lds.ur[(step * NCH + c) & 7][r] = st.sa[h] * (float)sum;
             }
         }
         if (BITS == 4) {
@@ -314,7 +317,7 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
                 const float bt = biased ? (bfp ? bf16_bits_to_f32(st.b[c]) : f16_bits_to_f32(st.b[c]))
                                         : -sc * (float)(1 << (BITS - 1));
                 lds.ws[buf][c][tid] = sc;
-                lds.wb[buf][c][tid] = BITS == 8 ? bt + 128.0f * sc : bt;
+                lds.br[(step * NCH + c) & 7][tid] = BITS == 8 ? bt + 128.0f * sc : bt;
             }
         }
     };
@@ -332,12 +335,9 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll 1
         for (int c = 0; c < NCH; ++c) {
-            float s4[4], b4[4];
+            float s4[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                s4[j] = lds.ws[buf][c][wn * 64 + 16 * j + li];
-                b4[j] = lds.wb[buf][c][wn * 64 + 16 * j + li];
-            }
+            for (int j = 0; j < 4; ++j) s4[j] = lds.ws[buf][c][wn * 64 + 16 * j + li];
             u32x4 bfr[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -360,12 +360,10 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
                                                                  cz, 0, 0, 0);
                 // C element e of block (i, j): row 4 lq + e, column li
                 const f32x4 sa = *(const f32x4*)&lds.sa[buf][c][wm * 64 + 16 * i + 4 * lq];
-                const f32x4 ua = *(const f32x4*)&lds.ua[buf][c][wm * 64 + 16 * i + 4 * lq];
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc[i][j][e] = fmaf(sa[e] * s4[j], (float)C[j][e], fmaf(ua[e], b4[j], acc[i][j][e]));
+                    for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(sa[e] * s4[j], (float)C[j][e], acc[i][j][e]);
                 // the next row block's MFMAs start after this flush: their zero
                 // accumulator input is tied to this block's results, so only one
                 // block's 16 int32 sums are live (two waves per SIMD fit the registers)
@@ -375,6 +373,24 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
             // MFMAs above this flush would not fit the register budget
             __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    // The bias terms sum_c (s_a * sum q_a)[row, c] * bias_term[col, c] of four
+    // chunks as one f32 product per 16x16 block (v_mfma_f32_16x16x4_f32: A
+    // row = lane % 16, k = lane / 16; B k = lane / 16, column = lane % 16; D in
+    // the int8 product's C layout), chunks q0 .. q0 + 3 from the LDS rings
+    // (k entries at or past `valid` read as zero).
+    auto bias4 = [&](uint32_t q0, uint32_t valid) {
+        const uint32_t sl = (q0 + lq) & 7;
+        const bool ok = lq < valid;
+        float av[4], bv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) av[i] = ok ? lds.ur[sl][wm * 64 + 16 * i + li] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bv[j] = ok ? lds.br[sl][wn * 64 + 16 * j + li] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     };
 
     const auto barrier = [] {
@@ -388,13 +404,20 @@ __device__ __forceinline__ void a8_tile(const AffineOp& op, const A8Operand& a, 
     const uint32_t steps = K / kGK;
     Stage stg;
     load(stg, 0);
-    store(stg, 0);
+    store(stg, 0, 0);
     barrier();
     for (uint32_t st = 0; st < steps; ++st) {
         load(stg, min(st + 1, steps - 1) * kGK);
         compute(st & 1);
-        store(stg, (st & 1) ^ 1);
+        // every fourth chunk: the bias terms of the last four (the ring of 8
+        // holds them while the next step's chunks are stored beside them)
+        if (NCH == 2 ? (st & 1) : ((st & 3) == 3)) bias4((st + 1) * NCH - 4, 4);
+        store(stg, (st & 1) ^ 1, st + 1);
         barrier();
+    }
+    {
+        const uint32_t q = steps * NCH, rem = q & 3;
+        if (rem) bias4(q - rem, rem);
     }
 
     // full tiles with a plain bf16 store (no D-op past ab_scale): one row
