@@ -292,7 +292,7 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
         stark_qmm_status st = build_affine_op(kr, a->b, a->m, a->n, a->k, x, a->d, a->d_ops, a->gather_indices, &op, &bits);
         if (st != STARK_QMM_OK) return st;
         if (!a->d || (!x && a->k)) return STARK_QMM_INVALID_ARGUMENT;
-        if (op.m > 16 && !kr->reference_accumulation && gemm_eligible(op, bits)) {
+        if (op.m > 16 && !kr->reference_accumulation && gemm_eligible(op, bits) && op.m <= gemm_rows(op.k)) {
             gemm[bits == 8][(op.flags & FLAG_SIGNED) != 0][op.corr_kind == STARK_QMM_CORRECTION_BIASES]
                 [op.w_dt == STARK_QMM_BF16].push_back(op);
         } else if (!affine_fast_eligible(op, bits) || op.gather || (op.m > 16 && !kr->reference_accumulation)) {

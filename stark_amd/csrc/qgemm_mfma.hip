@@ -306,13 +306,38 @@ bool gemm_eligible(const AffineOp& o, int bits) {
     if (!(o.corr_kind == STARK_QMM_CORRECTION_BIASES || o.corr_kind == STARK_QMM_CORRECTION_SYMMETRIC)) return false;
     if (o.group_size != 32 && o.group_size != 64 && o.group_size != 128) return false;
     if (o.k == 0 || o.k % kBK) return false;
-    // 32-bit buffer offsets (with a tile of rows to spare)
-    if ((uint64_t)(o.m + kBM) * o.k * 2 >= (1ull << 31) || (uint64_t)(o.n + kBN) * o.k * bits / 8 >= (1ull << 31))
-        return false;
+    // 32-bit buffer offsets into the codes (with a tile of rows to spare);
+    // the activation rows are split into launches that fit (gemm_rows)
+    if ((uint64_t)(o.n + kBN) * o.k * bits / 8 >= (1ull << 31) || gemm_rows(o.k) == 0) return false;
     return (((uintptr_t)o.codes | (uintptr_t)o.x) & 15) == 0;
 }
 
+// Activation rows one grid takes at K: a multiple of the tile rows whose
+// 32-bit byte offsets (with a tile of rows to spare) stay below 2^31.
+uint32_t gemm_rows(uint32_t k) {
+    const uint64_t rows = ((1ull << 31) - 1) / ((uint64_t)k * 2);
+    return rows <= (uint64_t)kBM ? 0u : (uint32_t)std::min<uint64_t>((rows - kBM) / kBM * kBM, 0x80000000u);
+}
+
+stark_qmm_status launch_affine_gemm_rows(const AffineOp& op, int bits, hipStream_t stream);
+
 stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t stream) {
+    // products too tall for 32-bit offsets run as several launches of whole rows
+    const uint32_t R = gemm_rows(op.k);
+    if (R == 0) return STARK_QMM_UNSUPPORTED;
+    const size_t dsz = op.d_dt == STARK_QMM_F32 ? 4 : 2;
+    for (uint32_t m0 = 0; m0 < op.m; m0 += R) {
+        AffineOp part = op;
+        part.m = std::min(R, op.m - m0);
+        part.x = (const uint8_t*)op.x + (size_t)m0 * op.k * 2;
+        part.d = (uint8_t*)op.d + (size_t)m0 * op.n * dsz;
+        const stark_qmm_status st = launch_affine_gemm_rows(part, bits, stream);
+        if (st != STARK_QMM_OK) return st;
+    }
+    return STARK_QMM_OK;
+}
+
+stark_qmm_status launch_affine_gemm_rows(const AffineOp& op, int bits, hipStream_t stream) {
     const dim3 grid((op.n + kBN - 1) / kBN, (op.m + kBM - 1) / kBM);
     if (grid.x == 0 || grid.y == 0) return STARK_QMM_OK;
     const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;

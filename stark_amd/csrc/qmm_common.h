@@ -230,6 +230,7 @@ stark_qmm_status launch_affine_decode(const AffineOp* ops, uint32_t count, hipSt
 stark_qmm_status launch_affine_materialized(const AffineOp& op, hipStream_t stream);
 // Prefill dequant-GEMM on the matrix cores for M > 16 (qgemm_mfma.hip).
 bool gemm_eligible(const AffineOp& op, int bits);
+uint32_t gemm_rows(uint32_t k);  // activation rows one dequant-GEMM grid takes at K
 stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t stream);
 stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, int bits, hipStream_t stream);
 // Route adjustment with optional gains (moe.hip).

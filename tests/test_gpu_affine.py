@@ -695,3 +695,28 @@ def test_prefill_gemm_batch_plane_types_and_groups(qmm, oracle, w_dt, gs):
         want, mag = bf16_effective_reference(oracle, W, H.from_dev(x, np.uint16), m, n, kk, bits, gs, layout, corr,
                                              w_dt, signed)
         check(got, want.ravel(), mag=mag.ravel(), label=f"batched gemm gs{gs} m{m} n{n} k{kk} b{bits}")
+
+
+def test_prefill_gemm_split_into_row_launches(qmm, oracle):
+    """A product too tall for one grid's 32-bit offsets (K = 12288: 87040 rows
+    per grid) runs as launches of whole rows: rows on both sides of the split
+    against the bf16-effective f64 product, the D-ops on the second part."""
+    m, n, k = 87040 + 300, 136, 12288
+    rng = np.random.default_rng(87)
+    W = H.affine_weights(oracle, rng, n, k, 4, 64, 1, 1, H.BF16)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(87)
+    x = torch.randn(m * k, generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    prior = torch.randn(m * n, generator=gen, device="cuda")
+    d = prior.clone()
+    qmm.MatmulKernel(H.BF16, H.BF16, H.F32).encode(qmm.MatmulArguments(
+        a=x, m=m, n=n, k=k, d=d, b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                                                  params=qmm.QuantParams(1, n, k // 64), mode=qmm.MODE_U4,
+                                                  correction_data=H.to_dev(W["corr"])),
+        d_transform=qmm.MatmulDOps(accumulate=True)))
+    torch.cuda.synchronize()
+    rows = np.array([0, 87039, 87040, 87041, m - 1])
+    xs = x.view(m, k)[torch.from_numpy(rows).cuda()].cpu().numpy().view(np.uint16).ravel()
+    want, mag = bf16_effective_reference(oracle, W, xs, len(rows), n, k, 4, 64, 1, 1, H.BF16, False)
+    got = d.view(m, n)[torch.from_numpy(rows).cuda()].cpu().numpy() - prior.view(m, n)[torch.from_numpy(rows).cuda()].cpu().numpy()
+    check(got.ravel(), want.ravel(), mag=mag.ravel() + 4.0, label="row-split gemm")
