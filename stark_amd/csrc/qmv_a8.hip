@@ -549,6 +549,27 @@ stark_qmm_status launch_affine_a8_gemm_group(const AffineOp* ops, const A8Operan
 
 stark_qmm_status launch_affine_a8(const AffineOp& op, const A8Operand& a, int bits, hipStream_t stream) {
     if (op.m == 0 || op.n == 0) return STARK_QMM_OK;
+    // a product too tall for one grid's 32-bit offsets: launches of whole rows
+    // (the activation codes, their scales and d advanced per part)
+    if (op.m > 16 && op.k > 0 && (uint64_t)op.m * op.k >= (1ull << 31)) {
+        const uint64_t fit = ((1ull << 31) - 1) / op.k;
+        const uint32_t R = fit > (uint64_t)kGB ? (uint32_t)((fit - kGB) / kGB * kGB) : 0u;
+        AffineOp part = op;
+        A8Operand pa = a;
+        part.m = R;
+        if (R > 16 && a8_gemm_eligible(part, a, bits)) {
+            const size_t dsz = op.d_dt == STARK_QMM_F32 ? 4 : 2;
+            for (uint32_t m0 = 0; m0 < op.m; m0 += R) {
+                part.m = std::min(R, op.m - m0);
+                part.d = (uint8_t*)op.d + (size_t)m0 * op.n * dsz;
+                pa.codes = a.codes + (size_t)m0 * op.k;
+                pa.scales = a.scales + (size_t)m0 * (op.k / a.group);
+                const stark_qmm_status st = launch_affine_a8(part, pa, bits, stream);
+                if (st != STARK_QMM_OK) return st;
+            }
+            return STARK_QMM_OK;
+        }
+    }
     // prefill sizes: the int8 GEMM on the matrix cores
     if (a8_gemm_eligible(op, a, bits)) {
         const bool g32 = a.group == 32 || op.group_size == 32;

@@ -493,3 +493,37 @@ def test_a8_prefill_batch_matches_single(qmm, oracle):
     for a, b, t in zip(many, single, made):
         assert torch.equal(a.d, b.d), f"batched and single differ for m={t[0]} n={t[1]} k={t[2]} bits={t[3]}"
     assert any(bool((a.d != 0).any()) for a in many)
+
+
+def test_a8_prefill_split_into_row_launches(qmm, oracle):
+    """An int8-activation product too tall for one grid's 32-bit offsets
+    (K = 12288: 174592 rows per grid) runs as launches of whole rows; rows on
+    both sides of the split against the oracle."""
+    m, n, k, ag, wg = 174592 + 300, 64, 12288, 128, 64
+    rng = np.random.default_rng(174)
+    w = H.affine_weights(oracle, rng, n, k, bits=4, gs=wg)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(174)
+    q = torch.randint(-127, 128, (m * k,), generator=gen, device="cuda", dtype=torch.int8)
+    sc = torch.rand(m * k // ag, generator=gen, device="cuda") * 0.02 + 1e-3
+    d = _dev_empty(m * n, torch.float32)
+    b = qmm.QuantizedB(codes=H.to_dev(w["codes"]), scales=H.to_dev(w["scales"]),
+                       params=qmm.QuantParams(layout=0, row_count=n, group_count=k // wg), mode=qmm.MODE_U4,
+                       group_size=wg, correction=qmm.BIASES, correction_data=H.to_dev(w["corr"]))
+    A = qmm.Int8SymmetricA(values=q, scales=sc, scale_group_size=ag, code_layout=qmm.SEQUENTIAL)
+    qmm.MatmulKernel(BF16, BF16, F32).encode(qmm.MatmulArguments(a=A, b=b, d=d, m=m, n=n, k=k))
+    torch.cuda.synchronize()
+    rows = np.array([0, 174591, 174592, m - 1])
+    ri = torch.from_numpy(rows).cuda()
+    qs = q.view(m, k)[ri].cpu().numpy().ravel()
+    ss = sc.view(m, k // ag)[ri].cpu().numpy().ravel()
+    got = d.view(m, n)[ri].cpu().numpy().ravel()
+    st, want = oracle.matmul(a=np.zeros(len(rows) * k, np.uint16), m=len(rows), n=n, k=k, codes=w["codes"],
+                             scales=w["scales"], correction=1, correction_data=w["corr"], layout=0, row_count=n,
+                             group_count=k // wg, bits=4, group_size=wg, output_dt=F32, a_codes=qs, a_scales=ss,
+                             a_scale_group_size=ag, a_grouped_by_nibble=False, threads=8)
+    assert st == 0
+    xf = (qs.astype(np.float32).reshape(len(rows), k) * np.repeat(ss.reshape(len(rows), k // ag), ag, axis=1))
+    mag = H.dequant_magnitude(oracle, w["codes"], w["scales"], w["corr"], n, k, 4, wg, 0, 1, BF16,
+                              xf.astype(np.float32).ravel(), F32, len(rows))
+    check(got, want, mag=mag, label="row-split a8 gemm")
