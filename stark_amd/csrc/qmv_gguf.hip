@@ -127,7 +127,9 @@ struct GGeo {
     static constexpr int SEGB = BPW * BB;               // bytes of a row per wave per pass
     static constexpr int PPR = SEGB / 16;               // 16-byte pieces per row
     static constexpr int NI = (kRows * PPR + 63) / 64;  // loads per lane
-    static constexpr int ROWB = SEGB + 16;              // padded LDS row
+    // LDS row: an odd number of 16-byte chunks, so that 8 rows read at one
+    // offset (a column of the code tile) fall on 8 distinct groups of 4 banks
+    static constexpr int ROWB = (SEGB / 16) % 2 ? SEGB : SEGB + 16;
     static constexpr int NSTEP = Q / kStep;
     static constexpr int GPP = PASS / GS, GPW = Q / GS;
     static constexpr int GX = DENSE ? GPP : GPP + S;    // group entries of the LDS tables
