@@ -24,8 +24,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Tiles of BM rows (256: eight waves; 128: four waves, for products of at
+// most 128 rows) x kBN columns; kBM is the taller of the two.
 constexpr int kBM = 256, kBN = 128, kBK = 64;
-constexpr int kThreads = 512;
 
 // LDS tiles: rows of 64 bf16 (128 bytes, 8 chunks of 16 bytes), chunk c of
 // row r stored at chunk c ^ (r & 7). Every access here moves 16 bytes per
@@ -34,8 +35,9 @@ constexpr int kThreads = 512;
 // and the dequantised W stores (4 rows x 2 chunks). (Measured against
 // c ^ ((r >> 1) & 7), which spreads 16 lanes over 64 banks: 611 vs 604
 // TFLOP/s on the Qwen3-8B prefill set; 144-byte padded rows: 597.)
+template <int BM>
 struct GemmLds {
-    u32x4 a[2][kBM][kBK / 8];
+    u32x4 a[2][BM][kBK / 8];
     u32x4 b[2][kBN][kBK / 8];
 };
 __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) { return c ^ (r & 7); }
@@ -46,13 +48,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p, uint6
 
 // Output tile (bx, by) of one product: columns 128 bx.., rows 256 by...
 // BITS: 4 or 8. CORR: 0 symmetric, 1 biases. BF: bf16 (else f16) planes.
-template <int BITS, int CORR, bool SIGNED, bool BF>
+template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
 __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint32_t by) {
-    __shared__ GemmLds lds;
+    constexpr int kThreads = 2 * BM;
+    __shared__ GemmLds<BM> lds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t M = op.m, N = op.n, K = op.k;
-    const uint32_t m0 = by * kBM, n0 = bx * kBN;
+    const uint32_t m0 = by * BM, n0 = bx * kBN;
     const uint32_t row_bytes = K * BITS / 8;
 
     // ---- per-thread load assignment
@@ -62,9 +65,10 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     // tile's 256 rows: against 128x128 tiles of four waves (two workgroups per
     // CU), half the dequantisation per MFMA, 869-871 vs 792-795 TFLOP/s on the
     // Qwen3-8B prefill set.
-    constexpr int WPT = 16;        // codes per thread per pass
-    constexpr int TPR = kBK / WPT;                  // threads per row
-    constexpr int WPASS = 1;  // passes over the rows
+    constexpr int CB = kBN * kBK * BITS / 8 / kThreads;  // code bytes per thread
+    constexpr int WPT = (CB > 16 ? 16 : CB) * 8 / BITS;  // codes per thread per pass
+    constexpr int TPR = kBK / WPT;                       // threads per row
+    constexpr int WPASS = CB > 16 ? CB / 16 : 1;         // passes over the rows
     constexpr int WW = WPT * BITS / 32;  // code words per thread
     struct Stage {
         u32x4 xa[4];
@@ -237,7 +241,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     // Full tiles with a plain bf16 store (no D-op past ab_scale): one row
     // pointer per (i, e), the column blocks at fixed offsets from it.
     if (!(op.flags & (FLAG_ACCUMULATE | FLAG_SOFT_CAP)) && !op.bias && op.d_dt == STARK_QMM_BF16 &&
-        m0 + kBM <= M && n0 + kBN <= N) {
+        m0 + BM <= M && n0 + kBN <= N) {
         uint16_t* const d = (uint16_t*)op.d;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -268,13 +272,13 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
             }
 }
 
-template <int BITS, int CORR, bool SIGNED, bool BF>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
-    gemm_tile<BITS, CORR, SIGNED, BF>(op, blockIdx.x, blockIdx.y);
+template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
+__global__ __launch_bounds__(2 * BM) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
+    gemm_tile<BITS, CORR, SIGNED, BF, BM>(op, blockIdx.x, blockIdx.y);
 }
 
-__host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o) {
-    return ((o.n + kBN - 1) / kBN) * ((o.m + kBM - 1) / kBM);
+__host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o, uint32_t bm) {
+    return ((o.n + kBN - 1) / kBN) * ((o.m + bm - 1) / bm);
 }
 
 // Several products in one grid (ops of one template class): the tiles of op
@@ -282,19 +286,19 @@ __host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o) {
 // block), so that the column blocks that share a weight tile keep one XCD
 // while the op's column-block count is a multiple of 8. Ops come longest K
 // first, so the costliest tiles are dispatched first.
-template <int BITS, int CORR, bool SIGNED, bool BF>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
+template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
+__global__ __launch_bounds__(2 * BM) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
     (void)batch;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
     uint32_t t = blockIdx.x, i = 0;
     for (; i + 1 < kb->count; ++i) {
-        const uint32_t nt = gemm_tiles(kb->op[i]);
+        const uint32_t nt = gemm_tiles(kb->op[i], BM);
         if (t < nt) break;
         t -= nt;
     }
     const AffineOp& op = kb->op[i];
     const uint32_t gx = (op.n + kBN - 1) / kBN;
-    gemm_tile<BITS, CORR, SIGNED, BF>(op, t % gx, t / gx);
+    gemm_tile<BITS, CORR, SIGNED, BF, BM>(op, t % gx, t / gx);
 }
 
 }  // namespace
@@ -338,11 +342,18 @@ stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t st
 }
 
 stark_qmm_status launch_affine_gemm_rows(const AffineOp& op, int bits, hipStream_t stream) {
-    const dim3 grid((op.n + kBN - 1) / kBN, (op.m + kBM - 1) / kBM);
+    // products of at most 128 rows take 128-row tiles of four waves (half
+    // the idle rows of a 256-row tile)
+    const uint32_t bm = op.m <= 128 ? 128 : 256;
+    const dim3 grid((op.n + kBN - 1) / kBN, (op.m + bm - 1) / bm);
     if (grid.x == 0 || grid.y == 0) return STARK_QMM_OK;
     const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     const bool bf = op.w_dt == STARK_QMM_BF16;
-#define QMM_G(B, C, S, F) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F>), grid, dim3(kThreads), 0, stream, op)
+#define QMM_G(B, C, S, F)                                                                        \
+    do {                                                                                         \
+        if (bm == 128) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 128>), grid, dim3(256), 0, stream, op); \
+        else hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 256>), grid, dim3(512), 0, stream, op);          \
+    } while (0)
 #define QMM_G_BITS(B)                                                      \
     if (bi) {                                                              \
         if (sg) { if (bf) QMM_G(B, 1, true, true); else QMM_G(B, 1, true, false); } \
@@ -375,10 +386,13 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
     std::vector<AffineOp> sorted(ops, ops + count);
     std::stable_sort(sorted.begin(), sorted.end(), [](const AffineOp& a, const AffineOp& b) { return a.k > b.k; });
     AffineBatch batch{};
+    uint32_t mmax = 0;
+    for (uint32_t i = 0; i < count; ++i) mmax = std::max(mmax, sorted[i].m);
+    const uint32_t bm = mmax <= 128 ? 128 : 256;  // as launch_affine_gemm_rows
     uint64_t tiles = 0;
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = sorted[i];
-        tiles += gemm_tiles(sorted[i]);
+        tiles += gemm_tiles(sorted[i], bm);
     }
     batch.count = count;
     batch.total = (uint32_t)tiles;
@@ -388,7 +402,11 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
     const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     const bool bf = op.w_dt == STARK_QMM_BF16;
     const dim3 grid((uint32_t)tiles);
-#define QMM_GG(B, C, S, F) hipLaunchKernelGGL((qgemm_group<B, C, S, F>), grid, dim3(kThreads), 0, stream, batch)
+#define QMM_GG(B, C, S, F)                                                                          \
+    do {                                                                                            \
+        if (bm == 128) hipLaunchKernelGGL((qgemm_group<B, C, S, F, 128>), grid, dim3(256), 0, stream, batch); \
+        else hipLaunchKernelGGL((qgemm_group<B, C, S, F, 256>), grid, dim3(512), 0, stream, batch);          \
+    } while (0)
 #define QMM_GG_BITS(B)                                                                 \
     if (bi) {                                                                          \
         if (sg) { if (bf) QMM_GG(B, 1, true, true); else QMM_GG(B, 1, true, false); } \
