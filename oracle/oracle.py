@@ -75,6 +75,7 @@ def _declare(l):
         "so_scale_min": (None, [vp, i32, vp, vp]),
         "so_decode_block": (i32, [u32, vp, sz, vp, sz]),
         "so_hybrid_packed_matvec": (i32, [u32, vp, sz, sz, vp, vp]),
+        "so_decode_rows": (i32, [u32, vp, sz, sz, vp]),
         "so_hybrid_affine_matvec": (i32, [vp, vp, vp, i32, i32, sz, sz, sz, vp, vp]),
         "so_moe_route": (None, [vp, vp, vp, u32, u32, u32, u32, u32]),
         "so_moe_gather_rows": (None, [vp, vp, u32, u32, u32, u32]),
@@ -369,12 +370,14 @@ def decode_block(kind: int, block_bytes) -> np.ndarray:
 
 
 def decode_rows(kind: int, data, rows: int, cols: int) -> np.ndarray:
+    """decode_block over every block of `rows` rows of `cols` values."""
     e, bb = block_layout(kind)
-    data = np.ascontiguousarray(data, np.uint8).reshape(rows, cols // e * bb)
+    data = np.ascontiguousarray(data, np.uint8)
+    if data.size != rows * (cols // e) * bb or cols % e:
+        raise ValueError("data does not hold rows x cols values")
     out = np.zeros((rows, cols), np.float32)
-    for r in range(rows):
-        for b in range(cols // e):
-            out[r, b * e:(b + 1) * e] = decode_block(kind, data[r, b * bb:(b + 1) * bb])
+    if lib().so_decode_rows(kind, _p(data), rows, cols, _p(out)):
+        raise ValueError("invalid quantization block")
     return out
 
 

@@ -641,6 +641,21 @@ int so_decode_block(uint32_t kind, const uint8_t* bytes, size_t nbytes, float* o
 
 /* weights.rs:2533-2550: decode_values for one row, then
  * `values.iter().zip(input).map(|(w, x)| w * x).sum()` (a left fold from -0.0). */
+/* decode_block over whole rows of blocks (test helper: the dequantised
+ * matrix for tolerance magnitudes); rows are independent, OpenMP over rows. */
+int so_decode_rows(uint32_t kind, const uint8_t* bytes, size_t rows, size_t columns, float* output) {
+    size_t be, bb;
+    if (so_block_layout(kind, &be, &bb) || columns % be) return 1;
+    size_t row_bytes = columns / be * bb;
+    int bad = 0;
+#pragma omp parallel for schedule(static) reduction(|:bad)
+    for (long r = 0; r < (long)rows; ++r)
+        for (size_t b = 0; b < columns / be; ++b)
+            bad |= so_decode_block(kind, bytes + (size_t)r * row_bytes + b * bb, bb,
+                                   output + (size_t)r * columns + b * be, be);
+    return bad ? 2 : 0;
+}
+
 int so_hybrid_packed_matvec(uint32_t kind, const uint8_t* bytes, size_t rows, size_t columns, const float* input,
                             float* output) {
     size_t be, bb;

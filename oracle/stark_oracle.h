@@ -151,6 +151,7 @@ int so_block_layout(uint32_t kind, size_t* elements, size_t* bytes);
 void so_scale_min(const uint8_t* scales, int index, uint8_t* scale, uint8_t* min);
 int so_decode_block(uint32_t kind, const uint8_t* bytes, size_t nbytes, float* output, size_t count);
 /* weights.rs:2533-2550: per row decode_values(...) . input, f32 sequential sum. */
+int so_decode_rows(uint32_t kind, const uint8_t* bytes, size_t rows, size_t columns, float* output);
 int so_hybrid_packed_matvec(uint32_t kind, const uint8_t* bytes, size_t rows, size_t columns, const float* input,
                             float* output);
 /* weights.rs:1284-1309 affine_row . input (OutputGroup [N,G] planes). */
