@@ -9,14 +9,17 @@
 // (ties: lower index), or u32::MAX when no finite logit is left.
 //
 // One workgroup of 1024 threads per row, in passes over the row (L2-resident):
-//  - the prefix kept by the filters is never sorted. Its length L is the
-//    minimum of top_k, the count of logits at or above max + ln(min_p), and
-//    for top-p the first prefix whose mass reaches p, found by a radix descent
-//    over the order-preserving 32-bit key of the logit with per-digit mass
-//    histograms. The masses are exp(x - max) in 2^-40 fixed point summed with
-//    integer atomics, so the result does not depend on thread timing; it
-//    differs from the reference's sequential f32 sum only in rounding, i.e.
-//    only where the prefix mass lands within about 1e-6 of p;
+//  - the prefix kept by the filters has length L, the minimum of top_k, the
+//    count of logits at or above max + ln(min_p), and for top-p the first
+//    prefix whose mass reaches p. Top-p follows the reference's f32 sums in
+//    its order: only terms exp(x - max) of at least 2^-27 can move them, and
+//    when at most 4096 logits carry such terms they are sorted in LDS and
+//    summed in order on one thread (exact_top_p_prefix). Rows with more
+//    significant terms (very flat rows) take a radix descent over the
+//    order-preserving key with per-digit mass histograms in 2^-40 fixed
+//    point (integer atomics: independent of thread timing), which differs
+//    from the sequential f32 sums only where the prefix mass lands within
+//    their rounding error of p;
 //  - the kept set, the first L logits in (value desc, index asc) order, is
 //    located by a second radix select over the key (and over the index among
 //    equal keys);
@@ -82,6 +85,18 @@ __device__ __forceinline__ float gumbel(uint64_t seed, uint32_t i, uint32_t voca
     return -logf(-logf(u));
 }
 
+// Top-p in the reference's order: terms of at least 2^-27 (times the maximum's)
+// sorted in LDS, at most kExactCap of them.
+constexpr int kExactCap = 4096;
+constexpr float kSignificant = 0x1p-27f;
+
+struct ExactLds {
+    unsigned long long key[kExactCap];  // fkey(x) << 32 | ~index: descending = (value desc, index asc)
+    float term[kExactCap];
+    float norm;
+    uint32_t n, len;
+};
+
 // order-preserving key of a non-NaN float (larger float -> larger key)
 __device__ __forceinline__ uint32_t fkey(float f) {
     const uint32_t b = __float_as_uint(f + 0.0f);
@@ -131,6 +146,77 @@ __device__ unsigned long long block_sum_u64(unsigned long long v, SampleLds& s) 
     atomicAdd(&s.acc64[0], v);
     __syncthreads();
     return s.acc64[0];
+}
+
+__device__ __forceinline__ float fkey_value(uint32_t k) {
+    return (k & 0x80000000u) ? __uint_as_float(k & 0x7fffffffu) : __uint_as_float(~k);
+}
+
+// Length of the top-p prefix as unified_sampling.rs:85-97 computes it: the
+// norm is the f32 sum of exp(x - max) over the logits sorted by value desc
+// (index asc), the mass adds exp(x - max) / norm in that order, and the prefix
+// ends before the first logit at which the mass has reached p. C is the count
+// of significant terms (see the caller); returns V when the mass never
+// reaches p.
+template <class ValueFn>
+__device__ uint32_t exact_top_p_prefix(const SampleArgs& a, ValueFn value, float F, uint32_t C, uint32_t V,
+                                       SampleLds& s) {
+    __shared__ ExactLds ex;
+    const uint32_t tid = threadIdx.x;
+    uint32_t N = 1;
+    while (N < C) N <<= 1;
+    __syncthreads();
+    if (tid == 0) ex.n = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < V; i += kST) {
+        const float x = value(i);
+        if (expf(x - F) >= kSignificant)
+            ex.key[atomicAdd(&ex.n, 1u)] = ((unsigned long long)fkey(x) << 32) | (0xffffffffu - i);
+    }
+    for (uint32_t j = C + tid; j < N; j += kST) ex.key[j] = 0;  // below every real key
+    __syncthreads();
+    // bitonic sort, descending
+    for (uint32_t k = 2; k <= N; k <<= 1)
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = tid; i < N; i += kST) {
+                const uint32_t o = i ^ j;
+                if (o > i) {
+                    const unsigned long long u = ex.key[i], w = ex.key[o];
+                    if ((i & k) == 0 ? u < w : u > w) {
+                        ex.key[i] = w;
+                        ex.key[o] = u;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    for (uint32_t r = tid; r < C; r += kST) ex.term[r] = expf(fkey_value((uint32_t)(ex.key[r] >> 32)) - F);
+    __syncthreads();
+    if (tid == 0) {
+        float norm = 0.0f;
+        for (uint32_t r = 0; r < C; ++r) norm += ex.term[r];
+        ex.norm = norm;
+    }
+    __syncthreads();
+    const float norm = ex.norm;
+    for (uint32_t r = tid; r < C; r += kST) ex.term[r] = ex.term[r] / norm;
+    __syncthreads();
+    if (tid == 0) {
+        float mass = 0.0f;
+        uint32_t len = V;
+        for (uint32_t r = 0; r < C; ++r) {
+            if (mass >= a.top_p) {
+                len = r;
+                break;
+            }
+            mass += ex.term[r];
+        }
+        if (len == V && mass >= a.top_p) len = C;
+        ex.len = len;
+    }
+    __syncthreads();
+    (void)s;
+    return ex.len;
 }
 
 __global__ __launch_bounds__(kST) void unified_sampling(SampleArgs a) {
@@ -190,58 +276,72 @@ __global__ __launch_bounds__(kST) void unified_sampling(SampleArgs a) {
         L = min(L, (uint32_t)block_sum_u64(c, s));
     }
     if (a.has_top_p && L > 1) {
-        const double kFix = 1099511627776.0;  // 2^40
-        const auto term = [&](float x) { return (unsigned long long)((double)expf(x - F) * kFix); };
-        unsigned long long z = 0;
-        for (uint32_t i = tid; i < V; i += kST) z += term(value(i));
-        const unsigned long long norm = block_sum_u64(z, s);
-        const unsigned long long target = (unsigned long long)ceil((double)a.top_p * (double)norm);
-        // radix descent: prefix of the key bits fixed so far, and the mass of
-        // every logit above the current bucket
-        uint32_t prefix = 0, pmask = 0;
-        unsigned long long above = 0;
-        bool found = false;
-        for (int shiftb = 24; shiftb >= 0; shiftb -= 8) {
-            __syncthreads();
-            if (tid < 256) s.hist[tid] = 0;
-            __syncthreads();
-            for (uint32_t i = tid; i < V; i += kST) {
-                const float x = value(i);
-                const uint32_t k = fkey(x);
-                if ((k & pmask) == prefix) atomicAdd(&s.hist[(k >> shiftb) & 255u], term(x));
-            }
-            __syncthreads();
-            if (tid == 0) {
-                uint32_t d = 256;
-                unsigned long long acc = above;
-                for (int b = 255; b >= 0; --b) {
-                    if (acc + s.hist[b] >= target) {
-                        d = (uint32_t)b;
-                        break;
-                    }
-                    acc += s.hist[b];
+        // Terms exp(x - max) below 2^-27 cannot move the reference's sequential
+        // f32 sums: the norm is at least 1 (the maximum's own term), and a
+        // running mass m is at least 1 / norm, so such a term (or its quotient
+        // by the norm) is below half an ulp of the running value and every
+        // later one is smaller still. When the terms at or above 2^-27 fit in
+        // LDS, they are sorted (value desc, index asc) and both sums run in the
+        // reference's order on one thread, which gives its prefix exactly.
+        uint32_t cnt = 0;
+        for (uint32_t i = tid; i < V; i += kST) cnt += expf(value(i) - F) >= kSignificant ? 1u : 0u;
+        const uint32_t C = (uint32_t)block_sum_u64(cnt, s);
+        if (C <= (uint32_t)kExactCap) {
+            L = min(L, exact_top_p_prefix(a, value, F, C, V, s));
+        } else {
+            const double kFix = 1099511627776.0;  // 2^40
+            const auto term = [&](float x) { return (unsigned long long)((double)expf(x - F) * kFix); };
+            unsigned long long z = 0;
+            for (uint32_t i = tid; i < V; i += kST) z += term(value(i));
+            const unsigned long long norm = block_sum_u64(z, s);
+            const unsigned long long target = (unsigned long long)ceil((double)a.top_p * (double)norm);
+            // radix descent: prefix of the key bits fixed so far, and the mass of
+            // every logit above the current bucket
+            uint32_t prefix = 0, pmask = 0;
+            unsigned long long above = 0;
+            bool found = false;
+            for (int shiftb = 24; shiftb >= 0; shiftb -= 8) {
+                __syncthreads();
+                if (tid < 256) s.hist[tid] = 0;
+                __syncthreads();
+                for (uint32_t i = tid; i < V; i += kST) {
+                    const float x = value(i);
+                    const uint32_t k = fkey(x);
+                    if ((k & pmask) == prefix) atomicAdd(&s.hist[(k >> shiftb) & 255u], term(x));
                 }
-                s.scal[0] = d;
-                s.acc64[1] = acc;
+                __syncthreads();
+                if (tid == 0) {
+                    uint32_t d = 256;
+                    unsigned long long acc = above;
+                    for (int b = 255; b >= 0; --b) {
+                        if (acc + s.hist[b] >= target) {
+                            d = (uint32_t)b;
+                            break;
+                        }
+                        acc += s.hist[b];
+                    }
+                    s.scal[0] = d;
+                    s.acc64[1] = acc;
+                }
+                __syncthreads();
+                const uint32_t d = s.scal[0];
+                if (d == 256) break;  // the whole row's mass stays below p: every logit is kept
+                above = s.acc64[1];
+                prefix |= d << shiftb;
+                pmask |= 255u << shiftb;
+                found = shiftb == 0;
             }
-            __syncthreads();
-            const uint32_t d = s.scal[0];
-            if (d == 256) break;  // the whole row's mass stays below p: every logit is kept
-            above = s.acc64[1];
-            prefix |= d << shiftb;
-            pmask |= 255u << shiftb;
-            found = shiftb == 0;
-        }
-        if (found) {
-            // logits with key == prefix all carry the same term t; the prefix
-            // ends at the first of them whose addition reaches the target
-            const float xk = (prefix & 0x80000000u) ? __uint_as_float(prefix & 0x7fffffffu) : __uint_as_float(~prefix);
-            const unsigned long long t = term(xk);
-            unsigned long long greater = 0;
-            for (uint32_t i = tid; i < V; i += kST) greater += fkey(value(i)) > prefix ? 1u : 0u;
-            greater = block_sum_u64(greater, s);
-            const unsigned long long need = t ? (target - above + t - 1) / t : 1ull;  // ties up to the crossing one
-            L = min(L, (uint32_t)min<unsigned long long>(greater + need, V));
+            if (found) {
+                // logits with key == prefix all carry the same term t; the prefix
+                // ends at the first of them whose addition reaches the target
+                const float xk = (prefix & 0x80000000u) ? __uint_as_float(prefix & 0x7fffffffu) : __uint_as_float(~prefix);
+                const unsigned long long t = term(xk);
+                unsigned long long greater = 0;
+                for (uint32_t i = tid; i < V; i += kST) greater += fkey(value(i)) > prefix ? 1u : 0u;
+                greater = block_sum_u64(greater, s);
+                const unsigned long long need = t ? (target - above + t - 1) / t : 1ull;  // ties up to the crossing one
+                L = min(L, (uint32_t)min<unsigned long long>(greater + need, V));
+            }
         }
     }
     L = max(L, 1u);

@@ -92,3 +92,47 @@ def test_non_finite_and_validation(qmm, oracle):
             qmm.unified_sampling(d, F32, 64, 1, m, seeds=torch.zeros(1, dtype=torch.int64, device="cuda"))
     with pytest.raises(qmm.MatmulError):
         qmm.unified_sampling(d, F32, 0, 1)
+
+
+def _ref_masses(x):
+    """The reference's running top-p masses (unified_sampling.rs:85-97) in f32:
+    mass[r] = sum over the first r sorted logits of exp(x - max) / norm."""
+    order = sorted(range(len(x)), key=lambda i: (-float(x[i]), i))
+    v = np.asarray(x, np.float32)[order]
+    t = np.exp(v - v[0]).astype(np.float32)
+    norm = np.float32(0)
+    for u in t:
+        norm = np.float32(norm + u)
+    mass, out = np.float32(0), [np.float32(0)]
+    for u in t:
+        mass = np.float32(mass + np.float32(u / norm))
+        out.append(mass)
+    return out
+
+
+def test_top_p_mass_on_the_boundary(qmm, oracle):
+    """Top-p where the reference's f32 prefix mass lands exactly on p (or one
+    f32 step from it): the kept prefix must be the reference's, so the
+    sampled tokens match over many seeds. Equal logits give terms of exactly 1
+    (3 logits with p = f32(2/3): the f32 mass after two is f32(2/3), which
+    stops there, while the exact mass 2/3 is below f32(2/3)); the random rows
+    take p as the reference's own mass after r logits and the next f32 above."""
+    rng = np.random.default_rng(77)
+    batch = 96
+    seeds = rng.integers(0, 2 ** 63, batch, dtype=np.uint64)
+    cases = [(np.zeros(3, np.float32), np.float32(2.0 / 3.0)),
+             (np.zeros(10, np.float32), np.float32(0.3)),
+             (np.zeros(10, np.float32), np.float32(0.7)),
+             (np.zeros(7, np.float32), np.float32(3.0 / 7.0))]
+    for v in (50, 3000):
+        x = rng.normal(0, 1.0, v).astype(np.float32)
+        masses = _ref_masses(x)
+        for r in (1, 2, 3):
+            cases.append((x, masses[r]))
+            cases.append((x, np.nextafter(masses[r], np.float32(2))))
+    for x, p in cases:
+        vocab = x.size
+        rows = np.tile(x, batch)
+        want = oracle.unified_sampling(rows, batch, vocab, seeds=seeds, top_p=float(p))
+        got = _run(qmm, rows, F32, vocab, batch, qmm.SamplingMethod(stochastic=True, top_p=float(p)), seeds, None)
+        assert np.array_equal(got, want), (vocab, float(p), got, want)
