@@ -22,7 +22,6 @@
 // a route; each output value of the matrix-core tile depends on its own
 // activation row alone.
 #include <cmath>
-#include <cstdlib>
 #include <mutex>
 
 #include "mfma_tile.h"
@@ -397,12 +396,18 @@ __global__ __launch_bounds__(kWg) void moe_route_up_one(GroupedLaunch launch, Ro
             rden = den;
         }
     }
-    // c. ranks: #{e' : key(e') > key(e)}
-    for (uint32_t e = tid; e < E; e += kWg) {
+    // c. ranks: #{e' : key(e') > key(e)}, eight consecutive lanes per expert
+    // over interleaved eighths of the keys (as moe_route_compact)
+    for (uint32_t it = tid; it < E * 8; it += kWg) {  // lane groups of 8 stay whole
+        const uint32_t qq = it & 7, e = it >> 3;
         const uint64_t k = keys[e];
         uint32_t rank = 0;
-        for (uint32_t f = 0; f < E; ++f) rank += keys[f] > k ? 1u : 0u;
-        if (rank < A) rid[rank] = e;
+#pragma unroll 4
+        for (uint32_t f = qq; f < E; f += 8) rank += keys[f] > k ? 1u : 0u;
+        rank += __shfl_xor(rank, 1, 64);
+        rank += __shfl_xor(rank, 2, 64);
+        rank += __shfl_xor(rank, 4, 64);
+        if (qq == 0 && rank < A) rid[rank] = e;
     }
     __syncthreads();
     // d. weights in rank order, renormalised; gains and the stable id sort
@@ -463,15 +468,152 @@ __global__ void moe_accumulate_ranks(const uint16_t* proj, const float* weights,
     const uint32_t row = blockIdx.y, p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= model) return;
     float acc = 0.0f;
-    for (uint32_t rank = 0; rank < active; ++rank) {
-        const uint32_t route = row * active + rank;
-        float product = bf16_bits_to_f32(proj[(size_t)route * model + p]) * weights[route];
-        if (round_product) product = bf16_bits_to_f32(f32_to_bf16_bits(product));
-        float value = (rank == 0 ? 0.0f : acc) + product;
-        if (round_accumulator) value = bf16_bits_to_f32(f32_to_bf16_bits(value));
-        acc = value;
+    // the operands of 8 ranks are loaded together, then added in rank order
+    for (uint32_t r0 = 0; r0 < active; r0 += 8) {
+        float pv[8], wv[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t route = row * active + min(r0 + j, active - 1);
+            pv[j] = bf16_bits_to_f32(proj[(size_t)route * model + p]);
+            wv[j] = weights[route];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t rank = r0 + j;
+            if (rank >= active) break;
+            float product = pv[j] * wv[j];
+            if (round_product) product = bf16_bits_to_f32(f32_to_bf16_bits(product));
+            float value = (rank == 0 ? 0.0f : acc) + product;
+            if (round_accumulator) value = bf16_bits_to_f32(f32_to_bf16_bits(value));
+            acc = value;
+        }
     }
     output[(size_t)row * model + p] = f32_to_bf16_bits(acc);
+}
+
+// ---- 4+5 fused for one token: the down products of the token's routes and
+// their accumulation in rank order, one workgroup per 16 output rows and one
+// wave per route (rank). The wave stages its route's activation row in LDS
+// (loaded before the expert id is known); lane (row r = lane / 4, quarter
+// q = lane % 4) loads its quarter of the route's expert row (NL 16-byte
+// pieces, whole groups), sums x*q and x per group on v_dot2 (products
+// exact) and adds s * sum(x q) + bias_term * sum(x); the quarters meet by two
+// shuffles in a fixed order, the route's product is rounded to bf16 as the
+// reference's down product writes it, and 16 threads accumulate the routes in
+// rank order with the reference's rounding switches (moe.rs:109-145), as
+// moe_accumulate_ranks does. This takes the down launch's 8 x (model / 16)
+// one-route items and the accumulation launch off the one-token chain.
+struct DownAccArgs {
+    const uint8_t* codes;    // down bank [E * model, H / 2]
+    const uint16_t* scales;  // bf16 planes
+    const uint16_t* corr;    // bf16 bias plane, or null (symmetric: bias_term = -8 s)
+    uint32_t os, gs;         // plane strides (elements)
+    const uint16_t* act;     // [A, H] bf16, rank r at r * H
+    const uint32_t* ids;     // [A] expert of each rank
+    const float* weights;    // [A]
+    uint16_t* out;           // [model] bf16
+    uint32_t model, hidden, experts, active, signed_codes, round_product, round_accumulator;
+};
+
+template <int NL, int GS>
+__global__ __launch_bounds__(512) void moe_down_acc_one(DownAccArgs a) {
+    constexpr int KQ = NL * 32;   // k values of a lane's quarter of the row (H / 4)
+    constexpr int GPL = KQ / GS;  // whole groups per lane
+    constexpr int XV = KQ / 2;    // 16-byte activation vectors of a row (H / 8)
+    static_assert(KQ % GS == 0, "a lane's quarter holds whole groups");
+    __shared__ float proj[8][16];
+    __shared__ float rw[8];
+    __shared__ u32x4 xs[8][XV];  // each wave's activation row
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t H = a.hidden, n0 = blockIdx.x * 16, r = lane >> 2, q = lane & 3;
+    // first the loads that need no route: the wave's activation row and the
+    // route weights (the codes' addresses wait for the expert id)
+    const bool live = w < a.active;
+    const u32x4* xg = (const u32x4*)(a.act + (size_t)min(w, a.active - 1) * H);
+    u32x4 x0 = live && lane < (uint32_t)XV ? xg[lane] : u32x4{0, 0, 0, 0};
+    u32x4 x1 = live && lane + 64 < (uint32_t)XV ? xg[lane + 64] : u32x4{0, 0, 0, 0};
+    const float wt = tid < a.active ? a.weights[tid] : 0.0f;
+    if (live) {
+        uint32_t e = a.ids[w];
+        e = e < a.experts ? e : 0u;  // out-of-range ids read expert 0's rows (moe.rs:87-107)
+        const size_t row = (size_t)e * a.model + n0 + r;
+        const u32x4* cp = (const u32x4*)(a.codes + row * (H / 2) + q * (KQ / 2));
+        u32x4 c[NL];
+#pragma unroll
+        for (int j = 0; j < NL; ++j) c[j] = cp[j];
+        float sc[GPL], bi[GPL];
+#pragma unroll
+        for (int g = 0; g < GPL; ++g) {
+            const size_t idx = row * a.os + (size_t)(q * GPL + g) * a.gs;
+            sc[g] = bf16_bits_to_f32(a.scales[idx]);
+            bi[g] = a.corr ? bf16_bits_to_f32(a.corr[idx]) : -8.0f * sc[g];
+        }
+        if (lane < (uint32_t)XV) xs[w][lane] = x0;
+        if (lane + 64 < (uint32_t)XV) xs[w][lane + 64] = x1;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        const u32x4* xw = xs[w] + q * (KQ / 8);
+        const uint32_t flip = a.signed_codes ? 0x88888888u : 0u;
+        float acc = 0.0f;
+#pragma unroll
+        for (int g = 0; g < GPL; ++g) {
+            float sq = 0.0f, sa = 0.0f;
+#pragma unroll
+            for (int j = g * (GS / 32); j < (g + 1) * (GS / 32); ++j)  // 16-byte pieces of the group
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {  // 8 codes, k = 32 j + 8 t + i (low nibble first)
+                    const uint32_t cw = c[j][t] ^ flip;
+                    const uint32_t ev = cw & 0x0F0F0F0Fu, od = (cw >> 4) & 0x0F0F0F0Fu;
+                    const u32x4 xv = xw[4 * j + t];  // bf16 pairs (x0, x1) (x2, x3) ..
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const float qe = (float)((ev >> (8 * b)) & 255u), qo = (float)((od >> (8 * b)) & 255u);
+                        const uint32_t qp = perm(__float_as_uint(qo), __float_as_uint(qe), 0x07060302u);
+                        sq = dot2_bf16(xv[b], qp, sq);
+                        sa = dot2_bf16(xv[b], 0x3F803F80u, sa);
+                    }
+                }
+            acc = fmaf(sc[g], sq, fmaf(bi[g], sa, acc));
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        if (q == 0) proj[w][r] = bf16_bits_to_f32(f32_to_bf16_bits(acc));
+    }
+    if (tid < a.active) rw[tid] = wt;
+    __syncthreads();
+    if (tid < 16 && n0 + tid < a.model) {
+        float acc = 0.0f;
+        for (uint32_t rank = 0; rank < a.active; ++rank) {
+            float product = proj[rank][tid] * rw[rank];
+            if (a.round_product) product = bf16_bits_to_f32(f32_to_bf16_bits(product));
+            float value = (rank == 0 ? 0.0f : acc) + product;
+            if (a.round_accumulator) value = bf16_bits_to_f32(f32_to_bf16_bits(value));
+            acc = value;
+        }
+        a.out[n0 + tid] = f32_to_bf16_bits(acc);
+    }
+}
+
+// The fused one-token down kernel for (H, group size), or null when the
+// shape is outside it (H / 128 pieces per lane in {2, 4, 6, 8}, whole
+// groups per lane).
+void* pick_down_acc_one(uint32_t H, uint32_t gs) {
+#define QMM_DA(NL)                                                             \
+    case NL:                                                                   \
+        if (gs == 32) return (void*)&moe_down_acc_one<NL, 32>;                 \
+        if (gs == 64 && (NL * 32) % 64 == 0) return (void*)&moe_down_acc_one<NL, (NL * 32) % 64 == 0 ? 64 : 32>; \
+        if (gs == 128 && (NL * 32) % 128 == 0) return (void*)&moe_down_acc_one<NL, (NL * 32) % 128 == 0 ? 128 : 32>; \
+        return nullptr;
+    if (H % 128) return nullptr;
+    switch (H / 128) {
+        QMM_DA(2)
+        QMM_DA(4)
+        QMM_DA(6)
+        QMM_DA(8)
+    default: return nullptr;
+    }
+#undef QMM_DA
 }
 
 #define QMM_GROUPED_KERNEL(NAME)                                  \
@@ -632,10 +774,7 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
     const uint64_t nkeys = (uint64_t)R * E;
     const bool sg = a->up.signed_codes != 0;
     // one token: route, slots and the up product in one launch
-    // (STARK_QMM_SEPARATE_ROUTE=1 in the environment keeps the separate route
-    // launch: a diagnostic, and the tests' way to compare the two paths)
-    const char* sep = std::getenv("STARK_QMM_SEPARATE_ROUTE");
-    const bool one = R == 1 && E <= kOneTokenExperts && !(sep && sep[0] == '1');
+    const bool one = R == 1 && E <= kOneTokenExperts;
     if (one) {
         RouteOneArgs ra{a->router_logits, a->expert_scales, E, A, a->round_weights_bf16, a->round_logits_bf16,
                         (uint32_t)adjust, sort, ids, weights, table, header};
@@ -671,7 +810,9 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
     // 3./4. grouped products, one launch per route-count class in use (the
     // one-token path has run the up product already)
     const int top = (int)count_class(max_count);
-    for (int pass = one ? 1 : 0; pass < 2; ++pass) {
+    // one token: the down products and the rank accumulation in one launch
+    void* down_acc = R == 1 && A <= 8 && model % 16 == 0 ? pick_down_acc_one(H, a->down.group_size) : nullptr;
+    for (int pass = one ? 1 : 0; pass < (down_acc ? 1 : 2); ++pass) {
         GroupedLaunch g{};
         const bool up = pass == 0;
         g.op = up ? bank_op(a->up, E * 2 * H, model, a->input) : bank_op(a->down, E * model, H, act);
@@ -693,6 +834,18 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
             void* argv[] = {&g};
             QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(grid), dim3(kWg), argv, 0, stream));
         }
+    }
+    if (down_acc) {
+        const AffineOp d = bank_op(a->down, E * model, H, act);
+        DownAccArgs da{(const uint8_t*)a->down.codes,
+                       (const uint16_t*)a->down.scales,
+                       a->down.correction == STARK_QMM_CORRECTION_BIASES ? (const uint16_t*)a->down.correction_data
+                                                                         : nullptr,
+                       d.os, d.gs, act, ids, weights, (uint16_t*)a->output, model, H, E, A,
+                       a->down.signed_codes ? 1u : 0u, a->round_products_bf16, a->round_accumulator_bf16};
+        void* argv[] = {&da};
+        QMM_HIP_CHECK(hipLaunchKernel(down_acc, dim3(model / 16), dim3(64 * A), argv, 0, stream));
+        return STARK_QMM_OK;
     }
     // 5. accumulate ranks in order
     hipLaunchKernelGGL(moe_accumulate_ranks, dim3((model + 255) / 256, R), dim3(256), 0, stream, proj, weights,

@@ -54,3 +54,48 @@ def test_static_rejects_workspace_beyond_scratch(qmm, oracle):
     with pytest.raises(qmm.MatmulError) as e:
         qmm.routed_experts_static(x, lg, up, down, rows, model, hidden, experts, active, output=out)
     assert e.value.status == qmm.WORKSPACE_TOO_SMALL
+
+
+def test_static_one_token_matches(qmm, oracle):
+    """One token at the Qwen3-30B-A3B geometry: the fused route + up launch
+    and the fused down + accumulation launch, on the static scratch."""
+    c = MC.case(oracle, 74, 1, model=2048, hidden=768, experts=128, active=8)
+    got, want = _both(qmm, c)
+    assert np.array_equal(got, want), f"{int((got != want).sum())} outputs differ"
+
+
+def test_static_under_graph_capture(qmm, oracle):
+    """The allocation-free entry point recorded in a HIP graph: every replay
+    with new inputs copied into the captured buffers equals an eager call of
+    the workspace entry point on those inputs, with eager work and
+    synchronizations between the replays."""
+    R, M, Hd, E, A = 1, 2048, 768, 128, 8
+    base = MC.case(oracle, 75, R, model=M, hidden=Hd, experts=E, active=A)
+    up, down = _banks(qmm, base)
+    x = H.to_dev(base["x"])
+    lg = H.to_dev(base["logits"])
+    out = torch.empty(R * M, dtype=torch.bfloat16, device="cuda")
+    qmm.routed_experts_static(x, lg, up, down, R, M, Hd, E, A, output=out)  # eager first call
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            qmm.routed_experts_static(x, lg, up, down, R, M, Hd, E, A, output=out, stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(76)
+    for rep in range(4):
+        nx = oracle.f32_to_bf16(rng.normal(0, 1, R * M).astype(np.float32))
+        nl = rng.normal(0, 2, R * E).astype(np.float32)
+        x.copy_(H.to_dev(nx))
+        lg.copy_(H.to_dev(nl))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.view(torch.int16).cpu().numpy().copy()
+        want = qmm.routed_experts(H.to_dev(nx), H.to_dev(nl), up, down, R, M, Hd, E, A)
+        torch.cuda.synchronize()
+        want = want.view(torch.int16).cpu().numpy()
+        assert np.array_equal(got, want), f"replay {rep}: {int((got != want).sum())} outputs differ"
