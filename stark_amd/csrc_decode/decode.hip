@@ -62,6 +62,33 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave reductions on DPP (quad_perm xor 1 and xor 2, half-row and row
+// mirrors: every lane of a 16-lane row holds the row's value) and the four
+// rows read into scalars, added as (r0 + r1) + (r2 + r3): a chain of VALU
+// operations instead of six LDS-pipe shuffles. The RMS norm keeps the xor
+// butterfly above, whose order the products' RMS-norm prologue repeats.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f32(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -140,7 +167,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(uint16_t* q, const uin
     const uint16_t* src = is_q ? q + (size_t)h * kHd : k + (size_t)(h - qh) * kHd;
     const uint16_t* w = is_q ? qw : kw;
     const float a = bf(src[i]), b = bf(src[i + 64]);
-    const float inv = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)kHd + eps);
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(a * a + b * b) / (float)kHd + eps);
     const float na = bf(to_bf(bf(to_bf(a * inv)) * bf(w[i])));
     const float nb = bf(to_bf(bf(to_bf(b * inv)) * bf(w[i + 64])));
     float sn, cs;
@@ -224,9 +251,9 @@ __global__ __launch_bounds__(64 * G) void attn_partial_kernel(const uint16_t* q,
         }
         s = acc * scale;
     }
-    const float m = wave_max(s);
+    const float m = wave_max_dpp(s);
     const float e = lane < np ? __expf(s - m) : 0.0f;
-    const float l = wave_sum(e);
+    const float l = wave_sum_dpp(e);
     ws[h][lane] = e;
     __syncthreads();
     // PV: lane = dims 2*lane, 2*lane + 1
@@ -267,7 +294,7 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
     const uint32_t nc = min(nchunks, (len + kChunk - 1) / kChunk);
     float mx = d < nc ? ml0.x : -INFINITY;
     for (uint32_t c = d + 128; c < nc; c += 128) mx = fmaxf(mx, ml[c].x);
-    mx = wave_max(mx);
+    mx = wave_max_dpp(mx);
     if ((d & 63) == 0) red[d >> 6] = mx;
     __syncthreads();
     const float m = fmaxf(red[0], red[1]);
@@ -279,7 +306,7 @@ __global__ __launch_bounds__(128) void attn_reduce_kernel(const float* po, const
         fs[c] = f;
         l = fmaf(v.y, f, l);
     }
-    l = wave_sum(l);
+    l = wave_sum_dpp(l);
     if ((d & 63) == 0) red[d >> 6] = l;
     __syncthreads();
     l = red[0] + red[1];
@@ -307,147 +334,238 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-__device__ __forceinline__ void norm_rope_pair(float a, float b, const uint16_t* w, uint32_t i, int32_t pos,
+__device__ __forceinline__ void norm_rope_pair(float a, float b, uint16_t wa, uint16_t wb, uint32_t i, int32_t pos,
                                                const RopeTable& rope, float eps, uint16_t& ra, uint16_t& rb) {
-    const float inv = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)kHd + eps);
-    const float na = bf(to_bf(bf(to_bf(a * inv)) * bf(w[i])));
-    const float nb = bf(to_bf(bf(to_bf(b * inv)) * bf(w[i + 64])));
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(a * a + b * b) / (float)kHd + eps);
+    const float na = bf(to_bf(bf(to_bf(a * inv)) * bf(wa)));
+    const float nb = bf(to_bf(bf(to_bf(b * inv)) * bf(wb)));
     float sn, cs;
     rope_sincos(rope, i, pos, sn, cs);
     ra = to_bf(na * cs - nb * sn);
     rb = to_bf(nb * cs + na * sn);
 }
 
-// Attention of one decode step with the q/k norm + RoPE + KV write and the
-// chunk reduction folded in: workgroup (kv head g, chunk c), 64*G threads,
-// wave h = query head h of the group.
-//  - every workgroup normalises and rotates its G query heads itself;
-//  - the workgroup whose chunk holds the new position builds that K row
-//    (norm + RoPE) and V row, uses them in place of the cache rows and writes
-//    them to the cache (later steps read them from there);
-//  - partial output, max and sum per chunk as attn_partial_kernel
-//    (attn_reduce_kernel combines the chunks; an in-kernel last-workgroup
-//    reduction needs a device-scope fence per workgroup, which writes back
-//    the XCD's L2 and costs more than the second launch).
+// Attention of one decode step with the q/k norm + RoPE + KV write folded
+// in: workgroup (kv head g, chunk c) of four waves, for the G query heads of
+// the group.
+//  - Registers, not LDS, hold the chunk's K and V: lane l of wave w owns
+//    position p = 16 w + l / 4 and dim quarter d4 = l % 4, and loads that
+//    row's 32 K values of the quarter (four 16-byte loads) for the scores of
+//    every head of the group (the quarters meet by two shuffles), and the V
+//    pairs (2 l, 2 l + 1) of the wave's 16 positions (16 loads of 4 bytes, a
+//    whole 256-byte row per load instruction) for PV. Each K and V value is
+//    read from memory once per workgroup and from no LDS at all.
+//  - Every workgroup normalises and rotates its G query heads itself (wave
+//    w takes heads w, w + 4, ..) into LDS; the workgroup whose chunk holds the
+//    new position builds that K row (norm + RoPE) and V row in LDS, uses them
+//    in place of the cache rows and writes them to the cache.
+//  - Scores to LDS, per-head max and sum (wave = head), exp weights to LDS,
+//    PV per wave over its 16 positions for every head, the four waves' sums
+//    added in order; partial output, max and sum per chunk as
+//    attn_partial_kernel (attn_combine_kernel combines the chunks; a
+//    cross-workgroup combine inside this launch costs more than the second
+//    launch).
 template <int G>
-__global__ __launch_bounds__(64 * G) void attn_fused_kernel(const uint16_t* q, const uint16_t* knew,
-                                                            const uint16_t* vnew, const uint16_t* qw,
-                                                            const uint16_t* kw, uint16_t* kcache, uint16_t* vcache,
-                                                            float* po, float* pml, const int32_t* pos_ptr, uint32_t kvh, uint32_t cap,
-                                                            uint32_t nchunks, float scale, RopeTable rope, float eps) {
-    constexpr int kRowK = kHd / 2 + 4;
-    constexpr int kVec = kChunk * kHd / 8;
-    __shared__ __attribute__((aligned(16))) uint32_t ks[kChunk * kRowK];
-    __shared__ uint32_t vs[kChunk * kHd / 2];
-    __shared__ __attribute__((aligned(16))) uint16_t qs[G][kHd];  // the rotated query, bf16
-    __shared__ float ws[G][kChunk];
-    const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63, h = t >> 6;
+__global__ __launch_bounds__(256) void attn_fused_kernel(const uint16_t* q, const uint16_t* knew,
+                                                         const uint16_t* vnew, const uint16_t* qw,
+                                                         const uint16_t* kw, uint16_t* kcache, uint16_t* vcache,
+                                                         float* po, float* pml, const int32_t* pos_ptr, uint32_t kvh,
+                                                         uint32_t cap, uint32_t nchunks, float scale, RopeTable rope,
+                                                         float eps) {
+    __shared__ __attribute__((aligned(16))) uint16_t qs[G][kHd];  // rotated queries, bf16
+    __shared__ __attribute__((aligned(16))) uint16_t nk[kHd];     // the new position's K row (rotated), bf16
+    __shared__ uint16_t nv[kHd];                                   // and its V row
+    __shared__ float sc[G][kChunk];                                // scores, then exp weights
+    __shared__ __attribute__((aligned(16))) float ew[kChunk][G];   // exp weights, position-major
+    __shared__ float part[4][G][kHd];                              // per-wave PV sums
+    const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const uint32_t p0 = c * kChunk;
-    constexpr int kPer = (kVec + 64 * G - 1) / (64 * G);
-    // The chunk's K/V rows are loaded before the position is known (every
-    // row below the capacity is cache memory; rows past the context and the
-    // new position's stale row are loaded and not used), so the position's
-    // load and the rows' loads share one memory round trip.
-    uint4 kv[kPer], vv[kPer];
-    {
-        const uint4* kg = (const uint4*)(kcache + ((size_t)g * cap + p0) * kHd);
-        const uint4* vg = (const uint4*)(vcache + ((size_t)g * cap + p0) * kHd);
+    const uint32_t pr = 16 * w + (lane >> 2), d4 = lane & 3;  // this lane's score row and dim quarter
+    // K and V of the chunk, loaded before the position is known (rows past the
+    // context and the new position's stale row are loaded and not used)
+    // Every load that does not need the position goes first: the group's
+    // queries, the new K and V rows, the norm weights, then the chunk's K and
+    // V (rows past the context and the new position's stale row are loaded
+    // and not used). The position's scalar load then shares their round trip.
+    constexpr int kQH = (G + 3) / 4;  // query heads per wave
+    uint16_t qa[kQH], qb[kQH];
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const uint32_t v = t + j * 64 * G, row = v / (kHd / 8);
-            const bool ok = v < (uint32_t)kVec && p0 + row < cap;
-            kv[j] = ok ? kg[v] : uint4{0, 0, 0, 0};
-            vv[j] = ok ? vg[v] : uint4{0, 0, 0, 0};
-        }
+    for (int i = 0; i < kQH; ++i) {
+        const uint32_t h = min(w + 4 * i, (uint32_t)G - 1);
+        qa[i] = q[(size_t)(g * G + h) * kHd + lane];
+        qb[i] = q[(size_t)(g * G + h) * kHd + lane + 64];
+    }
+    const uint16_t qwa = qw[lane], qwb = qw[lane + 64], kwa = kw[lane], kwb = kw[lane + 64];
+    const uint16_t kna = knew[(size_t)g * kHd + lane], knb = knew[(size_t)g * kHd + lane + 64];
+    const uint16_t vna = vnew[(size_t)g * kHd + lane], vnb = vnew[(size_t)g * kHd + lane + 64];
+    uint4 kq[4];
+    uint32_t vp[16];
+    {
+        const size_t base = (size_t)g * cap + p0;
+        const uint4* kr = (const uint4*)(kcache + (base + min(pr, cap - 1 - p0)) * kHd + 32 * d4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kq[i] = kr[i];
+        const uint32_t* vr = (const uint32_t*)(vcache + base * kHd) + lane;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) vp[j] = vr[(size_t)min(16 * w + j, cap - 1 - p0) * (kHd / 2)];
     }
     const int32_t pos = *pos_ptr;
     const uint32_t len = min((uint32_t)pos + 1, cap);
     if (p0 >= len) return;  // chunk past the context
     const uint32_t np = min((uint32_t)kChunk, len - p0);
     const bool own_row = (uint32_t)pos < cap && (uint32_t)pos >= p0 && (uint32_t)pos < p0 + kChunk;
-    {
-        // query head g*G + h: norm + RoPE
-        {
-            const uint16_t* src = q + (size_t)(g * G + h) * kHd;
+#pragma unroll
+    for (int i = 0; i < kQH; ++i) {  // query head g*G + w + 4 i: norm + RoPE
+        const uint32_t h = w + 4 * i;
+        if (h < (uint32_t)G) {
             uint16_t ra, rb;
-            norm_rope_pair(bf(src[lane]), bf(src[lane + 64]), qw, lane, pos, rope, eps, ra, rb);
+            norm_rope_pair(bf(qa[i]), bf(qb[i]), qwa, qwb, lane, pos, rope, eps, ra, rb);
             qs[h][lane] = ra;
             qs[h][lane + 64] = rb;
         }
-        // rows of the context only (scores and PV read rows < np), and not
-        // the new position's row, which wave 0 alone writes below
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const uint32_t v = t + j * 64 * G, row = v / (kHd / 8);
-            if (v < (uint32_t)kVec && row < np && !(own_row && p0 + row == (uint32_t)pos)) {
-                const uint32_t col = (v % (kHd / 8)) * 4;
-                *(uint4*)&ks[row * kRowK + col] = kv[j];
-                *(uint4*)&vs[row * (kHd / 2) + col] = vv[j];
-            }
-        }
-        if (own_row && h == 0) {  // the new position's K (norm + RoPE) and V rows
-            const uint32_t r = (uint32_t)pos - p0;
-            uint16_t ra, rb;
-            const uint16_t* ksrc = knew + (size_t)g * kHd;
-            norm_rope_pair(bf(ksrc[lane]), bf(ksrc[lane + 64]), kw, lane, pos, rope, eps, ra, rb);
-            const uint16_t va = vnew[(size_t)g * kHd + lane], vb = vnew[(size_t)g * kHd + lane + 64];
-            uint16_t* ks16 = (uint16_t*)&ks[r * kRowK];
-            uint16_t* vs16 = (uint16_t*)&vs[r * (kHd / 2)];
-            ks16[lane] = ra;
-            ks16[lane + 64] = rb;
-            vs16[lane] = va;
-            vs16[lane + 64] = vb;
-            const size_t crow = ((size_t)g * cap + (uint32_t)pos) * kHd;
-            kcache[crow + lane] = ra;
-            kcache[crow + lane + 64] = rb;
-            vcache[crow + lane] = va;
-            vcache[crow + lane + 64] = vb;
-        }
+    }
+    if (own_row && w == 0) {  // the new position's K (norm + RoPE) and V rows
+        uint16_t ra, rb;
+        norm_rope_pair(bf(kna), bf(knb), kwa, kwb, lane, pos, rope, eps, ra, rb);
+        const uint16_t va = vna, vb = vnb;
+        nk[lane] = ra;
+        nk[lane + 64] = rb;
+        nv[lane] = va;
+        nv[lane + 64] = vb;
+        const size_t crow = ((size_t)g * cap + (uint32_t)pos) * kHd;
+        kcache[crow + lane] = ra;
+        kcache[crow + lane + 64] = rb;
+        vcache[crow + lane] = va;
+        vcache[crow + lane + 64] = vb;
     }
     __syncthreads();
-    // scores: lane = position, wave = head; bf16 pairs of K and of the query
-    // (bf16 values) on v_dot2_f32_bf16, f32 accumulation
-    float s = -INFINITY;
-    {
-        uint32_t qp[kHd / 2];
+    if (own_row) {
+        const uint32_t r = (uint32_t)pos - p0;
+        if (pr == r) {
 #pragma unroll
-        for (int i = 0; i < kHd / 8; ++i) {
-            const uint4 u = ((const uint4*)qs[h])[i];
-            qp[4 * i] = u.x;
-            qp[4 * i + 1] = u.y;
-            qp[4 * i + 2] = u.z;
-            qp[4 * i + 3] = u.w;
+            for (int i = 0; i < 4; ++i) kq[i] = ((const uint4*)nk)[4 * d4 + i];
         }
-        if (lane < np) {
-            const uint4* kr = (const uint4*)&ks[lane * kRowK];
-            float acc = 0.0f;
+        if (r >= 16 * w && r < 16 * w + 16) {
 #pragma unroll
-            for (int i = 0; i < kHd / 8; ++i) {
-                const uint4 u = kr[i];
-                acc = dot2_bf16(u.x, qp[4 * i], acc);
-                acc = dot2_bf16(u.y, qp[4 * i + 1], acc);
-                acc = dot2_bf16(u.z, qp[4 * i + 2], acc);
-                acc = dot2_bf16(u.w, qp[4 * i + 3], acc);
-            }
-            s = acc * scale;
+            for (int j = 0; j < 16; ++j)
+                if (16 * w + j == r) vp[j] = ((const uint32_t*)nv)[lane];
         }
     }
-    const float m = wave_max(s);
-    const float e = lane < np ? __expf(s - m) : 0.0f;
-    const float l = wave_sum(e);
-    ws[h][lane] = e;
+    // scores: the lane's 32 dims for every head, the four quarters added by
+    // shuffles ((d0 + d1) + (d2 + d3) in every lane)
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const uint4* qq = (const uint4*)qs[h] + 4 * d4;
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 u = qq[i];
+            acc = dot2_bf16(kq[i].x, u.x, acc);
+            acc = dot2_bf16(kq[i].y, u.y, acc);
+            acc = dot2_bf16(kq[i].z, u.z, acc);
+            acc = dot2_bf16(kq[i].w, u.w, acc);
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        if (d4 == 0) sc[h][pr] = pr < np ? acc * scale : -INFINITY;
+    }
     __syncthreads();
-    float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll 8
-    for (uint32_t p = 0; p < np; ++p) {
-        const uint32_t u = vs[p * (kHd / 2) + lane];
-        const float wp = ws[h][p];
-        o0 = fmaf(wp, __uint_as_float(u << 16), o0);
-        o1 = fmaf(wp, __uint_as_float(u & 0xffff0000u), o1);
+    // per head: max, exp weights and their sum (lane = position)
+    for (uint32_t h = w; h < (uint32_t)G; h += 4) {
+        const float sv = sc[h][lane];
+        const float m = wave_max_dpp(sv);
+        const float e = lane < np ? __expf(sv - m) : 0.0f;
+        const float l = wave_sum_dpp(e);
+        ew[lane][h] = e;
+        if (lane == 0) *(float2*)&pml[((size_t)(g * G + h) * nchunks + c) * 2] = float2{m, l};
     }
-    const size_t prow = (size_t)(g * G + h) * nchunks + c;
-    *(float2*)&po[prow * kHd + 2 * lane] = float2{o0, o1};
-    if (lane == 0) *(float2*)&pml[prow * 2] = float2{m, l};
+    __syncthreads();
+    // PV over the wave's 16 positions for every head: dims 2 lane, 2 lane + 1
+    float o0[G], o1[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) o0[h] = o1[h] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t p = 16 * w + j;
+        if (p < np) {
+            const float va = __uint_as_float(vp[j] << 16), vb = __uint_as_float(vp[j] & 0xffff0000u);
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float e = ew[p][h];
+                o0[h] = fmaf(e, va, o0[h]);
+                o1[h] = fmaf(e, vb, o1[h]);
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) *(float2*)&part[w][h][2 * lane] = float2{o0[h], o1[h]};
+    __syncthreads();
+    for (uint32_t o = t; o < (uint32_t)G * kHd / 2; o += 256) {  // (head, dim pair): waves in order
+        const uint32_t h = o / (kHd / 2), dp = 2 * (o % (kHd / 2));
+        const float2 a = *(const float2*)&part[0][h][dp], b = *(const float2*)&part[1][h][dp];
+        const float2 cc = *(const float2*)&part[2][h][dp], dd = *(const float2*)&part[3][h][dp];
+        const size_t prow = (size_t)(g * G + h) * nchunks + c;
+        *(float2*)&po[prow * kHd + dp] = float2{(a.x + b.x) + (cc.x + dd.x), (a.y + b.y) + (cc.y + dd.y)};
+    }
+}
+
+// Combine the chunks of each query head: out = sum_c o_c e^(m_c - m) / sum_c l_c e^(m_c - m).
+// Workgroup (head, quarter of the dims), 256 threads: dim 32 quarter + t % 32
+// and chunk group t / 32 (chunks t / 32, t / 32 + 8, ..). The partial outputs
+// of the first 16 chunks per group and the first 256 chunk statistics are
+// loaded before the position is known; each group's weighted sum goes to LDS
+// and the eight groups are added in order.
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* po, const float* pml, uint16_t* out,
+                                                           const int32_t* pos_ptr, uint32_t nchunks, uint32_t cap) {
+    constexpr int kCG = 8, kPre = 16;
+    __shared__ float fs[kMaxChunks];
+    __shared__ float part[kCG][32];
+    __shared__ float red[4];
+    const uint32_t h = blockIdx.x, t = threadIdx.x, wv = t >> 6, cg = t >> 5, d = 32 * blockIdx.y + (t & 31);
+    const float* col = po + (size_t)h * nchunks * kHd + d;
+    float pre[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const uint32_t cc = cg + kCG * j;
+        pre[j] = cc < nchunks ? col[(size_t)cc * kHd] : 0.0f;
+    }
+    const float2* ml = (const float2*)pml + (size_t)h * nchunks;
+    const float2 ml0 = t < nchunks ? ml[t] : float2{0.0f, 0.0f};
+    const uint32_t len = min((uint32_t)*pos_ptr + 1, cap);
+    const uint32_t nc = min(nchunks, (len + kChunk - 1) / kChunk);
+    float mx = t < nc ? ml0.x : -INFINITY;
+    for (uint32_t cc = t + 256; cc < nc; cc += 256) mx = fmaxf(mx, ml[cc].x);
+    mx = wave_max_dpp(mx);
+    if ((t & 63) == 0) red[wv] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float l = 0.0f;
+    for (uint32_t cc = t; cc < nc; cc += 256) {
+        const float2 v = cc == t ? ml0 : ml[cc];
+        const float f = __expf(v.x - m);
+        fs[cc] = f;
+        l = fmaf(v.y, f, l);
+    }
+    l = wave_sum_dpp(l);
+    if ((t & 63) == 0) red[wv] = l;
+    __syncthreads();
+    l = (red[0] + red[1]) + (red[2] + red[3]);
+    float o = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const uint32_t cc = cg + kCG * j;
+        if (cc < nc) o = fmaf(pre[j], fs[cc], o);
+    }
+    for (uint32_t cc = cg + kCG * kPre; cc < nc; cc += kCG) o = fmaf(col[(size_t)cc * kHd], fs[cc], o);
+    part[cg][t & 31] = o;
+    __syncthreads();
+    if (t < 32) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < kCG; ++gi) sum += part[gi][t];
+        out[(size_t)h * kHd + d] = to_bf(sum / l);
+    }
 }
 
 // a = silu(g) * u in bf16 steps (gated_act_mul semantics), silu(g) = g / (1 +
@@ -587,7 +705,7 @@ int stark_decode_attention_fused(const void* q, const void* k, const void* v, co
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(kvh, nchunks);
 #define QMM_ATTN_F(GG)                                                                                          \
-    hipLaunchKernelGGL(attn_fused_kernel<GG>, grid, dim3(64 * GG), 0, s, (const uint16_t*)q, (const uint16_t*)k, \
+    hipLaunchKernelGGL(attn_fused_kernel<GG>, grid, dim3(256), 0, s, (const uint16_t*)q, (const uint16_t*)k, \
                        (const uint16_t*)v, (const uint16_t*)qw, (const uint16_t*)kw, (uint16_t*)kcache,          \
                        (uint16_t*)vcache, po, pml, pos, kvh, cap, nchunks, scale, rope, eps)
     switch (G) {
@@ -598,7 +716,7 @@ int stark_decode_attention_fused(const void* q, const void* k, const void* v, co
     default: return 1;
     }
 #undef QMM_ATTN_F
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3(qh), dim3(kHd), 0, s, po, pml, (uint16_t*)out, pos, nchunks, cap);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(qh, kHd / 32), dim3(256), 0, s, po, pml, (uint16_t*)out, pos, nchunks, cap);
     return hipGetLastError() == hipSuccess ? 0 : 10;
 }
 
