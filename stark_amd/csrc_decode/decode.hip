@@ -452,7 +452,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const uint16_t* q, cons
         }
     }
     // scores: the lane's 32 dims for every head, the four quarters added by
-    // shuffles ((d0 + d1) + (d2 + d3) in every lane)
+    // DPP quad permutes ((d0 + d1) + (d2 + d3) in every lane)
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         const uint4* qq = (const uint4*)qs[h] + 4 * d4;
@@ -465,8 +465,8 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const uint16_t* q, cons
             acc = dot2_bf16(kq[i].z, u.z, acc);
             acc = dot2_bf16(kq[i].w, u.w, acc);
         }
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
+        acc += dpp_f32<0xB1>(acc);  // quad_perm [1, 0, 3, 2]
+        acc += dpp_f32<0x4E>(acc);  // quad_perm [2, 3, 0, 1]
         if (d4 == 0) sc[h][pr] = pr < np ? acc * scale : -INFINITY;
     }
     __syncthreads();
