@@ -415,11 +415,19 @@ def timed(torch, step, steps, warmup, stream):
     return a.elapsed_time(b) / steps
 
 
+EAGER = False  # --eager: graph_timed issues the calls one by one (counter passes under rocprofv3)
+
+
 def graph_timed(torch, step, count, steps):
     """Capture `count` calls step(i, stream) (each on its own weight copy) in
     one HIP graph, replay it until at least `steps` calls have run after a
     clock ramp and one warm replay, and time the replays between two events.
-    Python dispatch is outside the figure. Returns ms per call."""
+    Python dispatch is outside the figure. Returns ms per call. With --eager
+    the calls are issued one by one instead (Python dispatch included)."""
+    if EAGER:
+        cur = torch.cuda.current_stream()
+        ms = timed(torch, lambda i: step(i % count, cur), steps, count, cur)
+        return ms, steps
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -731,6 +739,57 @@ def decode_line(args, torch):
                                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
 
 
+def attention_line(args, torch):
+    """Diagnostic (--attention): the decode step's attention pair alone -- the
+    fused q/k norm + RoPE + KV write + chunk partials launch and the chunk
+    combine -- at the Qwen3-8B shape (32 query / 8 KV heads of 128) after a
+    4096-token context, over 36 rotating layer caches (past the MALL), timed
+    as replays of one captured graph. Bytes: the K and V rows read (the new
+    position's included) plus the partials written and read back."""
+    import ctypes as C
+    from stark_amd import decode as DEC
+    D = DEC.lib()
+    qh, kvh, hd, ctx, layers = 32, 8, 128, 4096, LAYERS
+    cap = ctx + 264
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 50)
+    nch = D.stark_decode_attn_chunks(cap)
+    caches = [((torch.randn(kvh * cap * hd, generator=gen, device="cuda")).to(torch.bfloat16),
+               (torch.randn(kvh * cap * hd, generator=gen, device="cuda")).to(torch.bfloat16)) for _ in range(layers)]
+    q = torch.randn(qh * hd, generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn(kvh * hd, generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn(kvh * hd, generator=gen, device="cuda").to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(hd, generator=gen, device="cuda")).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(hd, generator=gen, device="cuda")).to(torch.bfloat16)
+    po = torch.empty(qh * nch * hd, dtype=torch.float32, device="cuda")
+    pml = torch.empty(qh * nch * 2, dtype=torch.float32, device="cuda")
+    out = torch.empty(qh * hd, dtype=torch.bfloat16, device="cuda")
+    pos = torch.tensor([ctx], dtype=torch.int32, device="cuda")
+    ptr = lambda t: C.c_void_p(t.data_ptr())
+
+    def step(i, s):
+        kc, vc = caches[i]
+        st = D.stark_decode_attention_fused(ptr(q), ptr(k), ptr(v), ptr(qw), ptr(kw), ptr(kc), ptr(vc), ptr(po),
+                                            ptr(pml), ptr(out), ptr(pos), qh, kvh, cap, 1e6, 1e-6,
+                                            C.c_void_p(s.cuda_stream))
+        if st != 0:
+            raise SystemExit(f"attention: status {st}")
+
+    ms, ran = graph_timed(torch, step, layers, args.steps)
+    used = (ctx + 1 + 63) // 64
+    nbytes = 2 * kvh * (ctx + 1) * hd * 2 + 2 * qh * used * (hd + 2) * 4 + qh * hd * 2 * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({"metric": "decode attention pair (fused partials + combine) HBM GB/s", "value": round(gbs, 1),
+                      "unit": "GB/s", "n_gpus": 1, "steps": ran, "warmup": layers, "ms_per_step": round(ms, 5),
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                      "data": "synthetic: N(0,1) K/V caches and q/k/v rows",
+                      "config": {"workload": f"decode attention at position {ctx}: 32/8 heads of 128, "
+                                             f"{layers} rotating layer caches, one captured HIP graph over them",
+                                 "bytes_per_step": nbytes},
+                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -748,6 +807,11 @@ def main():
                     help="config 1: also print the M = 2, 4, 8, 16 (speculative verify) lines")
     ap.add_argument("--copies", type=int, default=LAYERS,
                     help="config 1: distinct layer-weight copies the steps rotate through (36 = one Qwen3-8B)")
+    ap.add_argument("--eager", action="store_true",
+                    help="configs 2 and 3 and --attention: issue the calls one by one instead of graph replays "
+                         "(for counter passes)")
+    ap.add_argument("--attention", action="store_true",
+                    help="diagnostic: time the decode attention pair alone (Qwen3-8B shape, 36 rotating caches)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB bitwise_not pass (byte-counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -764,6 +828,11 @@ def main():
     from stark_amd import qmm as Q
     Q.lib()
     torch.cuda.set_device(torch.device("cuda:0"))
+    global EAGER
+    EAGER = args.eager
+    if args.attention:
+        attention_line(args, torch)
+        return
     {1: config1, 2: config2, 3: config3, 4: config4}[args.config](args, torch, Q)
 
 

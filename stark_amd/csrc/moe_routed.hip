@@ -276,6 +276,36 @@ struct GroupedLaunch {
     uint32_t cls, tiles, active, hidden, model;
 };
 
+// Work items (slot, tile) in XCD-aware order. Workgroups are dealt to the 8
+// XCDs round-robin (block b on XCD b % 8; a persistent loop with a grid that
+// is a multiple of 8 keeps item i on XCD i % 8), and each XCD has its own L2.
+// In the group-output plane layout a 128-byte plane line holds one group of
+// 64 consecutive bank rows, i.e. TPL tiles (8-row up tiles: 8; 16-row down
+// tiles: 4): item i = x + 8 k takes line group L = x + 8 (k / TPL) and its
+// tile k % TPL, so the tiles that share a plane line run on one XCD and the
+// line is fetched from HBM once. Items past the last line group (padding up
+// to padded_items) return false.
+__device__ __host__ inline uint32_t line_groups(uint32_t slots, uint32_t tiles, uint32_t tpl) {
+    return slots * (tiles / tpl);
+}
+__device__ __host__ inline uint32_t padded_items(uint32_t slots, uint32_t tiles, uint32_t tpl) {
+    return 8 * tpl * ((line_groups(slots, tiles, tpl) + 7) / 8);
+}
+__device__ __forceinline__ bool xcd_item(uint32_t i, uint32_t slots, uint32_t tiles, uint32_t tpl, uint32_t& slot,
+                                         uint32_t& t) {
+    const uint32_t lg = tiles / tpl, k = i >> 3;
+    const uint32_t L = (i & 7) + 8 * (k / tpl);
+    if (L >= slots * lg) return false;
+    slot = L / lg;
+    t = tpl * (L % lg) + k % tpl;
+    return true;
+}
+// tiles per plane line for a tile height (1 when the tiles do not divide into lines)
+__device__ __host__ inline uint32_t line_tiles(uint32_t tiles, uint32_t rows) {
+    const uint32_t tpl = 64 / rows;
+    return tiles % tpl == 0 ? tpl : 1u;
+}
+
 // silu(gate) * value in bf16 steps (gated_act_mul; SiLU as
 // src/backends/common/gpu_types/activation_type.rs:35-46)
 __device__ __forceinline__ uint16_t gated_silu(float value_f, float gate_f) {
@@ -292,11 +322,14 @@ __global__ __launch_bounds__(kWg) void moe_up_mfma(GroupedLaunch launch) {
     (void)launch;
     __shared__ MfmaLds<MP, MB, GS, 4, P1> lds;
     const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
-    const uint32_t items = L->header[L->cls] * L->tiles;
+    const uint32_t slots = L->header[L->cls], tpl = line_tiles(L->tiles, 8);
+    const uint32_t items = padded_items(slots, L->tiles, tpl);
     const uint32_t H = L->hidden, A = L->active, model = L->model;
     for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-        const uint32_t* rec = L->table + (size_t)(item / L->tiles) * kRecWords;
-        const uint32_t t = item % L->tiles, e = rec[0], cnt = rec[1];
+        uint32_t sl, t;
+        if (!xcd_item(item, slots, L->tiles, tpl, sl, t)) continue;
+        const uint32_t* rec = L->table + (size_t)sl * kRecWords;
+        const uint32_t e = rec[0], cnt = rec[1];
         const uint32_t nA = e * 2 * H + 8 * t, nB = nA + H;
         const uint32_t* routes = rec + 2;
         mfma_tile<MP, MB, GS, 4, SIGNED, P1>(
@@ -319,11 +352,14 @@ __global__ __launch_bounds__(kWg) void moe_down_mfma(GroupedLaunch launch) {
     (void)launch;
     __shared__ MfmaLds<MP, MB, GS, 4, P1> lds;
     const GroupedLaunch* L = (const GroupedLaunch*)__builtin_amdgcn_kernarg_segment_ptr();
-    const uint32_t items = L->header[L->cls] * L->tiles;
+    const uint32_t slots = L->header[L->cls], tpl = line_tiles(L->tiles, 16);
+    const uint32_t items = padded_items(slots, L->tiles, tpl);
     const uint32_t H = L->hidden, model = L->model;
     for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-        const uint32_t* rec = L->table + (size_t)(item / L->tiles) * kRecWords;
-        const uint32_t t = item % L->tiles, e = rec[0], cnt = rec[1];
+        uint32_t sl, t;
+        if (!xcd_item(item, slots, L->tiles, tpl, sl, t)) continue;
+        const uint32_t* rec = L->table + (size_t)sl * kRecWords;
+        const uint32_t e = rec[0], cnt = rec[1];
         const uint32_t nA = e * model + 16 * t;
         const uint32_t* routes = rec + 2;
         mfma_tile<MP, MB, GS, 4, SIGNED, P1>(
@@ -449,7 +485,8 @@ __global__ __launch_bounds__(kWg) void moe_route_up_one(GroupedLaunch launch, Ro
     __syncthreads();
     // the item: route (slot) and tile of 8 value rows
     const uint32_t H = L->hidden, model = L->model;
-    const uint32_t slot = blockIdx.x / L->tiles, t = blockIdx.x % L->tiles;
+    uint32_t slot, t;
+    if (!xcd_item(blockIdx.x, A, L->tiles, line_tiles(L->tiles, 8), slot, t)) return;  // padding block
     const uint32_t e = sid[slot] < E ? sid[slot] : 0u;
     const uint32_t nA = e * 2 * H + 8 * t, nB = nA + H;
     mfma_tile<1, 1, GS, 4, SIGNED, P1>(L->op, plane_flags(L->op), nA, nB, 1, [&](uint32_t) { return (size_t)0; }, lds);
@@ -525,7 +562,9 @@ __global__ __launch_bounds__(512) void moe_down_acc_one(DownAccArgs a) {
     __shared__ float rw[8];
     __shared__ u32x4 xs[8][XV];  // each wave's activation row
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint32_t H = a.hidden, n0 = blockIdx.x * 16, r = lane >> 2, q = lane & 3;
+    uint32_t one, tile;
+    if (!xcd_item(blockIdx.x, 1, a.model / 16, line_tiles(a.model / 16, 16), one, tile)) return;  // padding block
+    const uint32_t H = a.hidden, n0 = tile * 16, r = lane >> 2, q = lane & 3;
     // first the loads that need no route: the wave's activation row and the
     // route weights (the codes' addresses wait for the expert id)
     const bool live = w < a.active;
@@ -790,7 +829,8 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
         g.cls = 0;
         void* fn = pick_route_up_one(g.op.group_size, sg, model);
         void* argv[] = {&g, &ra};
-        QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(A * g.tiles), dim3(kWg), argv, 0, stream));
+        const uint32_t blocks = padded_items(A, g.tiles, line_tiles(g.tiles, 8));
+        QMM_HIP_CHECK(hipLaunchKernel(fn, dim3(blocks), dim3(kWg), argv, 0, stream));
     } else if (Lw.routes <= kFusedRoutes && R <= kFusedRows && nkeys <= kFusedKeys && nkeys * E <= kFusedCompares) {
         hipLaunchKernelGGL(moe_route_compact, dim3(1), dim3(1024), nkeys * 8, stream, a->router_logits, R, E, A,
                            a->round_weights_bf16, a->round_logits_bf16, a->expert_scales, (uint32_t)adjust, sort,
@@ -827,7 +867,8 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
             g.table = table + (size_t)c * Lw.max_slots * kRecWords;
             const uint64_t items = (uint64_t)class_slot_bound(c, Lw.routes, E, Lw.max_slots) * g.tiles;
             if (items == 0) continue;
-            const uint32_t grid = (uint32_t)std::min<uint64_t>(items, 4096);
+            // a multiple of 8 (the items' XCD order), at most 4096
+            const uint32_t grid = (uint32_t)std::min<uint64_t>((items + 7) / 8 * 8, 4096);
             void* fn = up ? pick_class<moe_up_mfma_k>(c, max_count, g.op.group_size, sg, model)
                           : pick_class<moe_down_mfma_k>(c, max_count, g.op.group_size, sg, H);
             if (!fn) return STARK_QMM_UNSUPPORTED_GROUP_SIZE;
@@ -844,7 +885,8 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
                        d.os, d.gs, act, ids, weights, (uint16_t*)a->output, model, H, E, A,
                        a->down.signed_codes ? 1u : 0u, a->round_products_bf16, a->round_accumulator_bf16};
         void* argv[] = {&da};
-        QMM_HIP_CHECK(hipLaunchKernel(down_acc, dim3(model / 16), dim3(64 * A), argv, 0, stream));
+        const uint32_t blocks = padded_items(1, model / 16, line_tiles(model / 16, 16));
+        QMM_HIP_CHECK(hipLaunchKernel(down_acc, dim3(blocks), dim3(64 * A), argv, 0, stream));
         return STARK_QMM_OK;
     }
     // 5. accumulate ranks in order
