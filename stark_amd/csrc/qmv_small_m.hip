@@ -57,9 +57,17 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     (void)batch;
     __shared__ SmLds lds;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
+    // Blocks are dealt to the 8 XCDs round-robin (block b on XCD b % 8); a
+    // group-output plane line holds 64 rows, i.e. two blocks of 32, so block
+    // b = x + 8 k runs tile pair 2 (x + 8 (k / 2)) + k % 2 and the two pairs
+    // of a line share the XCD's L2 (kb->total: the pairs; the launch is padded
+    // to 16-block steps and the padding blocks return).
+    const uint32_t bx = blockIdx.x, kx = bx >> 3;
+    const uint32_t blk = 2 * ((bx & 7) + 8 * (kx >> 1)) + (kx & 1);
+    if (blk >= kb->total) return;
     uint32_t oi = 0;
     for (uint32_t i = 1; i < kb->count; ++i)
-        if (blockIdx.x >= kb->op[i].block_begin) oi = i;
+        if (blk >= kb->op[i].block_begin) oi = i;
     const AffineOp& op = kb->op[oi];
     const uint32_t N = op.n, K = op.k, M = op.m;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -67,7 +75,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const uint32_t j = lane & 15, kq = lane >> 4;
     // tile tt covers rows n0[tt] .. +15 and writes those from t0 + 16 tt on; a
     // tile past N moves back to end at N, so every row is written once
-    const uint32_t t0 = (blockIdx.x - op.block_begin) * kRows * kSmTiles;
+    const uint32_t t0 = (blk - op.block_begin) * kRows * kSmTiles;
     uint32_t n0[kSmTiles];
 #pragma unroll
     for (int tt = 0; tt < kSmTiles; ++tt) n0[tt] = min(t0 + kRows * tt, N - kRows);
@@ -277,11 +285,13 @@ stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed
         blocks += (sorted[i].n + kRows * kSmTiles - 1) / (kRows * kSmTiles);
     }
     batch.count = count;
+    batch.total = blocks;
     if (blocks == 0) return STARK_QMM_OK;
+    const uint32_t grid = (blocks + 15) / 16 * 16;  // whole line pairs on every XCD
     if (signed_codes)
-        hipLaunchKernelGGL(qmv_small_m<true>, dim3(blocks), dim3(kWg), 0, stream, batch);
+        hipLaunchKernelGGL(qmv_small_m<true>, dim3(grid), dim3(kWg), 0, stream, batch);
     else
-        hipLaunchKernelGGL(qmv_small_m<false>, dim3(blocks), dim3(kWg), 0, stream, batch);
+        hipLaunchKernelGGL(qmv_small_m<false>, dim3(grid), dim3(kWg), 0, stream, batch);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
 }
