@@ -678,7 +678,7 @@ def decode_measure(args, torch):
     from stark_amd import decode as DEC
     cfg = DEC.Qwen3Config()
     ctx, gen_tokens = 4096, args.decode_tokens
-    m = DEC.Qwen3Decoder(cfg, capacity=ctx + gen_tokens + 8, seed=SEED + 40)
+    m = DEC.Qwen3Decoder(cfg, capacity=ctx + gen_tokens + 8, seed=SEED + 40, chain=args.decode_form == "chain")
     m.fill_context(ctx, seed=SEED + 41)
     m.step()  # eager: builds the library's per-shape schedules
     torch.cuda.synchronize()
@@ -719,7 +719,10 @@ def decode_measure(args, torch):
     return dict(tokens_per_s=round(tps, 1), ms_per_token=round(ms, 5), timed_tokens=timed_tokens,
                 workload=f"config 4 decode: {gen_tokens} greedy tokens after a {ctx}-token context, 36 layers, "
                          "vocab 151936 (W8 lm_head), one HIP graph replay per token; RMS norms and gated SiLU run as "
-                         "input prologues of the products",
+                         "input prologues of the products"
+                         + ("; per layer, o, gate/up, down and the next layer's q/k/v products run as one chained "
+                            "launch" if args.decode_form == "chain" else ""),
+                form=args.decode_form,
                 hbm_bytes_per_token_algorithmic=per_token, achieved_gbs=round(gbs, 1),
                 frac_of_hbm_peak=round(gbs / PEAK_HBM_GBS, 4))
 
@@ -802,6 +805,10 @@ def main():
     ap.add_argument("--decode-tokens", type=int, default=256,
                     help="configs 1 and 4: greedy tokens generated after the 4096-token context in the end-to-end "
                          "decode measurement (0 skips it)")
+    ap.add_argument("--decode-only", action="store_true", help="only the end-to-end decode line (config 4)")
+    ap.add_argument("--decode-form", choices=("chain", "fused"), default="fused",
+                    help="decode stand-in: products after attention as one chained launch per layer (chain) or one "
+                         "launch per product with norm/SiLU prologues (fused)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verify", action="store_true",
                     help="config 1: also print the M = 2, 4, 8, 16 (speculative verify) lines")
@@ -832,6 +839,9 @@ def main():
     EAGER = args.eager
     if args.attention:
         attention_line(args, torch)
+        return
+    if args.decode_only:
+        decode_line(args, torch)
         return
     {1: config1, 2: config2, 3: config3, 4: config4}[args.config](args, torch, Q)
 

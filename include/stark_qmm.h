@@ -223,6 +223,57 @@ STARK_QMM_API stark_qmm_status stark_qmm_encode_many_prologue(stark_qmm_kernel* 
                                                             uint32_t count, const stark_qmm_prologue* prologue,
                                                             void* stream);
 
+/* Chained products: several dependent stages of one-row products in ONE
+ * persistent launch. No counterpart in the reference, whose decoder encodes
+ * every product of a layer as a dispatch of its own
+ * (crates/stark-engine/src/encodable_block/transformer_layer.rs); this is for
+ * decode loops that want a layer's o -> gate/up -> down -> next q/k/v products
+ * without a launch boundary (and its fixed cost) between them. Each product
+ * computes exactly what stark_qmm_encode_many_prologue computes for it.
+ *
+ * Rows handed from one stage to a later one are TAGGED: one 32-bit word per
+ * element, bf16 value in the low half and a tag (1..0x7fff) in the high half.
+ * A product whose in_tag is non-zero reads tagged a (and, with the SiLU-gate
+ * prologue, tagged up values) and waits until every word it reads carries
+ * in_tag; one whose out_tag is non-zero writes tagged d. Plain rows (tag 0)
+ * must be complete before the launch. A stage may read only rows written by
+ * earlier stages or before the launch, and every element of a tagged row must
+ * be rewritten with another tag between two writes of the same tag: reusing
+ * the same tags in consecutive calls needs `seq`, a device word whose low bit
+ * differs between the calls (it flips bit 15 of every tag; NULL = no flip).
+ *
+ * k_slices > 1 splits the product's K into that many slices of 4096 whose row
+ * sums meet in the workspace and are added in slice order (bit-identical to
+ * stark_qmm_encode_many_prologue for K = 12288 and 3 slices); it needs a
+ * tagged output. Requirements: BF16 input/output/planes with biases, M = 1,
+ * 4-bit codes, group 64, K % 4096 == 0 (the RMS-norm prologue: K == 4096),
+ * N % 32 == 0, no gather, bias, soft cap or RHT; at most 16 tiles lists
+ * (products plus extra slices). Otherwise STARK_QMM_UNSUPPORTED.
+ *
+ * Every wait is bounded: a wait that gives up (about 0.1 s) sets the status
+ * word at workspace offset 0 non-zero (the caller clears it) and the rows of
+ * that launch are invalid. The launch needs every workgroup resident at once:
+ * do not run it concurrently with other kernels on the same device. */
+typedef struct stark_qmm_chain_product {
+    uint32_t struct_size;         /* sizeof(stark_qmm_chain_product) */
+    uint32_t stage;               /* stages run in increasing order */
+    const stark_qmm_args* args;   /* the product (a/d tagged as in_tag/out_tag say) */
+    uint32_t prologue;            /* STARK_QMM_PROLOGUE_* */
+    const void* prologue_data;    /* RMS norm: bf16 weights; SiLU gate: up row, in a's format */
+    float eps;
+    uint32_t in_tag, out_tag;     /* 0 = plain bf16 row */
+    uint32_t acc_tag;             /* tagged d with accumulate: tag d carries before it is read (0: at launch) */
+    uint32_t k_slices;            /* 0 or 1: whole K */
+} stark_qmm_chain_product;
+
+/* Workspace bytes stark_qmm_encode_chain needs for these products. */
+STARK_QMM_API stark_qmm_status stark_qmm_chain_workspace_size(const stark_qmm_chain_product* products, uint32_t count,
+                                                            uint64_t* bytes);
+
+STARK_QMM_API stark_qmm_status stark_qmm_encode_chain(stark_qmm_kernel* kernel, const stark_qmm_chain_product* products,
+                                                    uint32_t count, const uint32_t* seq, void* workspace,
+                                                    uint64_t workspace_bytes, void* stream);
+
 /* Replaces MatmulKernel::set_reference_accumulation (kernel.rs:34-37): when
  * enabled, every M uses the GEMV/verify kernels (f32 dequant semantics). */
 STARK_QMM_API stark_qmm_status stark_qmm_set_reference_accumulation(stark_qmm_kernel* kernel, uint32_t enabled);

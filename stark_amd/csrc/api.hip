@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "qmm_common.h"
+#include "stream_common.h"
 
 struct stark_qmm_kernel {
     uint32_t w_dt, x_dt, d_dt;
@@ -367,6 +368,119 @@ stark_qmm_status stark_qmm_encode_many_prologue(stark_qmm_kernel* kr, const star
     }
     const StreamPrologue p{pro->kind, pro->data, pro->eps};
     return launch_stream_prologue(ops.data(), (uint32_t)ops.size(), p, (hipStream_t)stream_ptr);
+}
+
+}  // extern "C"
+
+
+// Chained products (stream_common.h, qmv_chain.hip): validation, K slices and
+// the workspace layout -- a 256-byte status header, then for each product of
+// k_slices > 1 (in order) (k_slices - 1) x N 64-bit partial words.
+static stark_qmm_status chain_validate(const stark_qmm_chain_product* p, uint32_t count, uint64_t* bytes) {
+    if (!p && count) return STARK_QMM_INVALID_ARGUMENT;
+    uint64_t need = 256;
+    uint32_t lists = 0, stage = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (p[i].struct_size != sizeof(stark_qmm_chain_product)) return STARK_QMM_ABI_MISMATCH;
+        const stark_qmm_args* a = p[i].args;
+        if (!a) return STARK_QMM_INVALID_ARGUMENT;
+        if (a->struct_size != sizeof(stark_qmm_args)) return STARK_QMM_ABI_MISMATCH;
+        if (i && p[i].stage < stage) return STARK_QMM_INVALID_ARGUMENT;  // stages in increasing order
+        stage = p[i].stage;
+        const uint32_t sl = p[i].k_slices ? p[i].k_slices : 1;
+        if (a->a_kind != STARK_QMM_A_FULL_PRECISION || !a->b.codes || a->m != 1 || a->b.mode != STARK_QMM_MODE_U4 ||
+            a->b.group_size != 64 || a->k == 0 || a->k % 4096 || a->n == 0 || a->n % 32 || a->gather_indices ||
+            a->d_ops.bias || a->d_ops.rht_factors || a->d_ops.has_soft_cap || a->b.params.materialize_affine_input_sum ||
+            a->b.correction != STARK_QMM_CORRECTION_BIASES || (a->k / 4096) % sl || p[i].in_tag > 0x7fff ||
+            p[i].out_tag > 0x7fff || p[i].acc_tag > 0x7fff || (sl > 1 && !p[i].out_tag) ||
+            (p[i].acc_tag && !p[i].out_tag) || p[i].prologue > STARK_QMM_PROLOGUE_SILU_GATE ||
+            (p[i].prologue == STARK_QMM_PROLOGUE_RMS_NORM && a->k != 4096))
+            return STARK_QMM_UNSUPPORTED;
+        if (!a->a || !a->d || (p[i].prologue && (!p[i].prologue_data || ((uintptr_t)p[i].prologue_data & 15))))
+            return STARK_QMM_INVALID_ARGUMENT;
+        lists += sl;
+        if (sl > 1) need += (uint64_t)(sl - 1) * a->n * 8;
+    }
+    if (lists > (uint32_t)kMaxChainOps) return STARK_QMM_UNSUPPORTED;
+    *bytes = need;
+    return STARK_QMM_OK;
+}
+
+extern "C" {
+
+stark_qmm_status stark_qmm_chain_workspace_size(const stark_qmm_chain_product* products, uint32_t count,
+                                               uint64_t* bytes) {
+    if (!bytes) return STARK_QMM_INVALID_ARGUMENT;
+    return chain_validate(products, count, bytes);
+}
+
+stark_qmm_status stark_qmm_encode_chain(stark_qmm_kernel* kr, const stark_qmm_chain_product* p, uint32_t count,
+                                        const uint32_t* seq, void* workspace, uint64_t workspace_bytes,
+                                        void* stream_ptr) {
+    if (!kr) return STARK_QMM_INVALID_ARGUMENT;
+    if (kr->reference_accumulation || kr->x_dt != STARK_QMM_BF16 || kr->d_dt != STARK_QMM_BF16 ||
+        kr->w_dt != STARK_QMM_BF16)
+        return STARK_QMM_UNSUPPORTED;
+    uint64_t need = 0;
+    const stark_qmm_status vs = chain_validate(p, count, &need);
+    if (vs != STARK_QMM_OK) return vs;
+    if (!workspace || ((uintptr_t)workspace & 255)) return STARK_QMM_INVALID_ARGUMENT;
+    if (workspace_bytes < need) return STARK_QMM_WORKSPACE_TOO_SMALL;
+    std::vector<ChainOp> ops;
+    uint64_t* part = (uint64_t*)((uint8_t*)workspace + 256);
+    for (uint32_t i = 0; i < count; ++i) {
+        const stark_qmm_args* a = p[i].args;
+        const uint32_t esz = p[i].in_tag ? 4 : 2;
+        const void* x = (const uint8_t*)a->a + a->a_offset * esz;
+        AffineOp op;
+        int bits;
+        const stark_qmm_status st = build_affine_op(kr, a->b, 1, a->n, a->k, x, a->d, a->d_ops, nullptr, &op, &bits);
+        if (st != STARK_QMM_OK) return st;
+        if ((((uintptr_t)op.codes | (uintptr_t)x | (uintptr_t)op.scales | (uintptr_t)op.corr) & 15) ||
+            (op.os == 1 ? op.gs % 8 : op.os % 8))
+            return STARK_QMM_UNSUPPORTED;
+        const uint32_t sl = p[i].k_slices ? p[i].k_slices : 1, ks = a->k / sl;
+        for (uint32_t j = 0; j < sl; ++j) {
+            ChainOp c{};
+            const size_t g0 = (size_t)j * (ks / 64);  // first group of the slice
+            const size_t poff = op.os == 1 ? g0 * op.gs : g0;
+            c.codes = op.codes + (size_t)j * (ks / 2);
+            c.scales = (const uint16_t*)op.scales + poff;
+            c.corr = (const uint16_t*)op.corr + poff;
+            c.x = (const uint8_t*)x + (size_t)j * ks * esz;
+            c.d = a->d;
+            c.pro = p[i].prologue;
+            c.pro_data = p[i].prologue == STARK_QMM_PROLOGUE_SILU_GATE
+                             ? (const void*)((const uint8_t*)p[i].prologue_data + (size_t)j * ks * esz)
+                             : p[i].prologue_data;
+            c.eps = p[i].eps;
+            c.n = a->n;
+            c.k = ks;
+            c.ldc = a->k / 2;
+            c.os = op.os;
+            c.gs = op.gs;
+            c.ab_scale = op.ab_scale;
+            c.in_tag = p[i].in_tag;
+            c.out_tag = p[i].out_tag;
+            c.acc_tag = p[i].acc_tag;
+            c.flags = op.flags & (FLAG_ACCUMULATE | FLAG_SIGNED);
+            c.order = 2 * p[i].stage;
+            if (sl == 1) {
+                c.out = p[i].out_tag ? CHAIN_OUT_TAGGED : CHAIN_OUT_PLAIN;
+            } else if (j + 1 < sl) {
+                c.out = CHAIN_OUT_PARTIAL;
+                c.part = part + (size_t)j * a->n;
+            } else {
+                c.out = CHAIN_OUT_COMBINE;
+                c.part = part;
+                c.nparts = sl - 1;
+                c.order = 2 * p[i].stage + 1;  // after the other slices in every list
+            }
+            ops.push_back(c);
+        }
+        if (sl > 1) part += (size_t)(sl - 1) * a->n;
+    }
+    return launch_chain(ops.data(), (uint32_t)ops.size(), seq, (uint32_t*)workspace, (hipStream_t)stream_ptr);
 }
 
 }  // extern "C"

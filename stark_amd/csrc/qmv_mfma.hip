@@ -7,7 +7,7 @@
 #include <map>
 #include <mutex>
 
-#include "mfma_tile.h"
+#include "stream_common.h"
 
 namespace qmm {
 
@@ -38,10 +38,6 @@ constexpr int kWavesPerEu = MR >= 8 || (GS == 32 && MR >= 4) ? 2 : (MR >= 4 || B
 // workgroup issues the next tile's loads as soon as the current tile sits in
 // LDS, so HBM streams across tile boundaries; there are no atomics and no
 // per-launch state.
-struct Schedule {
-    const uint32_t* begin;  // [grid + 1] offsets into tiles
-    const uint32_t* tiles;  // [total tiles]
-};
 
 template <int MP, int MB, int GS, int BITS, bool SIGNED>
 __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<MP * MB, BITS, GS>))) void qmv_mfma(
@@ -154,6 +150,7 @@ struct StoreEntry {
     bool eager = false;          // uploaded outside capture
     bool landed = false;         // the eager upload has been seen complete
     bool pinned = false;         // referenced by a captured graph
+    hipStream_t stream = nullptr;  // stream of the eager upload
 };
 
 struct DeviceStore {
@@ -231,17 +228,13 @@ std::vector<uint32_t> build_schedule(const AffineOp* ops, uint32_t count, uint32
 
 // Device schedule of a shape set, uploaded on `stream` on first use (see the
 // store above).
-stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* out, hipStream_t stream,
-                              uint32_t rows = kRows) {
+stark_qmm_status store_schedule(const std::vector<uint32_t>& key, uint32_t grid,
+                                const std::function<std::vector<uint32_t>()>& build, Schedule* out,
+                                hipStream_t stream) {
     static std::mutex mu;
     static std::map<int, DeviceStore> stores;
     int dev = 0;
     QMM_HIP_CHECK(hipGetDevice(&dev));
-    std::vector<uint32_t> key{grid, rows};
-    for (uint32_t i = 0; i < count; ++i) {
-        key.push_back((ops[i].n + rows - 1) / rows);
-        key.push_back(ops[i].k);
-    }
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     QMM_HIP_CHECK(hipStreamIsCapturing(stream, &cap));
     const bool capturing = cap != hipStreamCaptureStatusNone;
@@ -251,7 +244,7 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
     auto it = ds.entries.find(key);
     if (it == ds.entries.end()) {
         StoreEntry e;
-        e.host = build_schedule(ops, count, grid, rows);
+        e.host = build();
         const uint32_t words = ((uint32_t)e.host.size() + 63) / 64 * 64;
         if (words > kStoreWords) return STARK_QMM_OUT_OF_MEMORY;
         if (ds.used + words > kStoreWords) {
@@ -276,10 +269,19 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
     }
     StoreEntry& e = it->second;
     if (capturing) {
-        // the graph carries its own upload, ordered before the product
-        if (e.eager && !e.landed) QMM_HIP_CHECK(hipEventSynchronize(e.done));
-        e.landed = e.eager;
-        if (!e.eager) {
+        // An eager upload that has completed serves the graph too. One still
+        // in flight (or of unknown state: nothing here may wait while a
+        // stream captures) is repeated inside the graph, ordered before the
+        // product; the words are the same.
+        // (an event recorded on the capturing stream itself is not queried:
+        // that would invalidate the capture)
+        if (e.eager && !e.landed && e.stream != stream) {
+            if (hipEventQuery(e.done) == hipSuccess)
+                e.landed = true;
+            else
+                (void)hipGetLastError();
+        }
+        if (!e.landed) {
             const stark_qmm_status st = upload(ds.base, e, stream);
             if (st != STARK_QMM_OK) return st;
         }
@@ -290,6 +292,7 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
         if (!e.done) QMM_HIP_CHECK(hipEventCreateWithFlags(&e.done, hipEventDisableTiming));
         QMM_HIP_CHECK(hipEventRecord(e.done, stream));
         e.eager = true;
+        e.stream = stream;
     } else if (!e.landed) {
         const hipError_t q = hipEventQuery(e.done);
         if (q == hipSuccess)
@@ -303,110 +306,17 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
     return STARK_QMM_OK;
 }
 
-// ---------------------------------------------------------------------------
-// Streaming kernel for one activation row of 4-bit codes, group size 64 and
-// K % 4096 == 0 (the decode shapes). Same arithmetic as TileEngine -- codes as
-// raw bf16 bit patterns, one-hot activation rows per group slot, one f32 flush
-// per group -- with a load layout built for HBM streaming:
-//  - Split columns. B column c = 8*hh + r of the MFMA holds row r of an 8-row
-//    subtile, byte half hh of a 128-byte block: lane r + 8*hh + 16*kb loads the
-//    16 bytes at 16*(4*hh + kb) of the block. One load instruction then covers
-//    128 contiguous bytes (whole cache lines) of each of 8 rows, and the codes
-//    go straight from the load into the MFMA operand with no LDS transpose.
-//    A rows 8*hh .. 8*hh+7 are the 8 group slots of byte half hh (x at that
-//    half's positions); the C entries that pair one half's activations with
-//    the other half's codes are never read.
-//  - Tiles of 32 rows (4 subtiles), units of 1024 k. A unit is 16 steps
-//    (4 k-blocks of 256 x 4 subtiles, 16 KiB of codes) and one flush period
-//    (16 groups per row, 8 per byte half). Wave w takes chunks w, w+4, ... of
-//    every tile; the four waves of a workgroup meet once per tile, at an
-//    LDS-only barrier. The scale and bias planes of a unit are 16 groups x 32
-//    rows: half cache lines in the group-output layout, whose other half is
-//    the neighbouring tile's, scheduled on the same XCD.
-//  - Loads in flight. A ring of 8 step registers, refilled 8 steps ahead
-//    across unit, tile and barrier boundaries (8 KiB per wave in flight). Two
-//    workgroups per CU: more bytes in flight only lengthen the queues.
-//  - Activations are staged per wave (no barrier) into one of kXR regions,
-//    as x * 2^E with a per-group exponent E (group_shift in qmm_common.h),
-//    tagged (activation id, chunk), so consecutive tiles of ops that read the
-//    same activations (q/k/v, gate/up) reuse them; the plane
-//    vectors of a unit are loaded with the unit and pass through a
-//    wave-private LDS block at the flush.
-constexpr int kXR = 3;         // activation regions per wave
-constexpr int kTR = 32;        // tile rows
-constexpr int kUnitK = 1024;   // k values per unit (16 groups of 64)
-constexpr int kListLds = kWg;  // schedule entries staged in LDS at kernel start (one per thread)
-
-template <int WV>  // waves per workgroup
-struct StreamLds {
-    u32x4 xp[WV][kXR][kUnitK / 8];  // activation pairs (x0,x4)(x1,x5).. per 8 values; x*2^E, odd values x*2^(E-4)
-    float xs[WV][kXR][kUnitK / 64];  // activation sum per group
-    int xe[WV][kXR][kUnitK / 64];    // 133 - E per group: the flush's ldexp (activations staged as x * 2^E)
-    f32x4 pl[WV][kTR * 8];          // (scale, bias term) of [row][group] of the wave's unit
-    float red[2][WV][kTR];           // per-wave row sums, double-buffered by tile parity
-    u32x4 zero[WV][4];
-    uint32_t list[kListLds];         // the workgroup's first kListLds schedule entries
-    float ssq[4];                    // sums of squares of the row by the first four waves (RMS-norm prologue)
-};
-
-template <int AUX = 0>
-__device__ __forceinline__ u32x4 buf_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Input prologues of the streaming kernel, applied to 8 bf16 values of the
-// row (t) with the matching 8 values of the prologue operand (w) as they are
-// staged; both are elementwise and written in the same operations as the
-// decode loop's separate kernels (rms_norm_kernel, silu_mul_kernel), so the
-// staged row is bit-identical to the one those write:
-//  - RMS norm: bf16(bf16(x * inv) * w), inv = 1 / sqrt(sum(x^2) / K + eps);
-//  - SiLU gate: bf16(up * bf16(silu(g))), the activation of GatedActMul's SiLU
-//    (crates/stark-engine/src/backends/cpu/kernel/gated_act_mul/gated_act_mul.rs)
-//    with the hardware exp2 and reciprocal in place of expf and a division:
-//    within one bf16 ulp of it (both round the f32 result to bf16).
-// Two f32 values to a bf16 pair (lo, hi), round to nearest even, in one
-// v_cvt_pk_bf16_f32.
-__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
-    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
-    const bf16x2_v v = {(__bf16)lo, (__bf16)hi};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-__device__ __forceinline__ float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
-__device__ __forceinline__ float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
-
-__device__ __forceinline__ u32x4 prologue_norm(u32x4 t, u32x4 w, float inv) {
-    u32x4 o;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t n = bf16_pair(lo_f32(t[q]) * inv, hi_f32(t[q]) * inv);
-        o[q] = bf16_pair(lo_f32(n) * lo_f32(w[q]), hi_f32(n) * hi_f32(w[q]));
+// Schedule of a shape set for `grid` workgroups and tiles of `rows` rows.
+stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid, Schedule* out, hipStream_t stream,
+                              uint32_t rows = kRows) {
+    std::vector<uint32_t> key{grid, rows};
+    for (uint32_t i = 0; i < count; ++i) {
+        key.push_back((ops[i].n + rows - 1) / rows);
+        key.push_back(ops[i].k);
     }
-    return o;
+    return store_schedule(key, grid, [&] { return build_schedule(ops, count, grid, rows); }, out, stream);
 }
 
-// silu(g) = g / (1 + e^-g) with the hardware exp2 and reciprocal
-__device__ __forceinline__ float silu_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
-
-__device__ __forceinline__ u32x4 prologue_silu(u32x4 g, u32x4 u) {
-    u32x4 o;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t sg = bf16_pair(silu_f32(lo_f32(g[q])), silu_f32(hi_f32(g[q])));
-        o[q] = bf16_pair(lo_f32(u[q]) * lo_f32(sg), hi_f32(u[q]) * hi_f32(sg));
-    }
-    return o;
-}
 
 // BF: bf16 planes (else f16); BIASED: bias plane (else symmetric). Both are
 // compile-time so that the per-unit plane conversion is straight-line code.
@@ -897,6 +807,12 @@ stark_qmm_status launch_class(int c, const AffineOp* o, uint32_t n, hipStream_t 
 }
 
 }  // namespace
+
+stark_qmm_status schedule_store(const std::vector<uint32_t>& key, uint32_t grid,
+                                const std::function<std::vector<uint32_t>()>& build, mfma::Schedule* out,
+                                hipStream_t stream) {
+    return store_schedule(key, grid, build, out, stream);
+}
 
 bool mfma_eligible(const AffineOp& o, int bits) {
     if ((bits != 4 && bits != 8) || o.x_dt != STARK_QMM_BF16 || o.gather || o.m == 0 || o.m > 16) return false;

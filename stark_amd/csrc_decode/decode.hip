@@ -649,9 +649,39 @@ __global__ void embed_kernel(const uint16_t* table, const int32_t* token, uint16
     if (i < n) x[i] = table[(size_t)tok * n + i];
 }
 
+// Tagged residual row (bf16 | tag << 16 per word, for chained products):
+// the embedding row of *token with tag ^ ((*seq & 1) << 15).
+__global__ void embed_tagged_kernel(const uint16_t* table, const int32_t* token, uint32_t* x, uint32_t n,
+                                    uint32_t vocab, uint32_t tag, const int32_t* seq) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t tok = min((uint32_t)*token, vocab - 1);
+    const uint32_t t = (tag ^ (((uint32_t)*seq & 1u) << 15)) << 16;
+    if (i < n) x[i] = (uint32_t)table[(size_t)tok * n + i] | t;
+}
+
+// out[i] = bf16 value of tagged word x[i]
+__global__ void untag_kernel(const uint32_t* x, uint16_t* out, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = (uint16_t)(x[i] & 0xffffu);
+}
+
 }  // namespace
 
 extern "C" {
+
+int stark_decode_embed_tagged(const void* table, const int32_t* token, void* x, uint32_t n, uint32_t vocab,
+                              uint32_t tag, const int32_t* seq, void* stream) {
+    if (vocab == 0 || tag == 0 || tag > 0x7fff) return 1;
+    hipLaunchKernelGGL(embed_tagged_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)table, token, (uint32_t*)x, n, vocab, tag, seq);
+    return hipGetLastError() == hipSuccess ? 0 : 10;
+}
+
+int stark_decode_untag(const void* x, void* out, uint32_t n, void* stream) {
+    hipLaunchKernelGGL(untag_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, (const uint32_t*)x,
+                       (uint16_t*)out, n);
+    return hipGetLastError() == hipSuccess ? 0 : 10;
+}
 
 int stark_decode_rms_norm(const void* x, const void* w, void* out, uint32_t n, float eps, void* stream) {
     if (n % 256) return 1;

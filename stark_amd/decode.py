@@ -45,6 +45,8 @@ def lib():
         L.stark_decode_silu_mul.argtypes = [vp, vp, vp, u32, vp]
         L.stark_decode_argmax.argtypes = [vp, u32, ip, ip, ip, u32, vp]
         L.stark_decode_embed.argtypes = [vp, ip, vp, u32, u32, vp]
+        L.stark_decode_embed_tagged.argtypes = [vp, ip, vp, u32, u32, u32, ip, vp]
+        L.stark_decode_untag.argtypes = [vp, vp, u32, vp]
         _LIB = L
     return _LIB
 
@@ -94,16 +96,28 @@ class Qwen3Decoder:
     fused: the attention/MLP RMS norms and the gated SiLU run as input
     prologues of the products that read them (stark_qmm_encode_many_prologue;
     bit-identical rows, three launches fewer per layer). None = whenever the
-    shapes allow it (hidden and intermediate multiples of 4096)."""
+    shapes allow it (hidden and intermediate multiples of 4096).
+
+    chain: a layer's products after attention -- o, gate/up, down (K split in
+    three slices) and the next layer's q/k/v -- run as ONE chained launch
+    (stark_qmm_encode_chain): the residual row and the gate/up rows are kept
+    as tagged words (bf16 | tag << 16) through which the stages hand over
+    inside the launch. Same rows, bit for bit, as the fused form. None =
+    whenever the shapes allow it (hidden 4096 and intermediate a multiple of
+    12288); off by default."""
 
     def __init__(self, cfg: Qwen3Config, capacity: int, seed: int = 0, device: str = "cuda",
-                 fused: Optional[bool] = None):
+                 fused: Optional[bool] = None, chain: bool = False):
         self.cfg, self.cap = cfg, capacity
         H, I, hd = cfg.hidden, cfg.intermediate, cfg.head_dim
         eligible = H % 4096 == 0 and I % 4096 == 0
         if fused and not eligible:
             raise ValueError("the fused prologues need hidden and intermediate sizes that are multiples of 4096")
         self.fused = eligible if fused is None else fused
+        chain_ok = self.fused and H == 4096 and I % 12288 == 0 and (cfg.q_heads + 2 * cfg.kv_heads) * hd % 32 == 0
+        if chain and not chain_ok:
+            raise ValueError("the chained launch needs the fused form, hidden 4096 and intermediate a multiple of 12288")
+        self.chain = bool(chain)
         qd, kd = cfg.q_heads * hd, cfg.kv_heads * hd
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
@@ -142,6 +156,10 @@ class Qwen3Decoder:
         self.u = torch.zeros(I, dtype=bf16, device=dev)
         self.a = torch.zeros(I, dtype=bf16, device=dev)
         self.logits = torch.zeros(cfg.vocab, dtype=torch.float32, device=dev)
+        if self.chain:  # tagged rows of the chained launches
+            self.xt = torch.zeros(H, dtype=torch.int32, device=dev)
+            self.gt = torch.zeros(I, dtype=torch.int32, device=dev)
+            self.ut = torch.zeros(I, dtype=torch.int32, device=dev)
         nch = lib().stark_decode_attn_chunks(capacity)
         self.po = torch.zeros(cfg.q_heads * nch * hd, dtype=torch.float32, device=dev)
         self.pml = torch.zeros(cfg.q_heads * nch * 2, dtype=torch.float32, device=dev)
@@ -161,9 +179,48 @@ class Qwen3Decoder:
                            params=Q.QuantParams(Q.GROUP_OUTPUT, mat["n"], mat["k"] // self.cfg.group)),
             d_transform=Q.MatmulDOps(accumulate=accumulate))
 
+    # tags of the chained form: the embedding row, then per layer i the
+    # residual after o, the gate/up rows, the residual after down
+    TAG_EMBED = 1
+
+    @staticmethod
+    def _tags(i):
+        return 2 + 3 * i, 3 + 3 * i, 4 + 3 * i
+
+    def _prepare_chain(self):
+        K4, eps, L = self.kern4, self.cfg.eps, self.layers
+        CP = Q.ChainProduct
+
+        def qkv(layer, in_tag, stage):
+            return [CP(self._args(layer[w], self.xt, out), stage, Q.PROLOGUE_RMS_NORM, layer["attn_norm"], eps,
+                       in_tag=in_tag) for w, out in (("q", self.q), ("k", self.k), ("v", self.v))]
+
+        self.chain_head = K4.prepare_chain(qkv(L[0], self.TAG_EMBED, 0))
+        self.chains = []
+        for i, layer in enumerate(L):
+            to, tgu, td = self._tags(i)
+            prods = [CP(self._args(layer["o"], self.attn, self.xt, accumulate=True), 0, out_tag=to),
+                     CP(self._args(layer["gate"], self.xt, self.gt), 1, Q.PROLOGUE_RMS_NORM, layer["mlp_norm"], eps,
+                        in_tag=to, out_tag=tgu),
+                     CP(self._args(layer["up"], self.xt, self.ut), 1, Q.PROLOGUE_RMS_NORM, layer["mlp_norm"], eps,
+                        in_tag=to, out_tag=tgu),
+                     CP(self._args(layer["down"], self.gt, self.xt, accumulate=True), 2, Q.PROLOGUE_SILU_GATE, self.ut,
+                        in_tag=tgu, out_tag=td, acc_tag=to, k_slices=self.cfg.intermediate // 4096)]
+            if i + 1 < len(L):
+                prods += qkv(L[i + 1], td, 3)
+            self.chains.append(K4.prepare_chain(prods))
+        need = max(c.workspace_bytes for c in self.chains + [self.chain_head])
+        self.chain_ws = torch.zeros((need + 7) // 8, dtype=torch.int64, device=self.x.device)
+
+    def chain_status(self) -> int:
+        """Non-zero when a wait of a chained launch gave up (rows invalid)."""
+        return int(self.chain_ws[0].item() & 0xffffffff)
+
     def _prepare(self):
         K4 = self.kern4
         self.batches = []
+        if self.chain:
+            self._prepare_chain()
         if self.fused:
             eps = self.cfg.eps
             for L in self.layers:
@@ -211,6 +268,9 @@ class Qwen3Decoder:
         sp = C.c_void_p(s.cuda_stream)
         H, I = cfg.hidden, cfg.intermediate
         p = lambda t: C.c_void_p(t.data_ptr())
+        if self.chain:
+            self._step_chain(D, s, sp, p, t)
+            return
         _ok(D.stark_decode_embed(p(self.embed), p(self.token), p(self.x), H, cfg.vocab, sp), "embed")
         t(-1, "embed")
         for i, (L, B) in enumerate(zip(self.layers, self.batches)):
@@ -244,6 +304,31 @@ class Qwen3Decoder:
                              self.history.numel(), sp),
             "argmax")
 
+    def _step_chain(self, D, s, sp, p, t):
+        """step() of the chained form: embedding (tagged), the first layer's
+        q/k/v, then per layer the attention and one chained launch."""
+        cfg, H = self.cfg, self.cfg.hidden
+        _ok(D.stark_decode_embed_tagged(p(self.embed), p(self.token), p(self.xt), H, cfg.vocab, self.TAG_EMBED,
+                                        p(self.pos), sp), "embed")
+        t(-1, "embed")
+        self.kern4.encode_chain(self.chain_head, self.chain_ws, self.pos, s)
+        t(0, "qkv")
+        for i, L in enumerate(self.layers):
+            _ok(D.stark_decode_attention_fused(p(self.q), p(self.k), p(self.v), p(L["q_norm"]), p(L["k_norm"]),
+                                               p(L["kcache"]), p(L["vcache"]), p(self.po), p(self.pml), p(self.attn),
+                                               p(self.pos), cfg.q_heads, cfg.kv_heads, self.cap, cfg.rope_theta,
+                                               cfg.eps, sp), "attention")
+            t(i, "attention")
+            self.kern4.encode_chain(self.chains[i], self.chain_ws, self.pos, s)
+            t(i, "chain")
+        _ok(D.stark_decode_untag(p(self.xt), p(self.x), H, sp), "untag")
+        _ok(D.stark_decode_rms_norm(p(self.x), p(self.final_norm), p(self.h), H, cfg.eps, sp), "final_norm")
+        t(-1, "final_norm")
+        self.kern_lm.encode_prepared(self.lm_batch, s)
+        t(-1, "lm_head")
+        _ok(D.stark_decode_argmax(p(self.logits), cfg.vocab, p(self.token), p(self.pos), p(self.history),
+                                  self.history.numel(), sp), "argmax")
+
     def capture(self):
         """Capture one token step in a graph (after one eager step has built
         the library's per-shape schedules)."""
@@ -256,3 +341,8 @@ class Qwen3Decoder:
         torch.cuda.current_stream().wait_stream(s)
         self.graph = g
         return g
+
+
+def qmm_untag(words: torch.Tensor) -> torch.Tensor:
+    """bf16 values of a tagged row (the chained form's residual row)."""
+    return Q.untag_rows(words)[0]

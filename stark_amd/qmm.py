@@ -177,6 +177,12 @@ class _Prologue(C.Structure):
 PROLOGUE_NONE, PROLOGUE_RMS_NORM, PROLOGUE_SILU_GATE = 0, 1, 2
 
 
+class _ChainProduct(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("stage", C.c_uint32), ("args", C.POINTER(_Args)),
+                ("prologue", C.c_uint32), ("prologue_data", C.c_void_p), ("eps", C.c_float),
+                ("in_tag", C.c_uint32), ("out_tag", C.c_uint32), ("acc_tag", C.c_uint32), ("k_slices", C.c_uint32)]
+
+
 # Every symbol include/stark_qmm.h declares, with its ctypes signature.
 SIGNATURES = {
     "stark_qmm_abi_version": (C.c_uint32, []),
@@ -187,6 +193,9 @@ SIGNATURES = {
     "stark_qmm_encode_many_prologue": (C.c_uint32, [C.c_void_p, C.POINTER(_Args), C.c_uint32, C.POINTER(_Prologue),
                                                     C.c_void_p]),
     "stark_qmm_set_reference_accumulation": (C.c_uint32, [C.c_void_p, C.c_uint32]),
+    "stark_qmm_chain_workspace_size": (C.c_uint32, [C.POINTER(_ChainProduct), C.c_uint32, C.POINTER(C.c_uint64)]),
+    "stark_qmm_encode_chain": (C.c_uint32, [C.c_void_p, C.POINTER(_ChainProduct), C.c_uint32, C.c_void_p, C.c_void_p,
+                                            C.c_uint64, C.c_void_p]),
     "stark_qmm_destroy": (None, [C.c_void_p]),
     "stark_qmm_mapped_many": (C.c_uint32, [C.POINTER(_MappedOp), C.c_uint32, C.POINTER(C.c_void_p), C.c_void_p]),
     "stark_qmm_mapped_many_async": (C.c_uint32, [C.POINTER(_MappedOp), C.c_uint32, C.POINTER(C.c_void_p),
@@ -402,6 +411,41 @@ class PreparedBatch:
     prologue_data: object = None  # the tensor the prologue reads
 
 
+@dataclass
+class ChainProduct:
+    """One product of a chained launch (stark_qmm_chain_product). Tagged rows
+    are int32 tensors of words bf16 | tag << 16; tag 0 = plain bf16 row."""
+    arguments: MatmulArguments
+    stage: int
+    prologue: int = PROLOGUE_NONE
+    prologue_data: Optional[torch.Tensor] = None
+    eps: float = 0.0
+    in_tag: int = 0
+    out_tag: int = 0
+    acc_tag: int = 0
+    k_slices: int = 1
+
+
+@dataclass
+class PreparedChain:
+    array: object      # ctypes array of stark_qmm_chain_product
+    args: object       # the stark_qmm_args they point to
+    keep: list         # the ChainProducts whose tensors they point into
+    workspace_bytes: int
+
+
+def tag_rows(values: torch.Tensor, tag: int) -> torch.Tensor:
+    """bf16 values -> tagged words (int32): bits | tag << 16."""
+    hi = (int(tag) & 0xffff) << 16
+    return (values.contiguous().view(torch.int16).to(torch.int32) & 0xffff) | (hi - (1 << 32) if hi >= 1 << 31 else hi)
+
+
+def untag_rows(words: torch.Tensor) -> torch.Tensor:
+    """tagged words -> (bf16 values, tags)."""
+    w = words.to(torch.int64) & 0xffffffff
+    return (w & 0xffff).to(torch.int16).view(torch.bfloat16), (w >> 16).to(torch.int32)
+
+
 class MatmulKernel:
     """trait MatmulKernel (kernel.rs:15-79) over stark_qmm_create/encode."""
 
@@ -458,6 +502,25 @@ class MatmulKernel:
                               eps: float = 0.0) -> "PreparedBatch":
         return PreparedBatch((_Args * len(arguments))(*[_args(a) for a in arguments]), list(arguments),
                              self._prologue(kind, data, eps), data)
+
+    def prepare_chain(self, products: Sequence["ChainProduct"]) -> "PreparedChain":
+        """Marshal the products of a chained launch (stark_qmm_encode_chain) once;
+        returns the batch and the workspace bytes it needs."""
+        args = (_Args * len(products))(*[_args(p.arguments) for p in products])
+        arr = (_ChainProduct * len(products))()
+        for i, p in enumerate(products):
+            if p.prologue != PROLOGUE_NONE and (p.prologue_data is None or not p.prologue_data.is_contiguous()):
+                raise ValueError("a prologue needs a contiguous operand")
+            arr[i] = _ChainProduct(C.sizeof(_ChainProduct), p.stage, C.pointer(args[i]), p.prologue,
+                                   _ptr(p.prologue_data), float(p.eps), p.in_tag, p.out_tag, p.acc_tag, p.k_slices)
+        need = C.c_uint64()
+        _check(lib().stark_qmm_chain_workspace_size(arr, len(products), C.byref(need)), "chain_workspace_size")
+        return PreparedChain(arr, args, list(products), need.value)
+
+    def encode_chain(self, chain: "PreparedChain", workspace: torch.Tensor, seq: Optional[torch.Tensor] = None,
+                     stream=None) -> None:
+        _check(lib().stark_qmm_encode_chain(self._h, chain.array, len(chain.keep), _ptr(seq), _ptr(workspace),
+                                            _nbytes(workspace), _stream(stream)), "encode_chain")
 
     def close(self) -> None:
         if getattr(self, "_h", None):

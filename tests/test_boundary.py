@@ -197,3 +197,49 @@ def test_mapped_many_validation_without_device():
     assert lib.stark_qmm_mapped_many_async(op, 1, outs, C.c_void_p(0x6000), None) == qmm.UNSUPPORTED
     assert lib.stark_qmm_mapped_many_async(op, 0, outs, C.c_void_p(0x6000), None) == qmm.INVALID_ARGUMENT
     assert lib.stark_qmm_mapped_many_async(op, 65, outs, C.c_void_p(0x6000), None) == qmm.INVALID_ARGUMENT
+
+
+
+def _chain_product(qmm, n, k, stage=0, prologue=0, in_tag=0, out_tag=0, acc_tag=0, k_slices=1):
+    """A chained product over fake (aligned, never dereferenced) addresses."""
+    a = qmm._Args()
+    a.struct_size = C.sizeof(qmm._Args)
+    a.a, a.d = 0x10000, 0x20000
+    a.b.codes, a.b.codes_size = 0x30000, n * k // 2
+    a.b.scales, a.b.correction_data = 0x40000, 0x50000
+    a.b.correction = 1  # biases
+    a.b.params.layout, a.b.params.row_count, a.b.params.group_count = qmm.GROUP_OUTPUT, n, k // 64
+    a.b.mode, a.b.group_size = qmm.MODE_U4, 64
+    a.b_transpose = 1
+    a.d_ops.ab_scale = 1.0
+    a.m, a.n, a.k = 1, n, k
+    p = qmm._ChainProduct(C.sizeof(qmm._ChainProduct), stage, C.pointer(a), prologue, 0x60000 if prologue else 0,
+                          1e-6, in_tag, out_tag, acc_tag, k_slices)
+    return p, a
+
+
+def _chain_bytes(qmm, *prods):
+    arr = (qmm._ChainProduct * len(prods))(*[p for p, _ in prods])
+    need = C.c_uint64()
+    st = qmm.lib().stark_qmm_chain_workspace_size(arr, len(prods), C.byref(need))
+    return st, need.value
+
+
+def test_chain_validation_on_host():
+    """stark_qmm_chain_workspace_size validates a chain without a device:
+    the workspace of a 3-slice product, and the shapes, tags and stage order
+    it refuses (STARK_QMM_UNSUPPORTED = 8, STARK_QMM_INVALID_ARGUMENT = 1)."""
+    from stark_amd import qmm
+    qmm.lib()
+    assert qmm.PROLOGUE_SILU_GATE == 2
+    down = dict(n=4096, k=12288, prologue=2, in_tag=3, out_tag=4, k_slices=3)
+    assert _chain_bytes(qmm, _chain_product(qmm, **down)) == (0, 256 + 2 * 4096 * 8)
+    assert _chain_bytes(qmm, _chain_product(qmm, **{**down, "k_slices": 1})) == (0, 256)
+    for bad in (dict(out_tag=0), dict(k_slices=5), dict(in_tag=0x8000), dict(k_slices=1, out_tag=0, acc_tag=2),
+                dict(prologue=1)):
+        st, _ = _chain_bytes(qmm, _chain_product(qmm, **{**down, **bad}))
+        assert st == 8, bad
+    assert _chain_bytes(qmm, _chain_product(qmm, 4096 + 16, 4096))[0] == 8  # N % 32
+    assert _chain_bytes(qmm, _chain_product(qmm, 4096, 2048))[0] == 8       # K % 4096
+    st, _ = _chain_bytes(qmm, _chain_product(qmm, 4096, 4096, stage=1), _chain_product(qmm, 4096, 4096, stage=0))
+    assert st == 1  # stages must not decrease
