@@ -37,6 +37,19 @@ LAYERS = 36
 SEED = 20261201
 
 
+
+# Secondary lines: printed one per line when a config is run on its own; in the
+# default run they are collected and attached to the headline line instead
+# (bench.py prints one JSON line).
+SINK = None
+
+
+def emit(d):
+    if SINK is not None:
+        SINK.append(d)
+    else:
+        print(json.dumps(d))
+
 def quantize_gpu(w, group=GROUP):
     """MLX affine quantization on the GPU (data generation only): per group
     scale=(max-min)/15, bias=min as bf16; q=clamp(round((w-bias)/scale)).
@@ -345,9 +358,48 @@ def config1(args, torch, Q):
     if decode is not None:
         line["config"]["decode_tokens_per_s"] = decode["tokens_per_s"]
         line["config"]["decode"] = decode
+    if args.headline_only:
+        print(json.dumps(line))
+        if args.verify:
+            verify_lines(args, torch, Q, gen, kern, layers, stream)
+        return
+    # The other configurations, measured in the same run and attached to this
+    # line (one line per run): verify M = 2..16, config 2, config 3, config 4
+    # prefill (bf16 and int8 activations). Each is summarised; a failure is
+    # recorded in place of its figures and does not stop the run.
+    global SINK
+    SINK = []
+    others = []
+
+    def collect(what, fn):
+        del SINK[:]
+        t0 = time.time()
+        try:
+            fn()
+            for d in SINK:
+                rf = d.get("roofline") or {}
+                others.append({"metric": d["metric"], "value": d["value"], "unit": d["unit"],
+                               "ms_per_step": d.get("ms_per_step"), "steps": d.get("steps"),
+                               "workload": d.get("config", {}).get("workload"),
+                               "roofline_frac": rf.get("frac"), "wall_s": round(time.time() - t0, 1)})
+        except Exception as e:  # recorded, not fatal: the headline figures above stand
+            others.append({"metric": what, "error": f"{type(e).__name__}: {e}"[:300]})
+        print(f"bench: {what} done in {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
+
+    collect("config 1 verify M=2,4,8,16", lambda: verify_lines(args, torch, Q, gen, kern, layers, stream))
+    del all_args, layers, outs
+    torch.cuda.empty_cache()
+    sub = argparse.Namespace(**{**vars(args), "steps": 200, "warmup": 40, "decode_tokens": 0})
+    collect("config 2", lambda: config2(sub, torch, Q))
+    torch.cuda.empty_cache()
+    collect("config 3", lambda: config3(sub, torch, Q))
+    torch.cuda.empty_cache()
+    collect("config 4 prefill", lambda: config4(argparse.Namespace(**{**vars(sub), "steps": 20, "warmup": 3}),
+                                                torch, Q))
+    torch.cuda.empty_cache()
+    SINK = None
+    line["other_configs"] = others
     print(json.dumps(line))
-    if args.verify:
-        verify_lines(args, torch, Q, gen, kern, layers, stream)
 
 
 def verify_lines(args, torch, Q, gen, kern, layers, stream):
@@ -372,7 +424,7 @@ def verify_lines(args, torch, Q, gen, kern, layers, stream):
                    args.warmup, stream)
         nbytes = algorithmic_bytes(m)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        print(json.dumps({"metric": f"q4 matvec HBM GB/s at M={m} (speculative verify)", "value": round(gbs, 1),
+        emit({"metric": f"q4 matvec HBM GB/s at M={m} (speculative verify)", "value": round(gbs, 1),
                           "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
                           "vs_baseline": None, "dtype": "bf16",
@@ -383,7 +435,7 @@ def verify_lines(args, torch, Q, gen, kern, layers, stream):
                                      "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
                                      "tokens_per_s": round(m * 1000.0 / ms, 1)},
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                                       "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+                                       "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
 
 
 def clock_ramp(torch, step, seconds=0.4):
@@ -505,7 +557,7 @@ def config2(args, torch, Q):
             del views, preps
     for name, m, ms, nbytes, copies, wbytes, ran in lines:
         gbs = nbytes / (ms * 1e-3) / 1e9
-        print(json.dumps({"metric": f"{name} matvec HBM GB/s", "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        emit({"metric": f"{name} matvec HBM GB/s", "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
                           "steps": ran, "warmup": copies, "ms_per_step": round(ms, 5),
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                           "dtype": "u8" if "u8" in name else "f32",
@@ -515,7 +567,7 @@ def config2(args, torch, Q):
                                                  f"over the copies, replayed",
                                      "bytes_per_step": nbytes, "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)},
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+                                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
 
 
 def config3(args, torch, Q):
@@ -573,7 +625,7 @@ def config3(args, torch, Q):
         u = sum(uniq) / len(uniq)
         nbytes = u * per_expert + E * Hm * 2 + T * Hm * 2 * 2 + T * E * 4
         gbs = nbytes / (ms * 1e-3) / 1e9
-        print(json.dumps({"metric": "Qwen3-30B-A3B MoE layer decode HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
+        emit({"metric": "Qwen3-30B-A3B MoE layer decode HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
                           "n_gpus": 1, "steps": ran, "warmup": copies, "ms_per_step": round(ms, 5),
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                           "data": "synthetic: N(0,0.02) weights W4 g64 (MLX affine rule), N(0,1) hidden states",
@@ -584,7 +636,7 @@ def config3(args, torch, Q):
                                      "tokens_per_s": round(T * 1000.0 / ms, 1),
                                      "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)},
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+                                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
 
 
 PEAK_MFMA_INT8_TOPS = 5000.0
@@ -612,7 +664,7 @@ def config4(args, torch, Q):
     ms = timed(torch, lambda i: kern.encode_prepared(batch, stream), args.steps, args.warmup, stream)
     flops = sum(2 * Mtok * n * k for _, n, k in SHAPES)
     tf = flops / (ms * 1e-3) / 1e12
-    print(json.dumps({"metric": "Qwen3-8B W4 prefill dequant-GEMM TFLOP/s", "value": round(tf, 1), "unit": "TFLOP/s",
+    emit({"metric": "Qwen3-8B W4 prefill dequant-GEMM TFLOP/s", "value": round(tf, 1), "unit": "TFLOP/s",
                       "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
                       "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                       "data": "synthetic: N(0,0.02) weights W4 g64 (MLX affine rule), N(0,1) bf16 activations",
@@ -621,7 +673,7 @@ def config4(args, torch, Q):
                                      round(Mtok * 1000.0 / (ms * LAYERS), 1)},
                       "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_MFMA_BF16_TFLOPS,
                                    "unit": "TFLOP/s", "frac": round(tf / PEAK_MFMA_BF16_TFLOPS, 4),
-                                   "traffic": None}}))
+                                   "traffic": None}})
     a8_prefill_line(args, torch, Q, layer, stream)
     if args.decode_tokens:
         decode_line(args, torch)
@@ -655,7 +707,7 @@ def a8_prefill_line(args, torch, Q, layer, stream):
     ms = timed(torch, lambda i: kern.encode_prepared(batch, stream), args.steps, args.warmup, stream)
     ops = sum(2 * Mtok * n * k for _, n, k in SHAPES)
     tops = ops / (ms * 1e-3) / 1e12
-    print(json.dumps({"metric": "Qwen3-8B A8W4 prefill int8 GEMM TOP/s", "value": round(tops, 1), "unit": "TOP/s",
+    emit({"metric": "Qwen3-8B A8W4 prefill int8 GEMM TOP/s", "value": round(tops, 1), "unit": "TOP/s",
                       "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
                       "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
                       "data": "synthetic: N(0,0.02) weights W4 g64, N(0,1) activations RHT-quantized to int8 "
@@ -666,7 +718,7 @@ def a8_prefill_line(args, torch, Q, layer, stream):
                                      round(Mtok * 1000.0 / (ms * LAYERS), 1)},
                       "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": PEAK_MFMA_INT8_TOPS,
                                    "unit": "TOP/s", "frac": round(tops / PEAK_MFMA_INT8_TOPS, 4),
-                                   "traffic": None}}))
+                                   "traffic": None}})
 
 
 def decode_measure(args, torch):
@@ -730,7 +782,7 @@ def decode_measure(args, torch):
 def decode_line(args, torch):
     d = decode_measure(args, torch)
     gbs = d["achieved_gbs"]
-    print(json.dumps({"metric": "Qwen3-8B W4 end-to-end greedy decode tokens/s", "value": d["tokens_per_s"],
+    emit({"metric": "Qwen3-8B W4 end-to-end greedy decode tokens/s", "value": d["tokens_per_s"],
                       "unit": "tokens/s", "n_gpus": 1, "steps": d["timed_tokens"], "warmup": 4,
                       "ms_per_step": d["ms_per_token"], "higher_is_better": True, "scaling": "weak",
                       "vs_baseline": None, "dtype": "bf16",
@@ -739,7 +791,7 @@ def decode_line(args, torch):
                       "config": {"workload": d["workload"],
                                  "hbm_bytes_per_token_algorithmic": d["hbm_bytes_per_token_algorithmic"]},
                       "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
 
 
 def attention_line(args, torch):
@@ -782,7 +834,7 @@ def attention_line(args, torch):
     used = (ctx + 1 + 63) // 64
     nbytes = 2 * kvh * (ctx + 1) * hd * 2 + 2 * qh * used * (hd + 2) * 4 + qh * hd * 2 * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
-    print(json.dumps({"metric": "decode attention pair (fused partials + combine) HBM GB/s", "value": round(gbs, 1),
+    emit({"metric": "decode attention pair (fused partials + combine) HBM GB/s", "value": round(gbs, 1),
                       "unit": "GB/s", "n_gpus": 1, "steps": ran, "warmup": layers, "ms_per_step": round(ms, 5),
                       "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                       "data": "synthetic: N(0,1) K/V caches and q/k/v rows",
@@ -790,7 +842,7 @@ def attention_line(args, torch):
                                              f"{layers} rotating layer caches, one captured HIP graph over them",
                                  "bytes_per_step": nbytes},
                       "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}))
+                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
 
 
 def main():
@@ -806,6 +858,9 @@ def main():
                     help="configs 1 and 4: greedy tokens generated after the 4096-token context in the end-to-end "
                          "decode measurement (0 skips it)")
     ap.add_argument("--decode-only", action="store_true", help="only the end-to-end decode line (config 4)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="config 1: print the headline line alone (the default run also measures verify M=2..16, "
+                         "configs 2 and 3 and the config-4 prefill and attaches them as other_configs)")
     ap.add_argument("--decode-form", choices=("chain", "fused"), default="fused",
                     help="decode stand-in: products after attention as one chained launch per layer (chain) or one "
                          "launch per product with norm/SiLU prologues (fused)")
