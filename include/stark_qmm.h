@@ -243,9 +243,10 @@ STARK_QMM_API stark_qmm_status stark_qmm_encode_many_prologue(stark_qmm_kernel* 
  * differs between the calls (it flips bit 15 of every tag; NULL = no flip).
  *
  * k_slices > 1 splits the product's K into that many slices of 4096 whose row
- * sums meet in the workspace and are added in slice order (bit-identical to
- * stark_qmm_encode_many_prologue for K = 12288 and 3 slices); it needs a
- * tagged output. Requirements: BF16 input/output/planes with biases, M = 1,
+ * sums meet in the workspace as words tagged part_tag (same rule as the row
+ * tags) and are added in slice order (bit-identical to
+ * stark_qmm_encode_many_prologue for K = 12288 and 3 slices); d may then be
+ * plain or tagged. Requirements: BF16 input/output/planes with biases, M = 1,
  * 4-bit codes, group 64, K % 4096 == 0 (the RMS-norm prologue: K == 4096),
  * N % 32 == 0, no gather, bias, soft cap or RHT; at most 16 tiles lists
  * (products plus extra slices). Otherwise STARK_QMM_UNSUPPORTED.
@@ -264,6 +265,7 @@ typedef struct stark_qmm_chain_product {
     uint32_t in_tag, out_tag;     /* 0 = plain bf16 row */
     uint32_t acc_tag;             /* tagged d with accumulate: tag d carries before it is read (0: at launch) */
     uint32_t k_slices;            /* 0 or 1: whole K */
+    uint32_t part_tag;            /* k_slices > 1: tag of the slices' partial sums (1..0x7fff) */
 } stark_qmm_chain_product;
 
 /* Workspace bytes stark_qmm_encode_chain needs for these products. */

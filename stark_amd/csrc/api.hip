@@ -392,7 +392,7 @@ static stark_qmm_status chain_validate(const stark_qmm_chain_product* p, uint32_
             a->b.group_size != 64 || a->k == 0 || a->k % 4096 || a->n == 0 || a->n % 32 || a->gather_indices ||
             a->d_ops.bias || a->d_ops.rht_factors || a->d_ops.has_soft_cap || a->b.params.materialize_affine_input_sum ||
             a->b.correction != STARK_QMM_CORRECTION_BIASES || (a->k / 4096) % sl || p[i].in_tag > 0x7fff ||
-            p[i].out_tag > 0x7fff || p[i].acc_tag > 0x7fff || (sl > 1 && !p[i].out_tag) ||
+            p[i].out_tag > 0x7fff || p[i].acc_tag > 0x7fff || p[i].part_tag > 0x7fff || (sl > 1 && !p[i].part_tag) ||
             (p[i].acc_tag && !p[i].out_tag) || p[i].prologue > STARK_QMM_PROLOGUE_SILU_GATE ||
             (p[i].prologue == STARK_QMM_PROLOGUE_RMS_NORM && a->k != 4096))
             return STARK_QMM_UNSUPPORTED;
@@ -463,6 +463,7 @@ stark_qmm_status stark_qmm_encode_chain(stark_qmm_kernel* kr, const stark_qmm_ch
             c.in_tag = p[i].in_tag;
             c.out_tag = p[i].out_tag;
             c.acc_tag = p[i].acc_tag;
+            c.part_tag = p[i].part_tag;
             c.flags = op.flags & (FLAG_ACCUMULATE | FLAG_SIGNED);
             c.order = 2 * p[i].stage;
             if (sl == 1) {

@@ -26,7 +26,7 @@
 //
 // Deep products are split in K into slices of 4096 (one tile of a slice per
 // workgroup, four units); the slices before the last write raw row sums as
-// 64-bit (tag << 32 | f32) words, and the last slice's tile adds them in slice
+// 64-bit (part_tag << 32 | f32) words, and the last slice's tile adds them in slice
 // order, ((p0 + p1) + p2), the order in which the one-launch kernel's twelve
 // waves add their units' sums, before the D-ops.
 //
@@ -373,15 +373,11 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 const uint32_t n = n0 + tid;
                 const bool own = n >= t0;  // rows of the previous tile (shifted last tile) are not written again
                 float o = (lds.red[par][0][tid] + lds.red[par][1][tid]) + (lds.red[par][2][tid] + lds.red[par][3][tid]);
-                const uint32_t out_tag = op.out_tag ^ flip;
+                const uint32_t out_tag = op.out_tag ^ flip, part_tag = op.part_tag ^ flip;
                 if (op.out == CHAIN_OUT_PARTIAL) {
                     if (own)
-                        __hip_atomic_store(op.part + n, ((uint64_t)out_tag << 32) | __float_as_uint(o),
+                        __hip_atomic_store(op.part + n, ((uint64_t)part_tag << 32) | __float_as_uint(o),
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else if (op.out == CHAIN_OUT_PLAIN) {
-                    o *= op.ab_scale;
-                    if (op.flags & FLAG_ACCUMULATE) o += bf16_bits_to_f32(((const uint16_t*)op.d)[n]);
-                    if (own) ((uint16_t*)op.d)[n] = f32_to_bf16_bits(o);
                 } else {
                     if (op.out == CHAIN_OUT_COMBINE) {
                         uint64_t w[8];
@@ -394,7 +390,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                         rd();
                         for (uint32_t spins = 0; !gave_up;) {
                             bool ok = true;
-                            for (uint32_t j = 0; j < np; ++j) ok = ok && (uint32_t)(w[j] >> 32) == out_tag;
+                            for (uint32_t j = 0; j < np; ++j) ok = ok && (uint32_t)(w[j] >> 32) == part_tag;
                             if (wave_all(ok)) break;
                             if (++spins > kSpinLimit) {
                                 give_up();
@@ -408,26 +404,31 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                         o = t + o;
                     }
                     o *= op.ab_scale;
-                    uint32_t* dw = (uint32_t*)op.d;
-                    if (op.flags & FLAG_ACCUMULATE) {
-                        uint32_t a = __hip_atomic_load(dw + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        if (op.acc_tag) {
-                            const uint32_t want = op.acc_tag ^ flip;
-                            for (uint32_t spins = 0; !gave_up;) {
-                                if (wave_all((a >> 16) == want)) break;
-                                if (++spins > kSpinLimit) {
-                                    give_up();
-                                    break;
+                    if (!op.out_tag) {  // plain bf16 d (ready at launch when accumulated)
+                        if (op.flags & FLAG_ACCUMULATE) o += bf16_bits_to_f32(((const uint16_t*)op.d)[n]);
+                        if (own) ((uint16_t*)op.d)[n] = f32_to_bf16_bits(o);
+                    } else {
+                        uint32_t* dw = (uint32_t*)op.d;
+                        if (op.flags & FLAG_ACCUMULATE) {
+                            uint32_t a = __hip_atomic_load(dw + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            if (op.acc_tag) {
+                                const uint32_t want = op.acc_tag ^ flip;
+                                for (uint32_t spins = 0; !gave_up;) {
+                                    if (wave_all((a >> 16) == want)) break;
+                                    if (++spins > kSpinLimit) {
+                                        give_up();
+                                        break;
+                                    }
+                                    __builtin_amdgcn_s_sleep(2);
+                                    a = __hip_atomic_load(dw + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                                 }
-                                __builtin_amdgcn_s_sleep(2);
-                                a = __hip_atomic_load(dw + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             }
+                            o += bf16_bits_to_f32(a & 0xffffu);
                         }
-                        o += bf16_bits_to_f32(a & 0xffffu);
+                        if (own)
+                            __hip_atomic_store(dw + n, (uint32_t)f32_to_bf16_bits(o) | (out_tag << 16),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
-                    if (own)
-                        __hip_atomic_store(dw + n, (uint32_t)f32_to_bf16_bits(o) | (out_tag << 16), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
             par ^= 1;

@@ -128,10 +128,10 @@ __device__ __forceinline__ u32x4 prologue_silu(u32x4 g, u32x4 u) {
 // that the producer writes through to the device-coherent level and the
 // consumer polls until every word it needs carries the expected tag.
 enum : uint32_t {
-    CHAIN_OUT_PLAIN = 0,    // d in the kernel's output type (ready after the launch)
+    CHAIN_OUT_PLAIN = 0,    // d plain bf16 (ready after the launch)
     CHAIN_OUT_TAGGED = 1,   // d tagged
-    CHAIN_OUT_PARTIAL = 2,  // K slice: raw row sums as (tag << 32 | f32 bits) into part
-    CHAIN_OUT_COMBINE = 3,  // last K slice: adds the nparts earlier slices' sums, then as TAGGED
+    CHAIN_OUT_PARTIAL = 2,  // K slice: raw row sums as (part_tag << 32 | f32 bits) into part
+    CHAIN_OUT_COMBINE = 3,  // last K slice: adds the nparts earlier slices' sums, then d plain or tagged
 };
 
 struct ChainOp {
@@ -146,7 +146,8 @@ struct ChainOp {
     float ab_scale, eps;
     uint32_t pro;          // STARK_QMM_PROLOGUE_*
     uint32_t in_tag;       // 0: x (and a gate's up row) plain, ready at launch; else the tag to wait for
-    uint32_t out, out_tag; // CHAIN_OUT_*; tag written (TAGGED, PARTIAL, COMBINE)
+    uint32_t out, out_tag; // CHAIN_OUT_*; tag written to d (0: d plain)
+    uint32_t part_tag;     // tag of the K slices' partial words (PARTIAL, COMBINE)
     uint32_t acc_tag;      // accumulate into tagged d: 0 = d ready at launch, else the tag d must carry first
     uint32_t nparts;       // COMBINE: earlier slices
     uint32_t flags;        // FLAG_ACCUMULATE, FLAG_SIGNED

@@ -180,7 +180,8 @@ PROLOGUE_NONE, PROLOGUE_RMS_NORM, PROLOGUE_SILU_GATE = 0, 1, 2
 class _ChainProduct(C.Structure):
     _fields_ = [("struct_size", C.c_uint32), ("stage", C.c_uint32), ("args", C.POINTER(_Args)),
                 ("prologue", C.c_uint32), ("prologue_data", C.c_void_p), ("eps", C.c_float),
-                ("in_tag", C.c_uint32), ("out_tag", C.c_uint32), ("acc_tag", C.c_uint32), ("k_slices", C.c_uint32)]
+                ("in_tag", C.c_uint32), ("out_tag", C.c_uint32), ("acc_tag", C.c_uint32), ("k_slices", C.c_uint32),
+                ("part_tag", C.c_uint32)]
 
 
 # Every symbol include/stark_qmm.h declares, with its ctypes signature.
@@ -424,6 +425,7 @@ class ChainProduct:
     out_tag: int = 0
     acc_tag: int = 0
     k_slices: int = 1
+    part_tag: int = 0
 
 
 @dataclass
@@ -512,7 +514,8 @@ class MatmulKernel:
             if p.prologue != PROLOGUE_NONE and (p.prologue_data is None or not p.prologue_data.is_contiguous()):
                 raise ValueError("a prologue needs a contiguous operand")
             arr[i] = _ChainProduct(C.sizeof(_ChainProduct), p.stage, C.pointer(args[i]), p.prologue,
-                                   _ptr(p.prologue_data), float(p.eps), p.in_tag, p.out_tag, p.acc_tag, p.k_slices)
+                                   _ptr(p.prologue_data), float(p.eps), p.in_tag, p.out_tag, p.acc_tag, p.k_slices,
+                                   p.part_tag)
         need = C.c_uint64()
         _check(lib().stark_qmm_chain_workspace_size(arr, len(products), C.byref(need)), "chain_workspace_size")
         return PreparedChain(arr, args, list(products), need.value)

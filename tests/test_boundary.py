@@ -200,7 +200,7 @@ def test_mapped_many_validation_without_device():
 
 
 
-def _chain_product(qmm, n, k, stage=0, prologue=0, in_tag=0, out_tag=0, acc_tag=0, k_slices=1):
+def _chain_product(qmm, n, k, stage=0, prologue=0, in_tag=0, out_tag=0, acc_tag=0, k_slices=1, part_tag=0):
     """A chained product over fake (aligned, never dereferenced) addresses."""
     a = qmm._Args()
     a.struct_size = C.sizeof(qmm._Args)
@@ -214,7 +214,7 @@ def _chain_product(qmm, n, k, stage=0, prologue=0, in_tag=0, out_tag=0, acc_tag=
     a.d_ops.ab_scale = 1.0
     a.m, a.n, a.k = 1, n, k
     p = qmm._ChainProduct(C.sizeof(qmm._ChainProduct), stage, C.pointer(a), prologue, 0x60000 if prologue else 0,
-                          1e-6, in_tag, out_tag, acc_tag, k_slices)
+                          1e-6, in_tag, out_tag, acc_tag, k_slices, part_tag)
     return p, a
 
 
@@ -232,10 +232,10 @@ def test_chain_validation_on_host():
     from stark_amd import qmm
     qmm.lib()
     assert qmm.PROLOGUE_SILU_GATE == 2
-    down = dict(n=4096, k=12288, prologue=2, in_tag=3, out_tag=4, k_slices=3)
+    down = dict(n=4096, k=12288, prologue=2, in_tag=3, out_tag=4, k_slices=3, part_tag=4)
     assert _chain_bytes(qmm, _chain_product(qmm, **down)) == (0, 256 + 2 * 4096 * 8)
     assert _chain_bytes(qmm, _chain_product(qmm, **{**down, "k_slices": 1})) == (0, 256)
-    for bad in (dict(out_tag=0), dict(k_slices=5), dict(in_tag=0x8000), dict(k_slices=1, out_tag=0, acc_tag=2),
+    for bad in (dict(part_tag=0), dict(part_tag=0x8000), dict(k_slices=5), dict(in_tag=0x8000), dict(k_slices=1, out_tag=0, acc_tag=2),
                 dict(prologue=1)):
         st, _ = _chain_bytes(qmm, _chain_product(qmm, **{**down, **bad}))
         assert st == 8, bad

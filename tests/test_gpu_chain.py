@@ -74,7 +74,7 @@ def _chain_products(Q, L, xt, gt, ut, attn, q, k, v, tags, eps=1e-6, slices=3):
             CP(_args(Q, L["gate"], xt, gt), 1, Q.PROLOGUE_RMS_NORM, L["mlp_norm"], eps, in_tag=to, out_tag=tgu),
             CP(_args(Q, L["up"], xt, ut), 1, Q.PROLOGUE_RMS_NORM, L["mlp_norm"], eps, in_tag=to, out_tag=tgu),
             CP(_args(Q, L["down"], gt, xt, accumulate=True), 2, Q.PROLOGUE_SILU_GATE, ut, in_tag=tgu, out_tag=td,
-               acc_tag=to, k_slices=slices),
+               acc_tag=to, k_slices=slices, part_tag=td),
             CP(_args(Q, L["q"], xt, q), 3, Q.PROLOGUE_RMS_NORM, L["next_norm"], eps, in_tag=td),
             CP(_args(Q, L["k"], xt, k), 3, Q.PROLOGUE_RMS_NORM, L["next_norm"], eps, in_tag=td),
             CP(_args(Q, L["v"], xt, v), 3, Q.PROLOGUE_RMS_NORM, L["next_norm"], eps, in_tag=td)]
@@ -120,6 +120,34 @@ def test_chain_layer_matches_separate_launches(qmm, D):
         assert torch.all((parts >> 32) & 0xffffffff == (4 ^ flip))
 
 
+def test_chain_down_slices_plain_rows_match_single_launch(qmm, D):
+    """The fused decoder's down product: three K slices of one chained launch
+    on plain bf16 rows (SiLU-gate prologue, accumulate into the residual),
+    against stark_qmm_encode_many_prologue's one launch: the same bits, on two
+    calls with the tag parity flipped between them."""
+    Q = qmm
+    L, x0, attn = _layer(D, 8)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(9)
+    g = torch.randn(I, generator=gen, device="cuda").to(torch.bfloat16)
+    u = torch.randn(I, generator=gen, device="cuda").to(torch.bfloat16)
+    K = Q.MatmulKernel(Q.BF16, Q.BF16, Q.BF16)
+    want = x0.clone()
+    K.encode_many_prologue([_args(Q, L["down"], g, want, accumulate=True)], Q.PROLOGUE_SILU_GATE, u)
+    x = x0.clone()
+    chain = K.prepare_chain([Q.ChainProduct(_args(Q, L["down"], g, x, accumulate=True), 0, Q.PROLOGUE_SILU_GATE, u,
+                                            k_slices=3, part_tag=7)])
+    ws = torch.zeros(chain.workspace_bytes // 8, dtype=torch.int64, device="cuda")
+    seq = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for call in range(2):
+        seq.fill_(call)
+        x.copy_(x0)
+        K.encode_chain(chain, ws, seq)
+        torch.cuda.synchronize()
+        assert int(ws[0].item()) == 0
+        assert _same(x, want)
+
+
 def test_chain_waits_on_stale_tags_give_up_and_flag(qmm, D):
     """A consumer whose tag never arrives (here: the o stage is told to write
     tag 2 but the gate/up stage waits for tag 9) gives up after its bounded
@@ -148,7 +176,7 @@ def test_chain_rejects(qmm, D):
     q, k, v = (torch.zeros(n, dtype=torch.bfloat16, device="cuda") for n in (QD, KD, KD))
     base = lambda: _chain_products(Q, L, xt, gt, ut, attn, q, k, v, (2, 3, 4))
     p = base()
-    p[3].out_tag = 0  # K slices need a tagged output
+    p[3].part_tag = 0  # K slices need a partial-sum tag
     with pytest.raises(Q.MatmulError):
         K.prepare_chain(p)
     p = base()
