@@ -325,10 +325,13 @@ stark_qmm_status schedule_for(const AffineOp* ops, uint32_t count, uint32_t grid
 // workgroups per CU; 12: one workgroup of three waves per SIMD, for launches
 // of 12288-deep products with fewer tiles than CUs, whose tiles then keep
 // three times the loads in flight).
-template <bool SIGNED, bool BF, bool BIASED, int PRO = STARK_QMM_PROLOGUE_NONE, int WV = 4>
+template <bool SIGNED, bool BF, bool BIASED, int PRO = STARK_QMM_PROLOGUE_NONE, int WV = 4, int TR = kTR>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4 ? 2 : WV / 4))) void qmv_stream(
     AffineBatch batch, Schedule sched) {
     (void)batch;
+    static_assert(TR == 32 || TR == 16, "tile rows");
+    constexpr int NS = TR / 8;             // 8-row subtiles of a tile
+    constexpr int NSTEP = 4 * NS;          // steps of a unit: 4 k blocks x NS subtiles
     constexpr uint32_t UB = kUnitK / 2;    // bytes of a row per unit
     constexpr uint32_t OOB = 0x80000000u;  // buffer offset past every resource: reads zero, no traffic
     constexpr uint32_t PLANE = 0x7fffffffu;  // plane resources: addressed by the op's strides
@@ -352,7 +355,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
                                            : ((cu32*)sched.tiles)[t];
     };
     const auto tile_row = [&](const AffineOp& op, uint32_t e) {  // first bank row of the tile
-        return min((e & 0xffffffu) * kTR, op.n - kTR);
+        return min((e & 0xffffffu) * TR, op.n - TR);
     };
 
     // RMS-norm prologue. The sum of squares runs in chunk-major order: the
@@ -397,18 +400,19 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
             pv[0] = buf_load(pr, xo);
             pv[1] = buf_load(pr, xo + 1024);
         }
-        // group-output [G][N4]: lane = (group, quarter of the 32 rows);
-        // output-group [N][G]: lane = (row, half of the 16 groups)
-        const size_t off = op.os == 1 ? (size_t)(c * 16 + ((lane >> 2) & 15)) * op.gs + n0 + 8 * (lane & 3)
-                                      : (size_t)(n0 + ((lane >> 1) & 31)) * op.os + c * 16 + 8 * (lane & 1);
+        // group-output [G][N4]: lane = (group, 8-row part of the TR rows);
+        // output-group [N][G]: lane = (row, half of the 16 groups); with
+        // 16-row tiles lanes 32..63 repeat lanes 0..31
+        const size_t off = op.os == 1 ? (size_t)(c * 16 + ((lane / NS) & 15)) * op.gs + n0 + 8 * (lane % NS)
+                                      : (size_t)(n0 + ((lane >> 1) & (TR - 1))) * op.os + c * 16 + 8 * (lane & 1);
         pls = buf_load(rsrc(op.scales, PLANE), (uint32_t)off * 2);
         plb = buf_load(rsrc(op.corr, PLANE), BIASED ? (uint32_t)off * 2 : OOB);
     };
     const auto code_rsrc = [&](const AffineOp& op, uint32_t n0) {
-        return rsrc(op.codes + (size_t)n0 * (op.k / 2), kTR * (op.k / 2));
+        return rsrc(op.codes + (size_t)n0 * (op.k / 2), TR * (op.k / 2));
     };
-    // step v of a unit: k block v / 4 of subtile v % 4
-    const auto step_soff = [&](const AffineOp& op, int v) { return (uint32_t)(8 * (v % 4)) * (op.k / 2) + (v / 4) * 128; };
+    // step v of a unit: k block v / NS of subtile v % NS
+    const auto step_soff = [&](const AffineOp& op, int v) { return (uint32_t)(8 * (v % NS)) * (op.k / 2) + (v / NS) * 128; };
 
     uint32_t i = lo, ri = 0, e = ((cu32*)sched.tiles)[lo];
     const AffineOp* opp = &kb_->op[e >> 24];
@@ -473,12 +477,12 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
         inv = 1.0f / sqrtf((lds.ssq[0] + lds.ssq[1] + lds.ssq[2] + lds.ssq[3]) / (float)opp->k + kb_->pro_eps);
     uint32_t tg0 = ~0u, tg1 = ~0u, tg2 = ~0u;  // (op << 16 | chunk) held by each activation region
     const auto tag_of = [&](uint32_t rg) { return rg == 0 ? tg0 : rg == 1 ? tg1 : tg2; };
-    f32x4 acc[4] = {};
+    f32x4 acc[NS] = {};
     uint32_t par = 0;
     for (;;) {
         const AffineOp& op = *opp;
         const uint32_t R = op.k / (WV * kUnitK);
-        const uint32_t t0 = (e & 0xffffffu) * kTR, n0 = min(t0, op.n - kTR);
+        const uint32_t t0 = (e & 0xffffffu) * TR, n0 = min(t0, op.n - TR);
         const uint32_t c = wave + WV * ri;
         const uint32_t rg = ri % kXR;
         const uint32_t tag = (op.xid << 16) | c;
@@ -530,14 +534,14 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
                 bv[q] = BIASED ? plane_f32(hb, BF) : -8.0f * sc;
             }
             float2* pw = (float2*)lds.pl[wave];
-            if (op.os == 1) {  // lane = (group, rows 8*quarter ..)
-                const uint32_t g = (lane >> 2) & 15, r0 = 8 * (lane & 3);
-                if (lane < 64) {
+            if (op.os == 1) {  // lane = (group, rows 8*part ..)
+                const uint32_t g = (lane / NS) & 15, r0 = 8 * (lane % NS);
+                if (lane < 16 * NS) {
 #pragma unroll
                     for (int q = 0; q < 8; ++q) pw[(r0 + q) * 16 + g] = float2{sv[q], bv[q]};
                 }
-            } else {  // lane = (row, groups 8*half ..)
-                const uint32_t row = (lane >> 1) & 31, g0 = 8 * (lane & 1);
+            } else if (lane < 2 * TR) {  // lane = (row, groups 8*half ..)
+                const uint32_t row = (lane >> 1) & (TR - 1), g0 = 8 * (lane & 1);
 #pragma unroll
                 for (int q = 0; q < 8; ++q) pw[row * 16 + g0 + q] = float2{sv[q], bv[q]};
             }
@@ -559,12 +563,12 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
         const __amdgpu_buffer_rsrc_t ncr = code_rsrc(nop, nn0);
         const uint32_t nvo = more ? r * (nop.k / 2) + nc * UB + piece : OOB;
 
-        // ---- the unit's 16 steps
-        f32x4 C0[4] = {}, C1[4] = {};
+        // ---- the unit's NSTEP steps
+        f32x4 C0[NS] = {}, C1[NS] = {};
         const u32x4* zero = lds.zero[wave];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int st = u % 4, ks = u / 4, sl = u % 8;
+        for (int u = 0; u < NSTEP; ++u) {
+            const int st = u % NS, ks = u / NS, sl = u % 8;
             // unpack this step's codes, then refill the ring slot: the
             // scheduling barrier keeps the refill after the last read of the
             // slot, so the slot keeps its registers across units (a copy of a
@@ -581,10 +585,10 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
                 bq[t][3] = w8 & 0x00F000F0u;  // (16 q3, 16 q7)
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (u < 8)
+            if (u + 8 < NSTEP)
                 ring[sl] = buf_load<kBufNt>(cr, vo, step_soff(op, u + 8));
             else
-                ring[sl] = buf_load<kBufNt>(ncr, nvo, step_soff(nop, u - 8));
+                ring[sl] = buf_load<kBufNt>(ncr, nvo, step_soff(nop, u + 8 - NSTEP));
             // A row c16 = (byte half hh, slot r): x of this lane's k block when
             // the block's group (4ks + 2hh + kb/2 of the unit) sits in slot r
             const u32x4* src = r == 2 * ks + (kb >> 1) ? xpw + 32 * ks + 16 * hh + 4 * kb : zero;
@@ -612,7 +616,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
             const int nq[4] = {ea.x, ea.y, eb.x, eb.y};
             const f32x4* pw = lds.pl[wave];
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
+            for (int st = 0; st < NS; ++st) {
                 const f32x4 cs = C0[st] + C1[st];
                 const uint32_t row = 8 * st + r;
                 const f32x4 pa = pw[(row * 16 + gb) / 2], pb = pw[(row * 16 + gb + 4) / 2];  // (s, b) of 2 groups each
@@ -626,7 +630,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
         // ---- tile end: the row sums of the four waves meet in LDS, then the D-ops
         if (ri + 1 == R) {
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
+            for (int st = 0; st < NS; ++st) {
                 float v = (acc[st][0] + acc[st][1]) + (acc[st][2] + acc[st][3]);
                 v = (kb >> 1) == hh ? v : 0.0f;  // lanes whose C rows pair the other byte half hold no row
                 v += __shfl_xor(v, 8, 64);
@@ -636,7 +640,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 4
                 acc[st] = f32x4{0, 0, 0, 0};
             }
             lds_barrier();
-            if (tid < (uint32_t)kTR) {
+            if (tid < (uint32_t)TR) {
                 const uint32_t n = n0 + tid;
                 if (n >= t0) {  // rows of the previous tile (shifted last tile) are not written again
                     // the waves' sums in fixed order: fours added pairwise, then the fours in turn
@@ -706,20 +710,32 @@ stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipSt
     // each keeps three times the loads in flight instead.
     bool deep = tiles < (uint32_t)cus;
     for (uint32_t i = 0; i < count; ++i) deep = deep && sorted[i].k % (12 * kUnitK) == 0;
-    const auto pick = [&](auto wv) {
-        constexpr int W = decltype(wv)::value;
-        return pk == STARK_QMM_PROLOGUE_RMS_NORM    ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_RMS_NORM, W>
-               : pk == STARK_QMM_PROLOGUE_SILU_GATE ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_SILU_GATE, W>
-                                                    : qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_NONE, W>;
+    // Otherwise, a launch with fewer 32-row tiles than CUs (a decode step's o
+    // product) takes 16-row tiles: twice the workgroups, and each wave's unit
+    // is 8 steps, its loads all in flight at once (the same arithmetic per
+    // row, so the same bits): 6.7 -> 5.8 us for the Qwen3-8B o product. Not
+    // with the RMS-norm prologue, whose every workgroup reads the whole row
+    // (the q/k/v launch measured 8.3 -> 9.1 us).
+    const bool half = !deep && tiles < (uint32_t)cus && pk != STARK_QMM_PROLOGUE_RMS_NORM;
+    uint32_t tiles16 = 0;
+    for (uint32_t i = 0; i < count; ++i) tiles16 += (sorted[i].n + 15) / 16;
+    const auto pick = [&](auto wv, auto tr) {
+        constexpr int W = decltype(wv)::value, T = decltype(tr)::value;
+        return pk == STARK_QMM_PROLOGUE_RMS_NORM    ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_RMS_NORM, W, T>
+               : pk == STARK_QMM_PROLOGUE_SILU_GATE ? qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_SILU_GATE, W, T>
+                                                    : qmv_stream<SIGNED, BF, BIASED, STARK_QMM_PROLOGUE_NONE, W, T>;
     };
-    auto kern = deep ? pick(std::integral_constant<int, 12>{}) : pick(std::integral_constant<int, 4>{});
+    using I4 = std::integral_constant<int, 4>;
+    auto kern = deep ? pick(std::integral_constant<int, 12>{}, std::integral_constant<int, 32>{})
+                     : half ? pick(I4{}, std::integral_constant<int, 16>{}) : pick(I4{}, std::integral_constant<int, 32>{});
     const int block = deep ? 12 * 64 : kWg;
+    const uint32_t rows = half ? 16u : (uint32_t)kTR, ntiles = half ? tiles16 : tiles;
     // two workgroups (eight waves) per CU, or one of twelve waves; a multiple of the 8 XCDs
     const uint32_t per_launch = (uint32_t)std::max(8, cus * (deep ? 1 : 2) / 8 * 8);
-    const uint32_t grid = std::min(std::min(persistent_grid(kern, block), per_launch), (tiles + 7) / 8 * 8);
+    const uint32_t grid = std::min(std::min(persistent_grid(kern, block), per_launch), (ntiles + 7) / 8 * 8);
     if (grid == 0) return STARK_QMM_DEVICE_FAILURE;
     Schedule sched;
-    const stark_qmm_status st = schedule_for(sorted.data(), count, grid, &sched, stream, kTR);
+    const stark_qmm_status st = schedule_for(sorted.data(), count, grid, &sched, stream, rows);
     if (st != STARK_QMM_OK) return st;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(block), 0, stream, batch, sched);
     QMM_HIP_CHECK(hipGetLastError());

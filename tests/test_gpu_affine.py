@@ -720,3 +720,35 @@ def test_prefill_gemm_split_into_row_launches(qmm, oracle):
     want, mag = bf16_effective_reference(oracle, W, xs, len(rows), n, k, 4, 64, 1, 1, H.BF16, False)
     got = d.view(m, n)[torch.from_numpy(rows).cuda()].cpu().numpy() - prior.view(m, n)[torch.from_numpy(rows).cuda()].cpu().numpy()
     check(got.ravel(), want.ravel(), mag=mag.ravel() + 4.0, label="row-split gemm")
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_decode_stream_kernel_tile_heights_agree(qmm, oracle, layout):
+    """A launch with fewer 32-row tiles than CUs runs 16-row tiles; batched
+    with a large product it runs 32-row tiles. The per-row arithmetic is the
+    same, so the product's outputs are the same bits either way (ragged N)."""
+    rng = np.random.default_rng(91 + layout)
+    n, k = 1000 + 8, 8192
+    W = H.affine_weights(oracle, rng, n, k, 4, 64, layout=layout)
+    x = H.activations(oracle, rng, 1, k)
+    F = H.affine_weights(oracle, rng, 12288, 4096, 4, 64, layout=1)
+    fx = H.activations(oracle, rng, 1, 4096)
+    kern = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+
+    def product(d):
+        return qmm.MatmulArguments(
+            a=H.to_dev(x), m=1, n=n, k=k, d=d,
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(layout, n, k // 64), mode=qmm.MODE_U4,
+                             correction_data=H.to_dev(W["corr"])))
+
+    alone = torch_empty(n, H.BF16)
+    kern.encode_many([product(alone)])  # 32 tiles of 32 rows: the 16-row form
+    batched = torch_empty(n, H.BF16)
+    filler = qmm.MatmulArguments(
+        a=H.to_dev(fx), m=1, n=12288, k=4096, d=torch_empty(12288, H.BF16),
+        b=qmm.QuantizedB(codes=H.to_dev(F["codes"]), scales=H.to_dev(F["scales"]),
+                         params=qmm.QuantParams(1, 12288, 64), mode=qmm.MODE_U4, correction_data=H.to_dev(F["corr"])))
+    kern.encode_many([product(batched), filler])  # 416 tiles of 32 rows
+    torch.cuda.synchronize()
+    assert torch.equal(alone, batched)
