@@ -4,6 +4,7 @@
 // crates/stark-engine/src/backends/cpu/kernel/matmul/kernel.rs:168-285 (sum,
 // then ab_scale, accumulate, bias, soft-cap, output rounding).
 #include <algorithm>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 
@@ -715,7 +716,9 @@ stark_qmm_status launch_stream_planes(const AffineOp* ops, uint32_t count, hipSt
     // is 8 steps, its loads all in flight at once (the same arithmetic per
     // row, so the same bits): 6.7 -> 5.8 us for the Qwen3-8B o product. Not
     // with the RMS-norm prologue, whose every workgroup reads the whole row
-    // (the q/k/v launch measured 8.3 -> 9.1 us).
+    // (the q/k/v launch measured 8.3 -> 9.1 us). Launches of more tiles lose
+    // with 16 rows (gate/up 15.3 -> 16.3 us, the headline layer set 5.07 ->
+    // 4.47 TB/s).
     const bool half = !deep && tiles < (uint32_t)cus && pk != STARK_QMM_PROLOGUE_RMS_NORM;
     uint32_t tiles16 = 0;
     for (uint32_t i = 0; i < count; ++i) tiles16 += (sorted[i].n + 15) / 16;
