@@ -196,7 +196,8 @@ struct AffineOp {
     float ab_scale, soft_cap;
     uint32_t bank_rows;      // weight rows present in the codes buffer (gather bound)
     uint32_t block_begin;    // first blockIdx.x of this op inside a batched launch
-    uint32_t xid;            // streaming kernel: ops with the same activations (x, K) share an id
+    uint32_t xid;            // streaming kernel: ops with the same activations (x, K) share an id;
+                             // small-M kernel: tile pairs per workgroup
 };
 
 constexpr int kMaxBatchOps = 8;

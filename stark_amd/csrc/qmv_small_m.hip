@@ -15,6 +15,16 @@
 // rows and re-stages the activations for every tile. Measured on the Qwen3-8B
 // layer set against the slot form: M = 16 1.0 -> 1.94 TB/s, M = 8 1.69 ->
 // 2.02 TB/s (at 8 rows half the A rows are empty and it still wins).
+//
+// A workgroup runs a run of 1 .. 3 tile pairs of one op pass-major, so one
+// activation stage serves up to 96 weight rows. The register buffers of the
+// code and activation prefetch are indexed by constants only: a buffer
+// picked at run time makes the compiler merge the buffers with copies, and a
+// load into registers whose previous load may be pending on another path
+// waits for every load in flight, which drains the prefetch. Measured on the
+// Qwen3-8B layer set: one pair per workgroup with run-time buffer choice
+// 2.44 / 2.08 TB/s at M = 8 / 16, runs of three with constant buffers
+// 3.27 / 2.90 TB/s.
 #include <algorithm>
 #include <type_traits>
 #include <vector>
@@ -32,6 +42,7 @@ constexpr int kSmQ = kSmPass / 4;        // k per wave per pass (4 groups)
 constexpr int kSmTiles = 2;              // 16-row tiles per workgroup pass
 constexpr int kSmRowB = kSmQ / 2 + 16;   // padded LDS row of a wave's codes (bytes)
 constexpr int kSmGroups = kSmPass / 64;  // groups per pass
+constexpr int kSmMaxRun = 3;             // tile pairs per workgroup, at most
 
 struct SmLds {
     union {
@@ -57,73 +68,81 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     (void)batch;
     __shared__ SmLds lds;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
-    // Blocks are dealt to the 8 XCDs round-robin (block b on XCD b % 8); a
-    // group-output plane line holds 64 rows, i.e. two blocks of 32, so block
-    // b = x + 8 k runs tile pair 2 (x + 8 (k / 2)) + k % 2 and the two pairs
-    // of a line share the XCD's L2 (kb->total: the pairs; the launch is padded
-    // to 16-block steps and the padding blocks return).
-    const uint32_t bx = blockIdx.x, kx = bx >> 3;
-    const uint32_t blk = 2 * ((bx & 7) + 8 * (kx >> 1)) + (kx & 1);
-    if (blk >= kb->total) return;
+    // A workgroup runs a run of up to kSmMaxRun consecutive tile pairs of one
+    // op (op.xid pairs; the last run of an op may be shorter). Blocks are
+    // dealt to the 8 XCDs round-robin (block b on XCD b % 8): block b runs run
+    // (b % 8) * (grid / 8) + b / 8, so consecutive runs, whose rows share the
+    // 64-row lines of the group-output planes, sit on one XCD and its L2
+    // (kb->total: the runs; the grid is padded to a multiple of 8).
+    const uint32_t bx = blockIdx.x;
+    const uint32_t L = bx;
+    if (L >= kb->total) return;
     uint32_t oi = 0;
     for (uint32_t i = 1; i < kb->count; ++i)
-        if (blk >= kb->op[i].block_begin) oi = i;
+        if (L >= kb->op[i].block_begin) oi = i;
     const AffineOp& op = kb->op[oi];
     const uint32_t N = op.n, K = op.k, M = op.m;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t j = lane & 15, kq = lane >> 4;
-    // tile tt covers rows n0[tt] .. +15 and writes those from t0 + 16 tt on; a
-    // tile past N moves back to end at N, so every row is written once
-    const uint32_t t0 = (blk - op.block_begin) * kRows * kSmTiles;
-    uint32_t n0[kSmTiles];
-#pragma unroll
-    for (int tt = 0; tt < kSmTiles; ++tt) n0[tt] = min(t0 + kRows * tt, N - kRows);
+    const uint32_t pair0 = (L - op.block_begin) * op.xid;
+    const uint32_t cnt = min(op.xid, (N + kRows * kSmTiles - 1) / (kRows * kSmTiles) - pair0);
+    const uint32_t passes = K / kSmPass, steps = passes * cnt;
+    // tile tt of the run's pair t covers rows n0(t, tt) .. +15 and writes
+    // those from 32 (pair0 + t) + 16 tt on; a tile past N moves back to end
+    // at N, so every row is written once
+    const auto tile_begin = [&](uint32_t t, int tt) { return kRows * (kSmTiles * (pair0 + t) + tt); };
+    const auto n0_of = [&](uint32_t t, int tt) { return min(tile_begin(t, tt), N - kRows); };
     const uint32_t row_bytes = K / 2;
     const bool bf = op.w_dt == STARK_QMM_BF16, biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
-    // Buffer loads at per-thread offsets fixed here (a pass adds its k):
-    // activation rows past M lie past their resource and read zeros.
+    // Buffer loads at per-thread offsets (a step adds its pair's rows and its
+    // pass's k): activation rows past M lie past their resource and read zeros.
     const __amdgpu_buffer_rsrc_t rc = sm_rsrc(op.codes, (uint64_t)N * row_bytes);
     const __amdgpu_buffer_rsrc_t rx = sm_rsrc(op.x, (uint64_t)M * K * 2);
     const __amdgpu_buffer_rsrc_t rs = sm_rsrc(op.scales, 0x7fffffffu);
-    const __amdgpu_buffer_rsrc_t rb = sm_rsrc(op.corr, 0x7fffffffu);
-    uint32_t co[kSmTiles][2], po[kSmTiles], xo[8];
+    const __amdgpu_buffer_rsrc_t rb = biased ? sm_rsrc(op.corr, 0x7fffffffu) : rs;
+    uint32_t co[2], xo[8];
 #pragma unroll
-    for (int tt = 0; tt < kSmTiles; ++tt) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t p = tid + 256 * i, r = p / 32, c = p % 32;
-            co[tt][i] = (n0[tt] + r) * row_bytes + 16 * c;
-        }
-        po[tt] = ((n0[tt] + tid % 16) * op.os + (tid / 16) * op.gs) * 2;
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t p = tid + 256 * i, r = p / 32, c = p % 32;
+        co[i] = r * row_bytes + 16 * c;
     }
+    const uint32_t po = ((tid % 16) * op.os + (tid / 16) * op.gs) * 2;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
         xo[i] = (m * K + 8 * c) * 2;
     }
 
-    // two register buffers: a pass's loads are issued two passes before it is
-    // staged (the passes alternate between the buffers)
+    // Steps run pass-major: step s is pass s / cnt of pair s % cnt, and a
+    // pass's activations are staged at its first step. Two register buffers
+    // for codes (a step's codes are issued two steps before it is staged) and
+    // two for activations.
     u32x4 wc[2][kSmTiles][2];  // codes: piece p = tid + 256 i of a tile's [16 rows][512 bytes]
     u32x4 xv[2][8];            // activations: vector v = tid + 256 i is row v / 128, values 8 (v % 128)
     uint32_t ps[2][kSmTiles], pb[2][kSmTiles];  // raw plane values of (group tid / 16, row tid % 16)
-    const auto load = [&](auto buf, uint32_t kbase) {
+    const auto load_codes = [&](auto buf, uint32_t t, uint32_t kbase) {
         constexpr int B = decltype(buf)::value;
         const uint32_t pg = (kbase / 64) * op.gs * 2;  // bytes of the pass's first plane group
 #pragma unroll
         for (int tt = 0; tt < kSmTiles; ++tt) {
+            const uint32_t n0 = n0_of(t, tt);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                wc[B][tt][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, co[tt][i] + kbase / 2, 0, 2));
-            ps[B][tt] = __builtin_amdgcn_raw_buffer_load_b16(rs, po[tt], pg, 0);
-            pb[B][tt] = biased ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, po[tt], pg, 0) : 0u;
+                wc[B][tt][i] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, co[i] + kbase / 2, n0 * row_bytes, 2));
+            const uint32_t pr = pg + n0 * op.os * 2;
+            ps[B][tt] = __builtin_amdgcn_raw_buffer_load_b16(rs, po, pr, 0);
+            pb[B][tt] = __builtin_amdgcn_raw_buffer_load_b16(rb, po, pr, 0);  // unused without biases
         }
+    };
+    const auto load_x = [&](auto buf, uint32_t kbase) {
+        constexpr int B = decltype(buf)::value;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             xv[B][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[i] + kbase * 2, 0, 0));
     };
-    const auto stage = [&](auto buf) {
+    const auto stage_codes = [&](auto buf) {
         constexpr int B = decltype(buf)::value;
 #pragma unroll
         for (int tt = 0; tt < kSmTiles; ++tt) {
@@ -135,6 +154,9 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             const float sc = plane_f32(ps[B][tt], bf);
             lds.pl[tt][tid / 16][tid % 16] = float2{sc, biased ? plane_f32(pb[B][tt], bf) : -8.0f * sc};
         }
+    };
+    const auto stage_x = [&](auto buf) {
+        constexpr int B = decltype(buf)::value;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t v = tid + 256 * i, m = v / 128, c = v % 128;
@@ -166,11 +188,13 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         }
     };
 
-    f32x4 acc[kSmTiles];
+    f32x4 acc[kSmMaxRun][kSmTiles];
 #pragma unroll
-    for (int tt = 0; tt < kSmTiles; ++tt) acc[tt] = f32x4{0, 0, 0, 0};
-    // the wave's 256 k of a pass: 8 chunks of 32, two per group
-    const auto compute = [&]() {
+    for (int r = 0; r < kSmMaxRun; ++r)
+#pragma unroll
+        for (int tt = 0; tt < kSmTiles; ++tt) acc[r][tt] = f32x4{0, 0, 0, 0};
+    // the wave's 256 k of a step: 8 chunks of 32, two per group
+    const auto compute = [&](f32x4 (&a_acc)[kSmTiles]) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             f32x4 C[kSmTiles];
@@ -202,24 +226,13 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
                 const float2 p = lds.pl[tt][gp][j];
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    acc[tt][q] = fmaf(p.x, ldexp_f32(C[tt][q], e4[q]), fmaf(p.y, x4[q], acc[tt][q]));
+                    a_acc[tt][q] = fmaf(p.x, ldexp_f32(C[tt][q], e4[q]), fmaf(p.y, x4[q], a_acc[tt][q]));
             }
         }
     };
 
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    const auto pass = [&](auto buf, uint32_t kbase) {
-        if (kbase) __syncthreads();  // every wave finished the previous pass's LDS
-        stage(buf);
-        __syncthreads();
-        // (a branch-free prefetch re-reading the last pass costs more here than
-        // the branch: four passes at K = 4096, M = 8 / 16 2.15 / 1.85 vs 2.42 / 2.03 TB/s)
-        if (kbase + 2 * kSmPass < K) load(buf, kbase + 2 * kSmPass);
-        compute();
-    };
-    load(B0{}, 0);
-    if (kSmPass < K) load(B1{}, kSmPass);
     // activation rows past M: zero once (their products and sums are zero)
     for (uint32_t v = tid; v < 16 * (kSmPass / 8); v += kWg) {
         const uint32_t m = v / (kSmPass / 8);
@@ -230,27 +243,76 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             lds.xs[v / kSmGroups][v % kSmGroups] = 0.0f;
             lds.xe[v / kSmGroups][v % kSmGroups] = 0;
         }
-    for (uint32_t kbase = 0; kbase < K; kbase += 2 * kSmPass) {
-        pass(B0{}, kbase);
-        if (kbase + kSmPass < K) pass(B1{}, kbase + kSmPass);
-    }
-    __syncthreads();  // the results overwrite the code stage
+    // The step loop is unrolled over two steps, so that a step's code buffer
+    // is its parity, a constant. A run of one pair (ONE) takes its activations
+    // two passes ahead into the buffer of the pass's parity (also the step's);
+    // a longer run takes them one pass (cnt steps) ahead into one buffer.
+    const auto run = [&](auto one_c) {
+        constexpr bool ONE = decltype(one_c)::value;
+        constexpr uint32_t XA = ONE ? 2 : 1;  // passes ahead of the activation loads
+        load_codes(B0{}, 0, 0);
+        uint32_t lp = 0, lt = 1;  // load cursor: pass and pair of step s + 2
+        if (lt == cnt) lt = 0, lp = 1;
+        if (steps > 1) load_codes(B1{}, lt, lp * kSmPass);
+        if (++lt == cnt) lt = 0, ++lp;
+        load_x(B0{}, 0);
+        if (ONE && passes > 1) load_x(B1{}, kSmPass);
+        uint32_t p = 0, t = 0;
+        const auto step = [&](auto b_c, uint32_t s) {
+            constexpr int SB = decltype(b_c)::value;
+            using BS = std::integral_constant<int, SB>;
+            using BX = std::integral_constant<int, ONE ? SB : 0>;
+            if (s) __syncthreads();  // every wave finished the previous step's LDS
+            stage_codes(BS{});
+            // a buffer's next activation loads are issued right after it is
+            // staged, on the same path (a load into registers whose previous
+            // load may still be pending on another path waits for every load)
+            if (ONE || t == 0) {
+                stage_x(BX{});
+                if (p + XA < passes) load_x(BX{}, (p + XA) * kSmPass);
+            }
+            __syncthreads();
+            if (s + 2 < steps) {
+                load_codes(BS{}, lt, lp * kSmPass);
+                if (++lt == cnt) lt = 0, ++lp;
+            }
+            if (ONE) {
+                compute(acc[0]);
+            } else {
 #pragma unroll
-    for (int tt = 0; tt < kSmTiles; ++tt)
+                for (int r = 0; r < kSmMaxRun; ++r)
+                    if (t == (uint32_t)r) compute(acc[r]);
+            }
+            if (++t == cnt) t = 0, ++p;
+        };
+        for (uint32_t s = 0; s < steps; s += 2) {
+            step(B0{}, s);
+            if (s + 1 < steps) step(B1{}, s + 1);
+        }
+    };
+    if (cnt == 1) run(std::true_type{});
+    else run(std::false_type{});
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lds.red[tt][wave][4 * kq + q][j] = acc[tt][q];
-    __syncthreads();
-    for (uint32_t t = tid; t < (uint32_t)(kSmTiles * 16 * kRows); t += kWg) {
-        const uint32_t tt = t / (16 * kRows), m = (t / kRows) % 16, r = t % kRows;
-        const uint32_t n = n0[tt] + r;
-        if (m >= M || n < t0 + kRows * tt) continue;
-        const size_t o = (size_t)m * N + n;
-        float v = op.ab_scale * ((lds.red[tt][0][m][r] + lds.red[tt][1][m][r]) +
-                                 (lds.red[tt][2][m][r] + lds.red[tt][3][m][r]));
-        if (op.flags & FLAG_ACCUMULATE) v += load_as_f32(op.d, op.d_dt, o);
-        if (op.bias) v += load_as_f32(op.bias, op.w_dt, n);
-        if (op.flags & FLAG_SOFT_CAP) v = op.soft_cap * tanhf(v / op.soft_cap);
-        store_from_f32(op.d, op.d_dt, o, v);
+    for (int r = 0; r < kSmMaxRun; ++r) {
+        if ((uint32_t)r >= cnt) break;
+        __syncthreads();  // the results overwrite the code stage / the previous pair's results
+#pragma unroll
+        for (int tt = 0; tt < kSmTiles; ++tt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) lds.red[tt][wave][4 * kq + q][j] = acc[r][tt][q];
+        __syncthreads();
+        for (uint32_t v = tid; v < (uint32_t)(kSmTiles * 16 * kRows); v += kWg) {
+            const uint32_t tt = v / (16 * kRows), m = (v / kRows) % 16, rr = v % kRows;
+            const uint32_t n = n0_of(r, tt) + rr;
+            if (m >= M || n < tile_begin(r, tt)) continue;
+            const size_t o = (size_t)m * N + n;
+            float y = op.ab_scale * ((lds.red[tt][0][m][rr] + lds.red[tt][1][m][rr]) +
+                                     (lds.red[tt][2][m][rr] + lds.red[tt][3][m][rr]));
+            if (op.flags & FLAG_ACCUMULATE) y += load_as_f32(op.d, op.d_dt, o);
+            if (op.bias) y += load_as_f32(op.bias, op.w_dt, n);
+            if (op.flags & FLAG_SOFT_CAP) y = op.soft_cap * tanhf(y / op.soft_cap);
+            store_from_f32(op.d, op.d_dt, o, y);
+        }
     }
 }
 
@@ -273,21 +335,40 @@ bool small_m_eligible(const AffineOp* ops, uint32_t count) {
 
 stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream) {
     if (count > (uint32_t)kMaxBatchOps) return STARK_QMM_INVALID_ARGUMENT;  // the batch holds kMaxBatchOps
-    // longest K first: the workgroups with the most passes are dispatched first
-    // instead of forming the tail of the launch
+    int dev = 0, cus = 0;
+    QMM_HIP_CHECK(hipGetDevice(&dev));
+    QMM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    // Runs: a workgroup takes up to kSmMaxRun tile pairs of one op, so one
+    // activation stage serves that many pairs. The run length of an op is the
+    // launch's pass count per resident workgroup (two per CU) over the op's
+    // passes: a launch of deep and shallow products then gives every
+    // workgroup about the same number of steps (the Qwen3-8B layer set: one
+    // pair of the K = 12288 down product or three pairs of the K = 4096
+    // products, 12 steps each, 492 workgroups), and a launch of few pairs
+    // keeps one pair per workgroup.
+    uint64_t units = 0;
+    for (uint32_t i = 0; i < count; ++i)
+        units += (uint64_t)((ops[i].n + kRows * kSmTiles - 1) / (kRows * kSmTiles)) * (ops[i].k / kSmPass);
+    const uint64_t slots = 2 * (uint64_t)std::max(cus, 1);
+    const uint64_t per_wg = (units + slots - 1) / slots;
+    // longest K first: its runs take the low run indices
     std::vector<AffineOp> sorted(ops, ops + count);
     std::stable_sort(sorted.begin(), sorted.end(), [](const AffineOp& a, const AffineOp& b) { return a.k > b.k; });
     AffineBatch batch{};
-    uint32_t blocks = 0;
+    uint32_t runs = 0;
     for (uint32_t i = 0; i < count; ++i) {
+        const uint32_t pairs = (sorted[i].n + kRows * kSmTiles - 1) / (kRows * kSmTiles);
+        const uint32_t run =
+            (uint32_t)std::min<uint64_t>(kSmMaxRun, std::max<uint64_t>(1, per_wg / (sorted[i].k / kSmPass)));
         batch.op[i] = sorted[i];
-        batch.op[i].block_begin = blocks;
-        blocks += (sorted[i].n + kRows * kSmTiles - 1) / (kRows * kSmTiles);
+        batch.op[i].block_begin = runs;
+        batch.op[i].xid = run;  // tile pairs per run
+        runs += (pairs + run - 1) / run;
     }
     batch.count = count;
-    batch.total = blocks;
-    if (blocks == 0) return STARK_QMM_OK;
-    const uint32_t grid = (blocks + 15) / 16 * 16;  // whole line pairs on every XCD
+    batch.total = runs;
+    if (runs == 0) return STARK_QMM_OK;
+    const uint32_t grid = (runs + 7) / 8 * 8;  // the same number of blocks on every XCD
     if (signed_codes)
         hipLaunchKernelGGL(qmv_small_m<true>, dim3(grid), dim3(kWg), 0, stream, batch);
     else

@@ -414,7 +414,7 @@ def test_matrix_core_kernel_shapes(qmm, oracle, n, k, gs, m, layout):
 @pytest.mark.parametrize("layout", [0, 1])
 def test_small_m_dense_kernel_shapes(qmm, oracle, n, k, m, layout):
     """M = 5 .. 16, 4-bit, group 64, K % 1024 == 0 takes the dense small-M
-    kernel (all 16 activation rows per MFMA, two 16-row tiles per pass): one
+    kernel (all 16 activation rows per MFMA, two 16-row tiles per step): one
     tile, a pair with a shifted second tile, ragged N, long K."""
     run_case(qmm, oracle, m=m, n=n, k=k, gs=64, layout=layout, seed=n + k + 3 * m + layout)
 
@@ -445,6 +445,42 @@ def test_small_m_dense_kernel_batch_matches_single(qmm, oracle):
     def args(m, n, kk, W, x):
         return qmm.MatmulArguments(
             a=x, m=m, n=n, k=kk, d=torch_empty(m * n, H.BF16),
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(1, n, kk // 64), correction_data=H.to_dev(W["corr"])))
+    many = [args(*t) for t in made]
+    k.encode_many(many)
+    single = [args(*t) for t in made]
+    for a in single:
+        k.encode(a)
+    torch.cuda.synchronize()
+    for a, b in zip(many, single):
+        assert torch.equal(a.d, b.d)
+
+
+@pytest.mark.parametrize("n,k", [(9000, 4096), (32010, 1024)])
+@pytest.mark.parametrize("m", [8, 16])
+def test_small_m_dense_kernel_runs(qmm, oracle, n, k, m):
+    """Launches with more tile pairs than resident workgroups: a workgroup
+    runs several pairs pass by pass (three at N = 9000, K = 4096; two at
+    N = 32010, K = 1024, whose last run holds one pair with a shifted tile)."""
+    run_case(qmm, oracle, m=m, n=n, k=k, gs=64, layout=1, seed=n + k + m)
+
+
+def test_small_m_dense_kernel_run_length_keeps_bits(qmm, oracle):
+    """A K = 12288 product and a K = 4096 product in one launch run one pair
+    per workgroup; alone, the K = 4096 product runs three. Every output row
+    keeps its bits."""
+    rng = np.random.default_rng(37)
+    k = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    made = []
+    for n, kk in [(4096, 12288), (12288, 4096)]:
+        W = H.affine_weights(oracle, rng, n, kk, 4, 64, layout=1)
+        x = H.to_dev(H.activations(oracle, rng, 8, kk))
+        made.append((n, kk, W, x))
+
+    def args(n, kk, W, x):
+        return qmm.MatmulArguments(
+            a=x, m=8, n=n, k=kk, d=torch_empty(8 * n, H.BF16),
             b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
                              params=qmm.QuantParams(1, n, kk // 64), correction_data=H.to_dev(W["corr"])))
     many = [args(*t) for t in made]
