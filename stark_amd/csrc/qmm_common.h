@@ -237,7 +237,7 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
 // Route adjustment with optional gains (moe.hip).
 stark_qmm_status launch_moe_adjust(uint32_t* ids, float* weights, const float* scales, uint32_t rows,
                                    uint32_t experts, uint32_t active, uint32_t sort_ids, hipStream_t stream);
-// Dense small-M kernel: 4-bit, group 64, M = 5 .. 16, K % 1024 == 0 (qmv_small_m.hip).
+// Dense small-M kernel: 4-bit, group 64, M = 3 .. 16, K % 1024 == 0 (qmv_small_m.hip).
 bool small_m_eligible(const AffineOp* ops, uint32_t count);
 stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream);
 // Matrix-core kernel for 4/8-bit products with M <= 16 (qmv_mfma.hip).

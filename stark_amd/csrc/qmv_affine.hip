@@ -18,8 +18,8 @@
 //   per pass delays compute but never the HBM stream;
 // * 4-bit x bf16: nibbles become bf16 (1 + q/16) with one shift and one
 //   and-or per pair and feed v_dot2_f32_bf16 (products exact, f32 sums);
-//   the offset is folded into the group's (scale, bias):
-//     s*sum(x*q) + b*sum(x) = 16s * sum(x*(1+q/16)) + (b - 16s) * sum(x)
+//   the offset leaves through the group's activation sum:
+//     s*sum(x*q) + b*sum(x) = 16s * (sum(x*(1+q/16)) - sum(x)) + b * sum(x)
 // * other types: v_cvt_f32_ubyte + f32 FMA;
 // * rows are reduced across the wave at the end.
 #include <cstdlib>
@@ -164,15 +164,15 @@ struct Geo {
     static constexpr int CPL = kPassValues / (64 * VPC);  // chunks per lane per pass
 };
 
-// (scale, bias_term) of weight row `w`, group `g`; DOT2 folds the +1 offset of
-// the (1 + q/16) encoding: (16 s, b - 16 s).
+// (scale, bias_term) of weight row `w`, group `g`; DOT2 scales s by 16 for
+// the (1 + q/16) encoding, whose +1 offset the accumulation removes by
+// subtracting the group's activation sum from the dot product (exact for a
+// one-hot row, so such a row gives s*q + b with one rounding, as the
+// reference; folding the offset into the bias as b - 16 s would round it
+// separately).
 template <int BITS, bool DOT2>
 __device__ __forceinline__ float2 fold_meta(float s, float bt) {
-    if (DOT2) {
-        const float s16 = 16.0f * s;
-        return make_float2(s16, bt - s16);
-    }
-    return make_float2(s, bt);
+    return make_float2(DOT2 ? 16.0f * s : s, bt);
 }
 
 template <int BITS, bool DOT2>
@@ -429,6 +429,7 @@ __global__ __launch_bounds__(kThreads) void qmv_affine_tile(AffineBatch batch) {
         }
 
         // ---- 4. dot products
+        const bool f32p = op.w_dt == STARK_QMM_F32;
         const uint32_t magic = 0x3F803F80u;  // bf16 1.0 in both halves
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
@@ -491,7 +492,12 @@ __global__ __launch_bounds__(kThreads) void qmv_affine_tile(AffineBatch batch) {
                             dsum = fmaf(ubyte<3>(wd[d]), xv[4 * d + 3], dsum);
                         }
                     }
-                    acc[r][m] = fmaf(e.x, dsum, fmaf(e.y, xs[m][i], acc[r][m]));
+                    const float dq = DOT2 ? dsum - xs[m][i] : dsum;  // sum(x q / 16) with the +1 offset removed
+                    // f32 planes: s * sum(x q) is rounded before the bias term
+                    // joins, as the reference rounds s * q before adding b
+                    // (with 16-bit planes that product is exact either way)
+                    acc[r][m] = f32p ? fmaf(e.y, xs[m][i], acc[r][m] + e.x * dq)
+                                     : fmaf(e.x, dq, fmaf(e.y, xs[m][i], acc[r][m]));
                 }
             }
         }

@@ -806,7 +806,7 @@ stark_qmm_status launch_gs(const AffineOp* o, uint32_t n, hipStream_t st) {
     case 64:
         if constexpr (MP == 1 && MB == 1 && BITS == 4)
             if (stream_eligible(o, n)) return sg ? launch_stream<true>(o, n, st) : launch_stream<false>(o, n, st);
-        if constexpr (MP == 8 && BITS == 4)  // M = 5 .. 16
+        if constexpr (MP >= 4 && BITS == 4)  // M = 3 .. 16
             if (small_m_eligible(o, n)) return launch_small_m(o, n, sg, st);
         return sg ? launch_one<MP, MB, 64, BITS, true>(o, n, st) : launch_one<MP, MB, 64, BITS, false>(o, n, st);
     default:

@@ -410,10 +410,10 @@ def test_matrix_core_kernel_shapes(qmm, oracle, n, k, gs, m, layout):
 
 
 @pytest.mark.parametrize("n,k", [(16, 1024), (40, 4096), (1000, 2048), (96, 12288)])
-@pytest.mark.parametrize("m", [5, 8, 9, 12, 16])
+@pytest.mark.parametrize("m", [3, 4, 5, 8, 9, 12, 16])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_small_m_dense_kernel_shapes(qmm, oracle, n, k, m, layout):
-    """M = 5 .. 16, 4-bit, group 64, K % 1024 == 0 takes the dense small-M
+    """M = 3 .. 16, 4-bit, group 64, K % 1024 == 0 takes the dense small-M
     kernel (all 16 activation rows per MFMA, two 16-row tiles per step): one
     tile, a pair with a shifted second tile, ragged N, long K."""
     run_case(qmm, oracle, m=m, n=n, k=k, gs=64, layout=layout, seed=n + k + 3 * m + layout)

@@ -146,9 +146,10 @@ def test_mfma_4bit_m1_exact(qmm, oracle, gs):
 @pytest.mark.parametrize("m", [2, 3, 4])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_mfma_4bit_small_m_exact(qmm, oracle, m, layout):
-    """qmv_mfma<2,1> (M = 2) and <4,1> (M = 3, 4), identity activation blocks."""
-    _affine_exact(qmm, oracle, n=48, k=4096, m=m, layout=layout, ncols=24, seed=m * 3 + layout,
-                  label=f"qmv_mfma w4 m{m}")
+    """qmv_mfma<2,1> (M = 2) and <4,1> (M = 3, 4; K % 1024 != 0 keeps them off
+    the dense small-M kernel), identity activation blocks."""
+    _affine_exact(qmm, oracle, n=48, k=4096 if m == 2 else 4032, m=m, layout=layout, ncols=24,
+                  seed=m * 3 + layout, label=f"qmv_mfma w4 m{m}")
 
 
 @pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
@@ -163,9 +164,9 @@ def test_mfma_8bit_signed_symmetric_exact(qmm, oracle, signed, correction):
                   seed=90 + signed, label="qmv_mfma w8 variants")
 
 
-# ------------------------------------------------------------ qmv_small_m (dense form, M = 5..16)
+# ------------------------------------------------------------ qmv_small_m (dense form, M = 3..16)
 
-@pytest.mark.parametrize("m", [5, 8, 16])
+@pytest.mark.parametrize("m", [3, 4, 5, 8, 16])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_small_m_exact(qmm, oracle, m, layout):
     _affine_exact(qmm, oracle, n=96, k=4096, m=m, layout=layout, ncols=32, seed=100 + m + layout,
@@ -191,6 +192,22 @@ def test_tile_kernel_f32_activations_exact(qmm, oracle, bits):
     """qmv_affine_tile: f32 activations take the VALU tile kernel."""
     _affine_exact(qmm, oracle, n=40, k=1024, m=2, bits=bits, x_dt=H.F32, ncols=24, seed=140 + bits,
                   label=f"qmv_affine_tile w{bits}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_tile_kernel_bf16_activations_exact(qmm, oracle, m):
+    """qmv_affine_tile, 4-bit codes as bf16 (1 + q/16) into v_dot2: per-row
+    planes whose group count is not a multiple of 8 (K = 4032) keep the
+    product off the matrix-core kernels."""
+    _affine_exact(qmm, oracle, n=48, k=4032, m=m, layout=0, ncols=24, seed=170 + m, label=f"qmv_affine_tile dot2 m{m}")
+
+
+@pytest.mark.parametrize("x_dt", [H.BF16, H.F32])
+def test_tile_kernel_f32_planes_exact(qmm, oracle, x_dt):
+    """qmv_affine_tile with f32 scale and bias planes (s*q is then rounded
+    before b joins, as in the reference), dot2 and f32-FMA forms."""
+    _affine_exact(qmm, oracle, n=40, k=1024, m=2, w_dt=H.F32, x_dt=x_dt, ncols=24, seed=175,
+                  label=f"qmv_affine_tile f32 planes x{x_dt}")
 
 
 @pytest.mark.parametrize("bits", [3, 5, 6])
