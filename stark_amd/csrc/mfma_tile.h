@@ -406,7 +406,20 @@ struct TileEngine {
         }
     }
 
-    // Walk every pass of a tile whose first pass has been load()ed.
+    // Parameters of the loads issued after a pass is staged: the tile's next
+    // pass, or the first pass of the workgroup's next tile.
+    struct NextLoad {
+        const AffineOp* op;
+        uint32_t pf, nA, nB, M, kbase;
+        bool keep_x, other_op;  // other_op: activation rows are m * op->k, not xrow(m)
+    };
+
+    // Walk every pass of a tile whose first pass has been load()ed. next(nl)
+    // fills nl with the next tile's first pass and returns true, or returns
+    // false. Both kinds of refill go through one load() call: loads written
+    // to the same registers from two call sites make the compiler join the
+    // two sets of values with copies, and a copy waits for its load, which
+    // would drain the prefetch.
     template <class XRow, class Next>
     __device__ __forceinline__ void run(const AffineOp& op, uint32_t pf, uint32_t nA, uint32_t nB, uint32_t M,
                                         XRow xrow, Next next, bool keep_x = false) {
@@ -421,10 +434,10 @@ struct TileEngine {
             stage(op, pf, nA, nB, kbase, gcnt, keep_x && kbase == 0);
             __syncthreads();
             // the registers are free: the next pass's (or tile's) loads fly while this pass computes
-            if (kbase + PASS < K)
-                load(op, pf, nA, nB, M, xrow, kbase + PASS);
-            else
-                next();
+            NextLoad nl{&op, pf, nA, nB, M, kbase + PASS, false, false};
+            if (kbase + PASS < K || next(nl))
+                load(*nl.op, nl.pf, nl.nA, nl.nB, nl.M,
+                     [&](uint32_t m) { return nl.other_op ? (size_t)m * nl.op->k : xrow(m); }, nl.kbase, nl.keep_x);
             const uint32_t koff = x_offset(K, kbase);
             if (kvals == (uint32_t)PASS)
                 compute<false>(pf, M, kvals, gcnt, koff, acc);
@@ -465,7 +478,7 @@ __device__ __forceinline__ void mfma_tile(const AffineOp& op, uint32_t pf, uint3
                                           XRow xrow, MfmaLds<MP, MB, GS, BITS, P1>& lds) {
     TileEngine<MP, MB, GS, BITS, SIGNED, P1> e(lds);
     e.load(op, pf, nA, nB, M, xrow, 0);
-    e.run(op, pf, nA, nB, M, xrow, [] {});
+    e.run(op, pf, nA, nB, M, xrow, [](typename TileEngine<MP, MB, GS, BITS, SIGNED, P1>::NextLoad&) { return false; });
 }
 
 }  // namespace mfma

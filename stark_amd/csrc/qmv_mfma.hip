@@ -70,15 +70,14 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(kWavesPerEu
         rows_of(cur, t0, n0);
         const uint32_t nxt = i + 1 < hi ? sched.tiles[i + 1] : 0u;
         bool next_keep_x = false;
-        e.run(op, pf, n0, n0 + 8, M, [&](uint32_t m) { return (size_t)m * op.k; }, [&] {
-            if (i + 1 < hi) {
-                uint32_t u0, m0;
-                rows_of(nxt, u0, m0);
-                const AffineOp& nop = kb->op[nxt >> 24];
-                next_keep_x = (nxt >> 24) == (cur >> 24) && nop.k <= (uint32_t)Geo<MP, MB, GS, BITS, kP1<BITS>>::XK;
-                e.load(nop, plane_flags(nop), m0, m0 + 8, nop.m, [&](uint32_t m) { return (size_t)m * nop.k; }, 0,
-                       next_keep_x);
-            }
+        e.run(op, pf, n0, n0 + 8, M, [&](uint32_t m) { return (size_t)m * op.k; }, [&](auto& nl) {
+            if (i + 1 >= hi) return false;
+            uint32_t u0, m0;
+            rows_of(nxt, u0, m0);
+            const AffineOp& nop = kb->op[nxt >> 24];
+            next_keep_x = (nxt >> 24) == (cur >> 24) && nop.k <= (uint32_t)Geo<MP, MB, GS, BITS, kP1<BITS>>::XK;
+            nl = {&nop, plane_flags(nop), m0, m0 + 8, nop.m, 0u, next_keep_x, true};
+            return true;
         }, keep_x);
         keep_x = next_keep_x;
         constexpr int MR = MP * MB;
