@@ -38,7 +38,10 @@ def _both(qmm, c):
 def test_static_matches_workspace_entry_point_twice(qmm, oracle):
     big = MC.case(oracle, 71, 16, model=2048, hidden=768, experts=128, active=8)
     small = MC.case(oracle, 72, 3, model=256, hidden=128, experts=16, active=4)
-    for c in (big, small):  # the second call is smaller and reuses the scratch
+    # one token at the config-3 geometry: the fused route + up launch and the
+    # fused down + accumulation launch, the decode case
+    one = MC.case(oracle, 73, 1, model=2048, hidden=768, experts=128, active=8)
+    for c in (big, small, one):  # each call is smaller than the first and reuses the scratch
         got, want = _both(qmm, c)
         assert np.array_equal(got, want), f"rows {c['rows']}: {int((got != want).sum())} outputs differ"
 
