@@ -466,6 +466,19 @@ def test_small_m_dense_kernel_runs(qmm, oracle, n, k, m):
     run_case(qmm, oracle, m=m, n=n, k=k, gs=64, layout=1, seed=n + k + m)
 
 
+@pytest.mark.parametrize("variant", ["symmetric", "f16_planes", "signed", "output_group", "m3", "d_ops"])
+def test_small_m_dense_kernel_runs_variants(qmm, oracle, variant):
+    """The multi-pair runs (N = 9000, K = 4096: three pairs per workgroup)
+    with each plane, code and output variant: symmetric codes (no bias
+    plane), f16 planes, signed codes, per-row planes, an odd M, and the
+    D-ops on a run's shifted last tile."""
+    kw = dict(m=8, n=9000, k=4096, gs=64, layout=1, seed=300 + len(variant))
+    kw.update({"symmetric": dict(correction=0), "f16_planes": dict(w_dt=H.F16), "signed": dict(signed=True),
+               "output_group": dict(layout=0), "m3": dict(m=3),
+               "d_ops": dict(m=5, ab_scale=0.5, accumulate=True, with_bias=True, soft_cap=20.0)}[variant])
+    run_case(qmm, oracle, **kw)
+
+
 def test_small_m_dense_kernel_run_length_keeps_bits(qmm, oracle):
     """A K = 12288 product and a K = 4096 product in one launch run one pair
     per workgroup; alone, the K = 4096 product runs three. Every output row
