@@ -211,6 +211,8 @@ stark_qmm_status encode_product(stark_qmm_kernel* kr, const stark_qmm_args* args
     // Prefill-sized products run the dequant-GEMM (bf16-rounded weight tiles, as
     // the reference's Metal GEMM); the reference-accumulation mode keeps the
     // f32-dequant GEMV kernels for every M (kernel.rs:34-37, metal mod.rs:341-357).
+    if (!kr->reference_accumulation && !materialize && bits == 4 && skinny_eligible(&op, 1))
+        return launch_skinny(&op, 1, (op.flags & FLAG_SIGNED) != 0, stream);
     if (!kr->reference_accumulation && !materialize && gemm_eligible(op, bits))
         return launch_affine_gemm(op, bits, stream);
     if (affine_fast_eligible(op, bits)) return launch_affine_gemv(&op, 1, bits, stream);
@@ -264,6 +266,7 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
     std::vector<AffineOp> fast4, fast8;
     // prefill-sized products by (bits, signed codes, biases, bf16 planes): one grid each
     std::vector<AffineOp> gemm[2][2][2][2];
+    std::vector<AffineOp> skinny[2];  // by signedness
     // int8-activation prefill products by grid class
     std::vector<AffineOp> a8_ops[16];
     std::vector<A8Operand> a8_as[16];
@@ -293,7 +296,9 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
         stark_qmm_status st = build_affine_op(kr, a->b, a->m, a->n, a->k, x, a->d, a->d_ops, a->gather_indices, &op, &bits);
         if (st != STARK_QMM_OK) return st;
         if (!a->d || (!x && a->k)) return STARK_QMM_INVALID_ARGUMENT;
-        if (op.m > 16 && !kr->reference_accumulation && gemm_eligible(op, bits) && op.m <= gemm_rows(op.k)) {
+        if (op.m > 16 && !kr->reference_accumulation && bits == 4 && skinny_eligible(&op, 1)) {
+            skinny[(op.flags & FLAG_SIGNED) != 0].push_back(op);
+        } else if (op.m > 16 && !kr->reference_accumulation && gemm_eligible(op, bits) && op.m <= gemm_rows(op.k)) {
             gemm[bits == 8][(op.flags & FLAG_SIGNED) != 0][op.corr_kind == STARK_QMM_CORRECTION_BIASES]
                 [op.w_dt == STARK_QMM_BF16].push_back(op);
         } else if (!affine_fast_eligible(op, bits) || op.gather || (op.m > 16 && !kr->reference_accumulation)) {
@@ -314,6 +319,12 @@ stark_qmm_status stark_qmm_encode_many(stark_qmm_kernel* kr, const stark_qmm_arg
         st = launch_affine_gemv(many.data(), (uint32_t)many.size(), bits, stream);
         if (st != STARK_QMM_OK) return st;
     }
+    for (int sg = 0; sg < 2; ++sg)
+        for (size_t s = 0; s < skinny[sg].size(); s += kMaxBatchOps) {
+            const uint32_t n = (uint32_t)std::min<size_t>(kMaxBatchOps, skinny[sg].size() - s);
+            const stark_qmm_status st = launch_skinny(skinny[sg].data() + s, n, sg != 0, stream);
+            if (st != STARK_QMM_OK) return st;
+        }
     for (int b8 = 0; b8 < 2; ++b8)
         for (auto& a : gemm[b8])
             for (auto& c : a)

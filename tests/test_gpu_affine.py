@@ -580,8 +580,9 @@ def test_prefill_gemm_full_width(qmm, oracle):
                                    (130, 1000, 192)])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_prefill_gemm_shapes(qmm, oracle, m, n, k, bits):
-    """M > 16 runs the matrix-core dequant-GEMM: bf16-effective weights, f32
-    accumulation. Checked against the f64 product of the same bf16 weights, and
+    """M > 16 runs the matrix-core dequant-GEMM (4-bit g64 products of at most
+    32 rows with K % 512 == 0 the skinny product, same arithmetic):
+    bf16-effective weights, f32 accumulation. Checked against the f64 product of the same bf16 weights, and
     against the exact-f32 CPU kernel at the reference's own GPU/CPU bar
     (quant_dispatch_test.rs:189: rel 0.05 / abs 0.4)."""
     rng = np.random.default_rng(m * 7 + n + bits)
@@ -607,6 +608,85 @@ def test_prefill_gemm_shapes(qmm, oracle, m, n, k, bits):
                               layout=layout, bits=bits, group_size=64, output_dt=H.F32, threads=8)
     assert st == 0
     assert np.all(np.abs(got.ravel() - exact) <= 0.05 * np.abs(exact) + 0.4)
+
+
+def _skinny_case(qmm, oracle, m, n, k, *, layout=1, correction=1, signed=False, w_dt=H.BF16, seed=0, d_dt=H.F32,
+                 ab_scale=1.0, accumulate=False, with_bias=False, soft_cap=None):
+    """A 4-bit g64 product of 17 .. 32 rows (the skinny product) against the
+    f64 product of the bf16-effective weights, at the prefill bar."""
+    rng = np.random.default_rng(seed)
+    W = H.affine_weights(oracle, rng, n, k, 4, 64, layout, correction, w_dt)
+    x = H.activations(oracle, rng, m, k, H.BF16)
+    prior = rng.normal(0, 1, m * n).astype(np.float32) if accumulate else None
+    bias = H.store(oracle, rng.normal(0, 0.5, n).astype(np.float32), w_dt) if with_bias else None
+    d = H.to_dev(H.store(oracle, prior, d_dt)) if accumulate else torch_empty(m * n, d_dt)
+    kern = qmm.MatmulKernel(w_dt, H.BF16, d_dt)
+    kern.encode(qmm.MatmulArguments(a=H.to_dev(x), m=m, n=n, k=k, d=d, b=qmm.QuantizedB(
+        codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]), params=qmm.QuantParams(layout, n, k // 64),
+        mode=qmm.MODE_U4, correction=correction, signed_codes=signed,
+        correction_data=None if W["corr"] is None else H.to_dev(W["corr"])),
+        d_transform=qmm.MatmulDOps(ab_scale=ab_scale, accumulate=accumulate,
+                                   bias=None if bias is None else H.to_dev(bias), soft_cap=soft_cap)))
+    torch.cuda.synchronize()
+    got = H.load(oracle, H.from_dev(d, np_dtype(d_dt)), d_dt).reshape(m, n).astype(np.float64)
+    want, mag = bf16_effective_reference(oracle, W, x, m, n, k, 4, 64, layout, correction, w_dt, signed)
+    want = want * ab_scale
+    if accumulate:
+        want = want + H.load(oracle, H.store(oracle, prior, d_dt), d_dt).reshape(m, n)
+    if with_bias:
+        want = want + H.load(oracle, bias, w_dt)[None, :n]
+        mag = mag + 4.0
+    if soft_cap is not None:
+        want = soft_cap * np.tanh(want / soft_cap)
+    check(got.ravel(), want.ravel(), mag=(mag * abs(ab_scale) + (4.0 if accumulate else 0.0)).ravel(),
+          label=f"skinny m{m} n{n} k{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 16, 512), (24, 40, 1536), (32, 1000, 4096), (20, 9000, 4096),
+                                   (32, 96, 12288), (31, 32010, 512), (33, 72, 1024), (48, 1000, 4096),
+                                   (64, 9000, 4096)])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_skinny_product_shapes(qmm, oracle, m, n, k, layout):
+    """17 .. 64 rows, 4-bit g64, K % 512 == 0: the skinny product (one tile
+    pair; ragged N; runs of several pairs at N = 9000 and 32010; deep K;
+    33 .. 64 rows as two 32-row blocks, the second one short)."""
+    _skinny_case(qmm, oracle, m, n, k, layout=layout, seed=m + n + k + layout)
+
+
+@pytest.mark.parametrize("variant", ["symmetric", "signed", "signed_symmetric", "f16_planes", "bf16_out", "d_ops"])
+def test_skinny_product_variants(qmm, oracle, variant):
+    kw = {"symmetric": dict(correction=0), "signed": dict(signed=True),
+          "signed_symmetric": dict(correction=0, signed=True),
+          "f16_planes": dict(w_dt=H.F16), "bf16_out": dict(d_dt=H.BF16),
+          "d_ops": dict(ab_scale=0.75, accumulate=True, with_bias=True, soft_cap=30.0)}[variant]
+    _skinny_case(qmm, oracle, 27, 9000, 4096, seed=400 + len(variant), **kw)
+
+
+def test_skinny_product_batch_matches_single(qmm, oracle):
+    """A K = 12288 and a K = 4096 product of 32 rows in one launch (one pair
+    per workgroup) give the bits of two single launches (three pairs per
+    workgroup for the K = 4096 one)."""
+    rng = np.random.default_rng(41)
+    k = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    made = []
+    for n, kk in [(4096, 12288), (12288, 4096)]:
+        W = H.affine_weights(oracle, rng, n, kk, 4, 64, layout=1)
+        x = H.to_dev(H.activations(oracle, rng, 32, kk))
+        made.append((n, kk, W, x))
+
+    def args(n, kk, W, x):
+        return qmm.MatmulArguments(
+            a=x, m=32, n=n, k=kk, d=torch_empty(32 * n, H.BF16),
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(1, n, kk // 64), correction_data=H.to_dev(W["corr"])))
+    many = [args(*t) for t in made]
+    k.encode_many(many)
+    single = [args(*t) for t in made]
+    for a in single:
+        k.encode(a)
+    torch.cuda.synchronize()
+    for a, b in zip(many, single):
+        assert torch.equal(a.d, b.d)
 
 
 @pytest.mark.parametrize("correction,signed,w_dt,gs", [(0, False, H.BF16, 64), (1, True, H.F16, 32),

@@ -225,13 +225,12 @@ def test_zero_point_correction_exact(qmm, oracle, bits):
 
 # ------------------------------------------------------------ prefill dequant-GEMM
 
-def _gemm_exact(Q, O, *, n, k, bits, correction=1, signed=False, layout=0, seed=0):
+def _gemm_exact(Q, O, *, n, k, bits, correction=1, signed=False, layout=0, seed=0, m=64, label="qgemm_mfma"):
     rng = np.random.default_rng(seed)
     gs = 64
     codes, s, b = _weights(O, rng, n, k, bits, gs, layout, correction, H.BF16)
     cols = _columns(rng, k, 40)
-    m = 64
-    cols = np.resize(cols, m)  # M = 64 > 16: the GEMM
+    cols = np.resize(cols, m)  # M = 64 takes the GEMM, 17 .. 32 (4-bit) the skinny product
     x = H.store(O, _one_hot(k, cols, H.BF16).ravel(), H.BF16)
     G = k // gs
     if correction == 1 and not signed and bits in (4, 8):
@@ -254,7 +253,7 @@ def _gemm_exact(Q, O, *, n, k, bits, correction=1, signed=False, layout=0, seed=
     torch.cuda.synchronize()
     got = d.cpu().numpy().reshape(m, n)
     bad = got.view(np.uint32) != want.view(np.uint32)
-    assert not bad.any(), (f"qgemm_mfma w{bits}: {int(bad.sum())} weights not bit-exact; first "
+    assert not bad.any(), (f"{label} w{bits} m{m}: {int(bad.sum())} weights not bit-exact; first "
                            f"{np.argwhere(bad)[0]}: got {got[bad][0]!r} want {want[bad][0]!r}")
 
 
@@ -269,6 +268,20 @@ def test_gemm_exact_against_bf16_effective_oracle(qmm, oracle, bits, layout):
 @pytest.mark.parametrize("correction,signed", [(0, False), (1, True), (0, True)])
 def test_gemm_exact_variants(qmm, oracle, correction, signed):
     _gemm_exact(qmm, oracle, n=128, k=256, bits=4, correction=correction, signed=signed, seed=180 + correction)
+
+
+@pytest.mark.parametrize("m", [17, 32, 40])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_skinny_exact_against_bf16_effective_oracle(qmm, oracle, m, layout):
+    """qgemm_skinny (4-bit, 17 .. 64 rows; 40 rows as blocks of 32 and 8)
+    dequantises to the same bf16 weights as the GEMM, bit for bit."""
+    _gemm_exact(qmm, oracle, n=96, k=512, bits=4, layout=layout, seed=190 + m + layout, m=m, label="qgemm_skinny")
+
+
+@pytest.mark.parametrize("correction,signed", [(0, False), (1, True), (0, True)])
+def test_skinny_exact_variants(qmm, oracle, correction, signed):
+    _gemm_exact(qmm, oracle, n=48, k=1024, bits=4, correction=correction, signed=signed, seed=195 + correction,
+                m=24, label="qgemm_skinny")
 
 
 # ------------------------------------------------------------ GGUF blocks (hybrid path)
