@@ -1,14 +1,13 @@
 // Skinny dequant product: 17 .. 64 activation rows (short prefill chunks and
-// speculative-verify batches above the small-M matvec; products of more than
-// 32 rows run as 32-row blocks), 4-bit MLX-affine codes, group size 64, bf16
-// activations.
+// speculative-verify batches above the small-M matvec), 4-bit MLX-affine
+// codes, group size 64, bf16 activations.
 //
 // Same arithmetic as the dequant-GEMM (qgemm_mfma.hip) that every product of
 // more than 16 rows takes: each weight is dequantised once to
 // w = bf16_rne(fma(q, s, bias_term)) -- an exact product and one f32 rounding,
 // then bf16 (the reference's BF16-effective dot, vision.rs:249-336) -- and
 // enters v_mfma_f32_16x16x32_bf16 as the B operand; the activation rows enter
-// as plain bf16 in two 16-row blocks (one dequantised operand serves both);
+// as plain bf16 in 16-row blocks (one dequantised operand serves them all);
 // the sums accumulate in f32 over the whole K. The GEMM runs 128-column tiles
 // through 64-value K steps, so a product of few rows costs the serial K loop
 // of its deepest tiles (the Qwen3-8B set: 155 us at 17 to 32 rows, as at
@@ -29,25 +28,39 @@ namespace {
 
 using namespace mfma;
 
-constexpr int kSkPass = 512;             // k per pass: 4 waves x 128
-constexpr int kSkQ = kSkPass / 4;        // k per wave per pass: 2 groups, 4 chunks of 32
-constexpr int kSkTiles = 2;              // 16-row weight tiles per pair
-constexpr int kSkRowB = kSkQ / 2 + 16;   // LDS row of a wave's codes: 80 bytes, 5 chunks (odd: no column conflicts)
-constexpr int kSkGroups = kSkPass / 64;  // groups per pass
-constexpr int kSkMB = 2;                 // 16-row activation blocks
-constexpr int kSkRows = 16 * kSkMB;      // activation rows (M <= 32)
-constexpr int kSkMaxRun = 3;             // tile pairs per workgroup, at most
-constexpr int kSkMaxM = 2 * kSkRows;     // products of more rows run as blocks of kSkRows
+constexpr int kSkTiles = 2;  // 16-row weight tiles per pair
 
+// Geometry of a class: MB 16-row activation blocks, P-value passes (four
+// waves of P / 4), runs of up to RUN tile pairs. Two classes: 17 .. 32 rows
+// (MB 2, P 512, RUN 3) and 33 .. 64 rows (MB 4, P 256, RUN 1: the activation
+// stage and the accumulators of four blocks fit two workgroups per CU only so).
+template <int MB, int P, int RUN>
+struct SkGeo {
+    static constexpr int Q = P / 4;                  // k per wave per pass
+    static constexpr int CH = Q / 32;                // 32-value chunks per wave per pass
+    static constexpr int GW = Q / 64;                // groups per wave per pass
+    static constexpr int GP = P / 64;                // groups per pass
+    static constexpr int CPR = P / 32;               // 16-byte code chunks of a row per pass
+    static constexpr int CPW = CPR / 4;              // of them per wave
+    static constexpr int CT = kRows * CPR;           // code chunks of a tile per pass (threads that load one)
+    static constexpr int PT = kRows * GP;            // plane entries of a tile per pass
+    static constexpr int ROWB = Q / 2 + 16;          // LDS row of a wave's codes (an odd number of chunks)
+    static constexpr int ROWS = 16 * MB;             // activation rows
+    static constexpr int XI = ROWS * (P / 8) / kWg;  // activation vectors per thread
+    static_assert(CT <= kWg && PT <= kWg && (ROWB / 16) % 2 == 1 && XI * kWg == ROWS * (P / 8), "geometry");
+};
+
+template <int MB, int P, int RUN>
 struct SkLds {
+    using G = SkGeo<MB, P, RUN>;
     union {
-        u32x4 stage[kSkTiles][4][kRows * kSkRowB / 16];  // codes [tile][wave][row][80 bytes]
-        float red[kSkTiles][4][kSkRows][kRows];          // per-wave partial outputs, after the last pass
+        u32x4 stage[kSkTiles][4][kRows * G::ROWB / 16];  // codes [tile][wave][row][ROWB bytes]
+        float red[4][G::ROWS][kRows];                    // one tile's per-wave partial outputs, after the last pass
     };
-    float2 pl[kSkTiles][kSkGroups][kRows];  // (scale, bias term) [tile][group][row]
+    float2 pl[kSkTiles][G::GP][kRows];  // (scale, bias term) [tile][group][row]
     // activation rows as bf16 in k order, padded by 64 bytes so that the 16
     // rows of one A read alternate between the two halves of the banks
-    u32x4 xp[kSkRows][kSkPass / 8 + 4];
+    u32x4 xp[G::ROWS][P / 8 + 4];
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* p, uint64_t bytes) {
@@ -72,12 +85,13 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t u, float s, float bt) {
     return w;
 }
 
-template <bool SIGNED>
+template <bool SIGNED, int MB, int P, int RUN>
 __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_skinny(AffineBatch batch) {
     (void)batch;
-    __shared__ SkLds lds;
+    using G = SkGeo<MB, P, RUN>;
+    __shared__ SkLds<MB, P, RUN> lds;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
-    // workgroup b runs run b: up to kSkMaxRun consecutive tile pairs of one op
+    // workgroup b runs run b: up to RUN consecutive tile pairs of one op
     // (op.xid pairs; the last run of an op may be shorter)
     const uint32_t L = blockIdx.x;
     if (L >= kb->total) return;
@@ -91,7 +105,7 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const uint32_t j = lane & 15, kq = lane >> 4;
     const uint32_t pair0 = (L - op.block_begin) * op.xid;
     const uint32_t cnt = min(op.xid, (N + kRows * kSkTiles - 1) / (kRows * kSkTiles) - pair0);
-    const uint32_t passes = K / kSkPass, steps = passes * cnt;
+    const uint32_t passes = K / P, steps = passes * cnt;
     // tile tt of the run's pair t covers rows n0(t, tt) .. +15 and writes
     // those from 32 (pair0 + t) + 16 tt on; a tile past N moves back to end
     // at N, so every row is written once
@@ -100,20 +114,21 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const uint32_t row_bytes = K / 2;
     const bool bf = op.w_dt == STARK_QMM_BF16, biased = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     // Buffer loads at per-thread offsets (a step adds its pair's rows and its
-    // pass's k): activation rows past M lie past their resource and read zeros.
+    // pass's k): activation rows past M lie past their resource and read zeros,
+    // and so do the code chunks of threads past a tile's pass.
     const __amdgpu_buffer_rsrc_t rc = sk_rsrc(op.codes, (uint64_t)N * row_bytes);
     const __amdgpu_buffer_rsrc_t rx = sk_rsrc(op.x, (uint64_t)M * K * 2);
     const __amdgpu_buffer_rsrc_t rs = sk_rsrc(op.scales, 0x7fffffffu);
     const __amdgpu_buffer_rsrc_t rb = biased ? sk_rsrc(op.corr, 0x7fffffffu) : rs;
-    // a tile's pass is 16 rows x 256 bytes: thread tid loads chunk tid % 16 of row tid / 16
-    const uint32_t co = (tid / 16) * row_bytes + 16 * (tid % 16);
-    // plane entry (group pt / 16, row pt % 16); threads 128.. repeat 0..127 and do not stage
-    const uint32_t pt = tid & 127;
+    // thread tid < CT loads chunk tid % CPR of row tid / CPR of a tile's pass
+    const uint32_t co = tid < (uint32_t)G::CT ? (tid / G::CPR) * row_bytes + 16 * (tid % G::CPR) : 0x80000000u;
+    // plane entry (group pt / 16, row pt % 16); threads past PT repeat and do not stage
+    const uint32_t pt = tid % G::PT;
     const uint32_t po = ((pt % 16) * op.os + (pt / 16) * op.gs) * 2;
-    uint32_t xo[8];
+    uint32_t xo[G::XI];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t v = tid + 256 * i, m = v / 64, c = v % 64;
+    for (int i = 0; i < G::XI; ++i) {
+        const uint32_t v = tid + kWg * i, m = v / (P / 8), c = v % (P / 8);
         xo[i] = (m * K + 8 * c) * 2;
     }
 
@@ -121,8 +136,8 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     // pass's activations are staged at its first step. Two register buffers
     // for codes (a step's codes are issued two steps before it is staged) and
     // two for activations.
-    u32x4 wc[2][kSkTiles];  // codes: chunk tid % 16 of row tid / 16 of a tile's pass
-    u32x4 xv[2][8];         // activations: vector v = tid + 256 i is row v / 64, values 8 (v % 64)
+    u32x4 wc[2][kSkTiles];  // codes: chunk tid % CPR of row tid / CPR of a tile's pass
+    u32x4 xv[2][G::XI];     // activations: vector v = tid + 256 i is row v / (P / 8), values 8 (v % (P / 8))
     uint32_t ps[2][kSkTiles], pb[2][kSkTiles];  // raw plane values of (group pt / 16, row pt % 16)
     const auto load_codes = [&](auto buf, uint32_t t, uint32_t kbase) {
         constexpr int B = decltype(buf)::value;
@@ -130,8 +145,8 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
 #pragma unroll
         for (int tt = 0; tt < kSkTiles; ++tt) {
             const uint32_t n0 = n0_of(t, tt);
-            wc[B][tt] = __builtin_bit_cast(u32x4,
-                                           __builtin_amdgcn_raw_buffer_load_b128(rc, co + kbase / 2, n0 * row_bytes, 2));
+            wc[B][tt] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, co + kbase / 2, n0 * row_bytes, 2));
             const uint32_t pr = pg + n0 * op.os * 2;
             ps[B][tt] = __builtin_amdgcn_raw_buffer_load_b16(rs, po, pr, 0);
             pb[B][tt] = __builtin_amdgcn_raw_buffer_load_b16(rb, po, pr, 0);  // unused without biases
@@ -140,16 +155,18 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const auto load_x = [&](auto buf, uint32_t kbase) {
         constexpr int B = decltype(buf)::value;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < G::XI; ++i)
             xv[B][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[i] + kbase * 2, 0, 0));
     };
     const auto stage_codes = [&](auto buf) {
         constexpr int B = decltype(buf)::value;
 #pragma unroll
         for (int tt = 0; tt < kSkTiles; ++tt) {
-            const uint32_t r = tid / 16, c = tid % 16;  // chunk c of the row belongs to wave c / 4
-            *(u32x4*)((uint8_t*)lds.stage[tt][c / 4] + r * kSkRowB + 16 * (c % 4)) = wc[B][tt];
-            if (tid < 128) {
+            if (tid < (uint32_t)G::CT) {
+                const uint32_t r = tid / G::CPR, c = tid % G::CPR;  // chunk c of the row belongs to wave c / CPW
+                *(u32x4*)((uint8_t*)lds.stage[tt][c / G::CPW] + r * G::ROWB + 16 * (c % G::CPW)) = wc[B][tt];
+            }
+            if (tid < (uint32_t)G::PT) {
                 const float sc = plane_f32(ps[B][tt], bf);
                 lds.pl[tt][pt / 16][pt % 16] = float2{sc, biased ? plane_f32(pb[B][tt], bf) : -8.0f * sc};
             }
@@ -158,37 +175,37 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     const auto stage_x = [&](auto buf) {
         constexpr int B = decltype(buf)::value;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t v = tid + 256 * i, m = v / 64, c = v % 64;
+        for (int i = 0; i < G::XI; ++i) {
+            const uint32_t v = tid + kWg * i, m = v / (P / 8), c = v % (P / 8);
             if (m < M) lds.xp[m][c] = xv[B][i];  // rows past M stay zero (cleared once)
         }
     };
 
-    f32x4 acc[kSkMaxRun][kSkTiles][kSkMB];
+    f32x4 acc[RUN][kSkTiles][MB];
 #pragma unroll
-    for (int r = 0; r < kSkMaxRun; ++r)
+    for (int r = 0; r < RUN; ++r)
 #pragma unroll
         for (int tt = 0; tt < kSkTiles; ++tt)
 #pragma unroll
-            for (int b = 0; b < kSkMB; ++b) acc[r][tt][b] = f32x4{0, 0, 0, 0};
-    // the wave's 128 k of a step: 4 chunks of 32 (two per group); lane (j, kq)
-    // dequantises the 8 codes k = 8kq .. 8kq+7 of a chunk of tile row j, the
-    // B operand of both activation blocks
-    const auto compute = [&](f32x4 (&a_acc)[kSkTiles][kSkMB]) {
+            for (int b = 0; b < MB; ++b) acc[r][tt][b] = f32x4{0, 0, 0, 0};
+    // the wave's Q values of a step: CH chunks of 32 (two per group); lane
+    // (j, kq) dequantises the 8 codes k = 8kq .. 8kq+7 of a chunk of tile row
+    // j, the B operand of every activation block
+    const auto compute = [&](f32x4 (&a_acc)[kSkTiles][MB]) {
 #pragma unroll
-        for (int cc = 0; cc < kSkQ / 32; ++cc) {
-            const uint32_t gp = wave * (kSkQ / 64) + cc / 2;  // group within the pass
-            u32x4 a[kSkMB];
+        for (int cc = 0; cc < G::CH; ++cc) {
+            const uint32_t gp = wave * G::GW + cc / 2;  // group within the pass
+            u32x4 a[MB];
 #pragma unroll
-            for (int b = 0; b < kSkMB; ++b) a[b] = lds.xp[16 * b + j][wave * (kSkQ / 8) + 4 * cc + kq];
+            for (int b = 0; b < MB; ++b) a[b] = lds.xp[16 * b + j][wave * (G::Q / 8) + 4 * cc + kq];
 #pragma unroll
             for (int tt = 0; tt < kSkTiles; ++tt) {
                 const uint32_t u =
-                    *(const uint32_t*)((const uint8_t*)lds.stage[tt][wave] + j * kSkRowB + 16 * cc + 4 * kq);
+                    *(const uint32_t*)((const uint8_t*)lds.stage[tt][wave] + j * G::ROWB + 16 * cc + 4 * kq);
                 const float2 p = lds.pl[tt][gp][j];
                 const u32x4 w = dequant8<SIGNED>(u, p.x, p.y);
 #pragma unroll
-                for (int b = 0; b < kSkMB; ++b)
+                for (int b = 0; b < MB; ++b)
                     a_acc[tt][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, a[b]), __builtin_bit_cast(bf16x8, w), a_acc[tt][b], 0, 0, 0);
             }
@@ -198,9 +215,9 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
     // activation rows past M: zero once (their products are zero)
-    for (uint32_t v = tid; v < kSkRows * (kSkPass / 8); v += kWg) {
-        const uint32_t m = v / (kSkPass / 8);
-        if (m >= M) lds.xp[m][v % (kSkPass / 8)] = u32x4{0, 0, 0, 0};
+    for (uint32_t v = tid; v < (uint32_t)G::ROWS * (P / 8); v += kWg) {
+        const uint32_t m = v / (P / 8);
+        if (m >= M) lds.xp[m][v % (P / 8)] = u32x4{0, 0, 0, 0};
     }
     // The step loop is unrolled over two steps, so that a step's code buffer
     // is its parity, a constant. A run of one pair (ONE) takes its activations
@@ -213,10 +230,10 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
         load_codes(B0{}, 0, 0);
         uint32_t lp = 0, lt = 1;  // load cursor: pass and pair of step s + 2
         if (lt == cnt) lt = 0, lp = 1;
-        if (steps > 1) load_codes(B1{}, lt, lp * kSkPass);
+        if (steps > 1) load_codes(B1{}, lt, lp * P);
         if (++lt == cnt) lt = 0, ++lp;
         load_x(B0{}, 0);
-        if (ONE && passes > 1) load_x(B1{}, kSkPass);
+        if (ONE && passes > 1) load_x(B1{}, P);
         uint32_t p = 0, t = 0;
         const auto step = [&](auto b_c, uint32_t s) {
             constexpr int SB = decltype(b_c)::value;
@@ -226,18 +243,18 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             stage_codes(BS{});
             if (ONE || t == 0) {
                 stage_x(BX{});
-                if (p + XA < passes) load_x(BX{}, (p + XA) * kSkPass);
+                if (p + XA < passes) load_x(BX{}, (p + XA) * P);
             }
             __syncthreads();
             if (s + 2 < steps) {
-                load_codes(BS{}, lt, lp * kSkPass);
+                load_codes(BS{}, lt, lp * P);
                 if (++lt == cnt) lt = 0, ++lp;
             }
             if (ONE) {
                 compute(acc[0]);
             } else {
 #pragma unroll
-                for (int r = 0; r < kSkMaxRun; ++r)
+                for (int r = 0; r < RUN; ++r)
                     if (t == (uint32_t)r) compute(acc[r]);
             }
             if (++t == cnt) t = 0, ++p;
@@ -247,65 +264,77 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
             if (s + 1 < steps) step(B1{}, s + 1);
         }
     };
-    if (cnt == 1) run(std::true_type{});
-    else run(std::false_type{});
+    if constexpr (RUN == 1) {
+        run(std::true_type{});
+    } else {
+        if (cnt == 1) run(std::true_type{});
+        else run(std::false_type{});
+    }
 
+    // results, one tile at a time: the four waves' sums meet in LDS (over the
+    // code stage) and the rows go out with the D-ops
 #pragma unroll
-    for (int r = 0; r < kSkMaxRun; ++r) {
+    for (int r = 0; r < RUN; ++r) {
         if ((uint32_t)r >= cnt) break;
-        __syncthreads();  // the results overwrite the code stage / the previous pair's results
 #pragma unroll
-        for (int tt = 0; tt < kSkTiles; ++tt)
+        for (int tt = 0; tt < kSkTiles; ++tt) {
+            __syncthreads();  // the code stage / the previous results are read
 #pragma unroll
-            for (int b = 0; b < kSkMB; ++b)
+            for (int b = 0; b < MB; ++b)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) lds.red[tt][wave][16 * b + 4 * kq + q][j] = acc[r][tt][b][q];
-        __syncthreads();
-        for (uint32_t v = tid; v < (uint32_t)(kSkTiles * kSkRows * kRows); v += kWg) {
-            const uint32_t tt = v / (kSkRows * kRows), m = (v / kRows) % kSkRows, rr = v % kRows;
-            const uint32_t n = n0_of(r, tt) + rr;
-            if (m >= M || n < tile_begin(r, tt)) continue;
-            const size_t o = (size_t)m * N + n;
-            float y = op.ab_scale * ((lds.red[tt][0][m][rr] + lds.red[tt][1][m][rr]) +
-                                     (lds.red[tt][2][m][rr] + lds.red[tt][3][m][rr]));
-            if (op.flags & FLAG_ACCUMULATE) y += load_as_f32(op.d, op.d_dt, o);
-            if (op.bias) y += load_as_f32(op.bias, op.w_dt, n);
-            if (op.flags & FLAG_SOFT_CAP) y = op.soft_cap * tanhf(y / op.soft_cap);
-            store_from_f32(op.d, op.d_dt, o, y);
+                for (int q = 0; q < 4; ++q) lds.red[wave][16 * b + 4 * kq + q][j] = acc[r][tt][b][q];
+            __syncthreads();
+            for (uint32_t v = tid; v < (uint32_t)(G::ROWS * kRows); v += kWg) {
+                const uint32_t m = v / kRows, rr = v % kRows;
+                const uint32_t n = n0_of(r, tt) + rr;
+                if (m >= M || n < tile_begin(r, tt)) continue;
+                const size_t o = (size_t)m * N + n;
+                float y = op.ab_scale * ((lds.red[0][m][rr] + lds.red[1][m][rr]) + (lds.red[2][m][rr] + lds.red[3][m][rr]));
+                if (op.flags & FLAG_ACCUMULATE) y += load_as_f32(op.d, op.d_dt, o);
+                if (op.bias) y += load_as_f32(op.bias, op.w_dt, n);
+                if (op.flags & FLAG_SOFT_CAP) y = op.soft_cap * tanhf(y / op.soft_cap);
+                store_from_f32(op.d, op.d_dt, o, y);
+            }
         }
     }
 }
+
+// the two classes: rows 17 .. 32 and 33 .. 64
+using Small = SkGeo<2, 512, 3>;
+using Wide = SkGeo<4, 256, 1>;
+constexpr uint32_t kSkMaxM = Wide::ROWS;
 
 }  // namespace
 
 bool skinny_eligible(const AffineOp* ops, uint32_t count) {
     for (uint32_t i = 0; i < count; ++i) {
         const AffineOp& o = ops[i];
-        if (o.m <= 16 || o.m > (uint32_t)kSkMaxM || o.group_size != 64 || o.k % kSkPass || o.n < (uint32_t)kRows ||
-            o.gather)
+        if (o.m <= 16 || o.m > kSkMaxM || o.group_size != 64 || o.k % 512 || o.n < (uint32_t)kRows || o.gather)
             return false;
         if (o.x_dt != STARK_QMM_BF16 || !(o.w_dt == STARK_QMM_BF16 || o.w_dt == STARK_QMM_F16)) return false;
         if (!(o.corr_kind == STARK_QMM_CORRECTION_BIASES || o.corr_kind == STARK_QMM_CORRECTION_SYMMETRIC))
             return false;
         if (((uintptr_t)o.codes | (uintptr_t)o.x) & 15) return false;
         // 32-bit buffer offsets
-        if ((uint64_t)o.n * o.k / 2 >= (1ull << 31) || (uint64_t)kSkRows * o.k * 2 >= (1ull << 31)) return false;
+        if ((uint64_t)o.n * o.k / 2 >= (1ull << 31) || (uint64_t)kSkMaxM * o.k * 2 >= (1ull << 31)) return false;
     }
     return count > 0;
 }
 
 namespace {
 
-// One launch of at most kMaxBatchOps ops of at most kSkRows rows each.
-stark_qmm_status launch_skinny_blocks(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream) {
+// One launch of a class's ops (at most kMaxBatchOps, each of at most the
+// class's rows). Run lengths as in the small-M kernel: the launch's pass count
+// per resident workgroup (two per CU) over the op's passes, 1 .. RUN.
+template <int MB, int P, int RUN>
+stark_qmm_status launch_class(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream) {
+    if (count > (uint32_t)kMaxBatchOps) return STARK_QMM_INVALID_ARGUMENT;  // the batch holds kMaxBatchOps
     int dev = 0, cus = 0;
     QMM_HIP_CHECK(hipGetDevice(&dev));
     QMM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    // Run lengths as in the small-M kernel: the launch's pass count per
-    // resident workgroup (two per CU) over the op's passes, 1 .. kSkMaxRun.
     uint64_t units = 0;
     for (uint32_t i = 0; i < count; ++i)
-        units += (uint64_t)((ops[i].n + kRows * kSkTiles - 1) / (kRows * kSkTiles)) * (ops[i].k / kSkPass);
+        units += (uint64_t)((ops[i].n + kRows * kSkTiles - 1) / (kRows * kSkTiles)) * (ops[i].k / P);
     const uint64_t slots = 2 * (uint64_t)std::max(cus, 1);
     const uint64_t per_wg = (units + slots - 1) / slots;
     std::vector<AffineOp> sorted(ops, ops + count);  // longest K first: its runs take the low indices
@@ -314,8 +343,7 @@ stark_qmm_status launch_skinny_blocks(const AffineOp* ops, uint32_t count, bool 
     uint32_t runs = 0;
     for (uint32_t i = 0; i < count; ++i) {
         const uint32_t pairs = (sorted[i].n + kRows * kSkTiles - 1) / (kRows * kSkTiles);
-        const uint32_t run =
-            (uint32_t)std::min<uint64_t>(kSkMaxRun, std::max<uint64_t>(1, per_wg / (sorted[i].k / kSkPass)));
+        const uint32_t run = (uint32_t)std::min<uint64_t>(RUN, std::max<uint64_t>(1, per_wg / (sorted[i].k / P)));
         batch.op[i] = sorted[i];
         batch.op[i].block_begin = runs;
         batch.op[i].xid = run;  // tile pairs per run
@@ -325,36 +353,25 @@ stark_qmm_status launch_skinny_blocks(const AffineOp* ops, uint32_t count, bool 
     batch.total = runs;
     if (runs == 0) return STARK_QMM_OK;
     if (signed_codes)
-        hipLaunchKernelGGL(qgemm_skinny<true>, dim3(runs), dim3(kWg), 0, stream, batch);
+        hipLaunchKernelGGL((qgemm_skinny<true, MB, P, RUN>), dim3(runs), dim3(kWg), 0, stream, batch);
     else
-        hipLaunchKernelGGL(qgemm_skinny<false>, dim3(runs), dim3(kWg), 0, stream, batch);
+        hipLaunchKernelGGL((qgemm_skinny<false, MB, P, RUN>), dim3(runs), dim3(kWg), 0, stream, batch);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
 }
 
 }  // namespace
 
-// Products of 33 .. 64 rows run as blocks of kSkRows rows (the rows' own
-// activations and outputs; every block reads the weights once): against the
-// GEMM's 156-161 us on the Qwen3-8B set at 33 .. 64 rows.
 stark_qmm_status launch_skinny(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream) {
-    std::vector<AffineOp> blocks;
-    for (uint32_t i = 0; i < count; ++i) {
-        const AffineOp& o = ops[i];
-        const size_t dsz = o.d_dt == STARK_QMM_F32 ? 4 : 2;
-        for (uint32_t m0 = 0; m0 < o.m; m0 += kSkRows) {
-            AffineOp b = o;
-            b.m = std::min<uint32_t>(kSkRows, o.m - m0);
-            b.x = (const uint8_t*)o.x + (size_t)m0 * o.k * 2;
-            b.d = (uint8_t*)o.d + (size_t)m0 * o.n * dsz;
-            blocks.push_back(b);
+    std::vector<AffineOp> cls[2];  // rows 17 .. 32, 33 .. 64
+    for (uint32_t i = 0; i < count; ++i) cls[ops[i].m > (uint32_t)Small::ROWS].push_back(ops[i]);
+    for (int c = 0; c < 2; ++c)
+        for (size_t s = 0; s < cls[c].size(); s += kMaxBatchOps) {
+            const uint32_t n = (uint32_t)std::min<size_t>(kMaxBatchOps, cls[c].size() - s);
+            const stark_qmm_status st = c ? launch_class<4, 256, 1>(cls[c].data() + s, n, signed_codes, stream)
+                                          : launch_class<2, 512, 3>(cls[c].data() + s, n, signed_codes, stream);
+            if (st != STARK_QMM_OK) return st;
         }
-    }
-    for (size_t s = 0; s < blocks.size(); s += kMaxBatchOps) {
-        const uint32_t n = (uint32_t)std::min<size_t>(kMaxBatchOps, blocks.size() - s);
-        const stark_qmm_status st = launch_skinny_blocks(blocks.data() + s, n, signed_codes, stream);
-        if (st != STARK_QMM_OK) return st;
-    }
     return STARK_QMM_OK;
 }
 

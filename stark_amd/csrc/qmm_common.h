@@ -240,7 +240,7 @@ stark_qmm_status launch_moe_adjust(uint32_t* ids, float* weights, const float* s
 // Dense small-M kernel: 4-bit, group 64, M = 3 .. 16, K % 1024 == 0 (qmv_small_m.hip).
 bool small_m_eligible(const AffineOp* ops, uint32_t count);
 stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream);
-// Skinny dequant product: 4-bit, group 64, M = 17 .. 64 (32-row blocks), K % 512 == 0, the
+// Skinny dequant product: 4-bit, group 64, M = 17 .. 64, K % 512 == 0, the
 // dequant-GEMM's bf16-effective arithmetic (qgemm_skinny.hip).
 bool skinny_eligible(const AffineOp* ops, uint32_t count);
 stark_qmm_status launch_skinny(const AffineOp* ops, uint32_t count, bool signed_codes, hipStream_t stream);
