@@ -364,7 +364,7 @@ def config1(args, torch, Q):
             verify_lines(args, torch, Q, gen, kern, layers, stream)
         return
     # The other configurations, measured in the same run and attached to this
-    # line (one line per run): verify M = 2..16, config 2, config 3, config 4
+    # line (one line per run): verify M = 2..16 and M = 32, 64, config 2, config 3, config 4
     # prefill (bf16 and int8 activations). Each is summarised; a failure is
     # recorded in place of its figures and does not stop the run.
     global SINK
@@ -386,7 +386,7 @@ def config1(args, torch, Q):
             others.append({"metric": what, "error": f"{type(e).__name__}: {e}"[:300]})
         print(f"bench: {what} done in {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
 
-    collect("config 1 verify M=2,4,8,16", lambda: verify_lines(args, torch, Q, gen, kern, layers, stream))
+    collect("config 1 verify M=2,4,8,16,32,64", lambda: verify_lines(args, torch, Q, gen, kern, layers, stream))
     del all_args, layers, outs
     torch.cuda.empty_cache()
     sub = argparse.Namespace(**{**vars(args), "steps": 200, "warmup": 40, "decode_tokens": 0})
@@ -403,10 +403,11 @@ def config1(args, torch, Q):
 
 
 def verify_lines(args, torch, Q, gen, kern, layers, stream):
-    """Config 1 at M = 2, 4, 8, 16 (speculative verify): the same layer set and
+    """Config 1 at M = 2, 4, 8, 16 (speculative verify) and 32, 64 (short
+    prefill chunks, the skinny dequant product): the same layer set and
     rotating copies, M activation rows per product (q/k/v and gate/up share
-    theirs), one line each (opt-in: the default run prints the M = 1 line only)."""
-    for m in (2, 4, 8, 16):
+    theirs), one line each (attached to the default run's line)."""
+    for m in (2, 4, 8, 16, 32, 64):
         xs = {}
         for name, n, k in SHAPES:
             key = {"k_proj": "q_proj", "v_proj": "q_proj", "up_proj": "gate_proj"}.get(name, name)
@@ -424,7 +425,8 @@ def verify_lines(args, torch, Q, gen, kern, layers, stream):
                    args.warmup, stream)
         nbytes = algorithmic_bytes(m)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        emit({"metric": f"q4 matvec HBM GB/s at M={m} (speculative verify)", "value": round(gbs, 1),
+        what = "speculative verify" if m <= 16 else "short prefill, bf16-effective weights"
+        emit({"metric": f"q4 matvec HBM GB/s at M={m} ({what})", "value": round(gbs, 1),
                           "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
                           "vs_baseline": None, "dtype": "bf16",
@@ -859,14 +861,14 @@ def main():
                          "decode measurement (0 skips it)")
     ap.add_argument("--decode-only", action="store_true", help="only the end-to-end decode line (config 4)")
     ap.add_argument("--headline-only", action="store_true",
-                    help="config 1: print the headline line alone (the default run also measures verify M=2..16, "
+                    help="config 1: print the headline line alone (the default run also measures verify M=2..64, "
                          "configs 2 and 3 and the config-4 prefill and attaches them as other_configs)")
     ap.add_argument("--decode-form", choices=("chain", "fused"), default="fused",
                     help="decode stand-in: products after attention as one chained launch per layer (chain) or one "
                          "launch per product with norm/SiLU prologues (fused)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verify", action="store_true",
-                    help="config 1: also print the M = 2, 4, 8, 16 (speculative verify) lines")
+                    help="config 1: also print the M = 2, 4, 8, 16 (speculative verify) and M = 32, 64 (short prefill) lines")
     ap.add_argument("--copies", type=int, default=LAYERS,
                     help="config 1: distinct layer-weight copies the steps rotate through (36 = one Qwen3-8B)")
     ap.add_argument("--eager", action="store_true",
