@@ -70,14 +70,11 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(2))) void q
     (void)batch;
     __shared__ SmLds lds;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
-    // A workgroup runs a run of up to kSmMaxRun consecutive tile pairs of one
-    // op (op.xid pairs; the last run of an op may be shorter). Blocks are
-    // dealt to the 8 XCDs round-robin (block b on XCD b % 8): block b runs run
-    // (b % 8) * (grid / 8) + b / 8, so consecutive runs, whose rows share the
-    // 64-row lines of the group-output planes, sit on one XCD and its L2
-    // (kb->total: the runs; the grid is padded to a multiple of 8).
-    const uint32_t bx = blockIdx.x;
-    const uint32_t L = bx;
+    // Workgroup b runs run b: up to kSmMaxRun consecutive tile pairs of one op
+    // (op.xid pairs; the last run of an op may be shorter). A run's rows
+    // already share the 64-row lines of the group-output planes; consecutive
+    // runs on one XCD measured slower than this plain order.
+    const uint32_t L = blockIdx.x;
     if (L >= kb->total) return;
     uint32_t oi = 0;
     for (uint32_t i = 1; i < kb->count; ++i)
@@ -370,11 +367,10 @@ stark_qmm_status launch_small_m(const AffineOp* ops, uint32_t count, bool signed
     batch.count = count;
     batch.total = runs;
     if (runs == 0) return STARK_QMM_OK;
-    const uint32_t grid = (runs + 7) / 8 * 8;  // the same number of blocks on every XCD
     if (signed_codes)
-        hipLaunchKernelGGL(qmv_small_m<true>, dim3(grid), dim3(kWg), 0, stream, batch);
+        hipLaunchKernelGGL(qmv_small_m<true>, dim3(runs), dim3(kWg), 0, stream, batch);
     else
-        hipLaunchKernelGGL(qmv_small_m<false>, dim3(grid), dim3(kWg), 0, stream, batch);
+        hipLaunchKernelGGL(qmv_small_m<false>, dim3(runs), dim3(kWg), 0, stream, batch);
     QMM_HIP_CHECK(hipGetLastError());
     return STARK_QMM_OK;
 }
