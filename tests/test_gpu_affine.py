@@ -689,6 +689,34 @@ def test_skinny_product_batch_matches_single(qmm, oracle):
         assert torch.equal(a.d, b.d)
 
 
+def test_encode_many_mixed_row_classes_match_single(qmm, oracle):
+    """One encode_many call over products of 1, 2, 8, 24, 48 and 100 rows (the
+    streaming kernel, the slot form, the small-M kernel, both skinny classes
+    and the GEMM) gives each product the bits of its own encode call."""
+    rng = np.random.default_rng(43)
+    k = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    made = []
+    for m, n, kk in [(1, 4096, 4096), (2, 1000, 4096), (8, 96, 4096), (24, 1000, 4096), (48, 96, 1024),
+                     (100, 256, 1024)]:
+        W = H.affine_weights(oracle, rng, n, kk, 4, 64, layout=1)
+        x = H.to_dev(H.activations(oracle, rng, m, kk))
+        made.append((m, n, kk, W, x))
+
+    def args(m, n, kk, W, x):
+        return qmm.MatmulArguments(
+            a=x, m=m, n=n, k=kk, d=torch_empty(m * n, H.BF16),
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(1, n, kk // 64), correction_data=H.to_dev(W["corr"])))
+    many = [args(*t) for t in made]
+    k.encode_many(many)
+    single = [args(*t) for t in made]
+    for a in single:
+        k.encode(a)
+    torch.cuda.synchronize()
+    for (m, n, kk, _, _), a, b in zip(made, many, single):
+        assert torch.equal(a.d, b.d), f"m{m} n{n} k{kk}"
+
+
 @pytest.mark.parametrize("correction,signed,w_dt,gs", [(0, False, H.BF16, 64), (1, True, H.F16, 32),
                                                        (0, True, H.BF16, 128), (1, False, H.F16, 64)])
 def test_prefill_gemm_corrections(qmm, oracle, correction, signed, w_dt, gs):
