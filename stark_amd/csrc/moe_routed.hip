@@ -388,6 +388,7 @@ __global__ __launch_bounds__(kWg) void moe_down_mfma(GroupedLaunch launch) {
 // the down product and the rank accumulation read. This takes the separate
 // route launch off the one-token chain.
 constexpr uint32_t kOneTokenExperts = 256;
+constexpr uint64_t kOneTokenWork = 1ull << 20;  // A * H * E bound of the fused path (top-8, H 768, 128 experts: 0.75)
 
 struct RouteOneArgs {
     const float* logits;
@@ -815,8 +816,13 @@ stark_qmm_status routed_run(const stark_qmm_routed_args* a, uint8_t* ws, uint64_
     const uint32_t sort = a->expert_scales ? a->sort_expert_ids : 1;
     const uint64_t nkeys = (uint64_t)R * E;
     const bool sg = a->up.signed_codes != 0;
-    // one token: route, slots and the up product in one launch
-    const bool one = R == 1 && E <= kOneTokenExperts;
+    // one token: route, slots and the up product in one launch, while the
+    // route that each of its A * H / 8 workgroups repeats (O(E^2) compares)
+    // costs less than the separate route launch (measured, one token,
+    // separate against fused: model 2048 / hidden 768 / 128 experts 19.4 vs
+    // 17.1 us; 256 experts 21.4 vs 22.6; hidden 1536, 128 experts 37.4 vs
+    // 38.3; 256 experts 39.3 vs 49.1)
+    const bool one = R == 1 && E <= kOneTokenExperts && (uint64_t)A * H * E <= kOneTokenWork;
     if (one) {
         RouteOneArgs ra{a->router_logits, a->expert_scales, E, A, a->round_weights_bf16, a->round_logits_bf16,
                         (uint32_t)adjust, sort, ids, weights, table, header};
