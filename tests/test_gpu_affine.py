@@ -717,6 +717,41 @@ def test_encode_many_mixed_row_classes_match_single(qmm, oracle):
         assert torch.equal(a.d, b.d), f"m{m} n{n} k{kk}"
 
 
+def test_encode_many_row_classes_in_graph_replays(qmm, oracle):
+    """encode_many over products of 1, 8, 24 and 48 rows recorded in a HIP graph:
+    three replays, with eager launches and synchronizations between them, each
+    give the eager call's bits."""
+    rng = np.random.default_rng(47)
+    k = qmm.MatmulKernel(H.BF16, H.BF16, H.BF16)
+    made = []
+    for m, n, kk in [(1, 2080, 4096), (8, 1000, 4096), (24, 1000, 2048), (48, 136, 1024)]:
+        W = H.affine_weights(oracle, rng, n, kk, 4, 64, layout=1)
+        made.append((m, n, kk, W, H.to_dev(H.activations(oracle, rng, m, kk))))
+
+    def args(m, n, kk, W, x):
+        return qmm.MatmulArguments(
+            a=x, m=m, n=n, k=kk, d=torch_empty(m * n, H.BF16),
+            b=qmm.QuantizedB(codes=H.to_dev(W["codes"]), scales=H.to_dev(W["scales"]),
+                             params=qmm.QuantParams(1, n, kk // 64), correction_data=H.to_dev(W["corr"])))
+    eager = [args(*t) for t in made]
+    k.encode_many(eager)
+    torch.cuda.synchronize()
+    cap = [args(*t) for t in made]
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        k.encode_many(cap, stream=s)
+    for rep in range(3):
+        for a in cap:
+            a.d.fill_(0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for (m, n, kk, _, _), a, b in zip(made, cap, eager):
+            assert torch.equal(a.d, b.d), f"replay {rep}: m{m} n{n} k{kk}"
+        k.encode_many([args(*made[0])])  # eager work between the replays
+
+
 @pytest.mark.parametrize("correction,signed,w_dt,gs", [(0, False, H.BF16, 64), (1, True, H.F16, 32),
                                                        (0, True, H.BF16, 128), (1, False, H.F16, 64)])
 def test_prefill_gemm_corrections(qmm, oracle, correction, signed, w_dt, gs):
