@@ -275,6 +275,7 @@ struct GgufOp {
     uint32_t n, k, m;
     uint32_t x_dt, d_dt;     // 0/0 means f32/f32
     uint32_t block_begin;
+    uint32_t run;            // dense matrix-core form: tile pairs per workgroup (set by the launch)
 };
 struct GgufBatch {
     GgufOp op[kMaxBatchOps];

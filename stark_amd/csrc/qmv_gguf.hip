@@ -102,6 +102,7 @@ __global__ void gguf_generic(GgufOp op) {
 
 
 // ------------------------------------------------------------------ geometry
+constexpr int kGgMaxRun = 3;  // dense form: tile pairs per workgroup, at most
 // M real rows take MR = 2M activation rows (hi/lo); MP rows per MFMA block.
 template <int KIND, int MP, int MB>
 struct GGeo {
@@ -197,6 +198,10 @@ struct GEngine {
     // rows (pieces past the pass's blocks read as zero through the buffer
     // resource) and the f32 activation chunks.
     __device__ __forceinline__ void load(const GgufOp& op, const uint32_t (&n0)[TPW], uint32_t M, uint32_t kbase) {
+        load_codes(op, n0, kbase);
+        load_x(op, M, kbase);
+    }
+    __device__ __forceinline__ void load_codes(const GgufOp& op, const uint32_t (&n0)[TPW], uint32_t kbase) {
         const uint32_t K = op.k, kvals = min((uint32_t)PASS, K - kbase);
         const uint32_t row_bytes = K / BE * BB;
         const uint32_t vbytes = kvals / BE * BB;  // valid bytes of a row in this pass
@@ -214,6 +219,9 @@ struct GEngine {
                 w[tt][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(crs, vo, 0, kBufNt));
             }
         }
+    }
+    __device__ __forceinline__ void load_x(const GgufOp& op, uint32_t M, uint32_t kbase) {
+        const uint32_t K = op.k, kvals = min((uint32_t)PASS, K - kbase);
         // activations: chunks past the rows, the pass or K read zeros from past the resource
         const __amdgpu_buffer_rsrc_t xrs =
             __builtin_amdgcn_make_buffer_rsrc((void*)op.x, 0, (int)min((uint64_t)M * K * 4, (uint64_t)0x7fffffffu), 0x00020000);
@@ -230,7 +238,10 @@ struct GEngine {
     // Stage codes and activations, then (after a barrier) decode the pass's
     // block headers into per-group scale and bias.
     __device__ __forceinline__ void stage(uint32_t kvals, uint32_t M, uint32_t* status) {
-        bool bad = false;
+        stage_codes();
+        stage_x(kvals, M, status);
+    }
+    __device__ __forceinline__ void stage_codes() {
 #pragma unroll
         for (int tt = 0; tt < TPW; ++tt) {
             uint8_t* ws = (uint8_t*)lds.stage[tt][wave];
@@ -240,6 +251,9 @@ struct GEngine {
                 if (p < (uint32_t)(kRows * PPR)) *(u32x4*)(ws + (p / PPR) * ROWB + (p % PPR) * 16) = w[tt][i];
             }
         }
+    }
+    __device__ __forceinline__ void stage_x(uint32_t kvals, uint32_t M, uint32_t* status) {
+        bool bad = false;
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
             const uint32_t v = tid + i * kWg, r = v / (PASS / 8), c = v % (PASS / 8);
@@ -483,6 +497,60 @@ struct GEngine {
         }
     }
 
+    // Dense form, a run of cnt tile pairs (pair0 ..) pass-major: step s is
+    // pass s / cnt of pair s % cnt; a pass's activations are converted and
+    // staged at its first step and serve every pair of the run (their loads
+    // are issued right after that staging, a pass ahead); a step's codes are
+    // issued a step ahead. Pair t accumulates in acc[t]. Runs of more than one
+    // pair need K % PASS == 0 (only a one-pair run has a tail pass).
+    template <int RUN>
+    __device__ __forceinline__ void run_runs(const GgufOp& op, uint32_t pair0, uint32_t cnt, uint32_t M,
+                                             uint32_t* status, f32x4 (&acc)[RUN][TPW]) {
+        static_assert(G::DENSE, "runs are the dense form's");
+        const uint32_t K = op.k, N = op.n, passes = (K + PASS - 1) / PASS, steps = passes * cnt;
+        const auto rows = [&](uint32_t t, uint32_t (&n0)[TPW]) {
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) n0[tt] = min(kRows * (TPW * (pair0 + t) + tt), N - kRows);
+        };
+#pragma unroll
+        for (int r = 0; r < RUN; ++r)
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) acc[r][tt] = f32x4{0, 0, 0, 0};
+        uint32_t n0[TPW];
+        rows(0, n0);
+        load_codes(op, n0, 0);
+        load_x(op, M, 0);
+        uint32_t p = 0, t = 0;
+        for (uint32_t s = 0; s < steps; ++s) {
+            const uint32_t kbase = p * PASS, kvals = min((uint32_t)PASS, K - kbase);
+            if (s) __syncthreads();  // every wave finished the previous step's LDS
+            stage_codes();
+            if (t == 0) {
+                stage_x(kvals, M, status);
+                if (p + 1 < passes) load_x(op, M, kbase + PASS);
+            }
+            __syncthreads();
+            if (s + 1 < steps) {
+                uint32_t m0[TPW];
+                rows(t + 1 < cnt ? t + 1 : 0, m0);
+                load_codes(op, m0, (t + 1 < cnt ? p : p + 1) * PASS);
+            }
+            decode_meta(kvals);
+            __syncthreads();
+            if (t == 0) {
+                if (kvals == (uint32_t)PASS)
+                    compute_dense<false>(kvals, acc[0]);
+                else
+                    compute_dense<true>(kvals, acc[0]);
+            } else {
+#pragma unroll
+                for (int r = 1; r < RUN; ++r)
+                    if (t == (uint32_t)r) compute_dense<false>(kvals, acc[r]);
+            }
+            if (++t == cnt) t = 0, ++p;
+        }
+    }
+
     __device__ __forceinline__ void run(const GgufOp& op, const uint32_t (&n0)[TPW], uint32_t M, uint32_t* status) {
         const uint32_t K = op.k;
         f32x4 acc[MB * TPW];
@@ -547,6 +615,37 @@ __global__ __launch_bounds__(kWg) __attribute__((amdgpu_waves_per_eu(MB >= 4 ? 2
     const GgufOp& op = kb->op[oi];
     const uint32_t N = op.n;
     constexpr int TPW = GGeo<KIND, MP, MB>::TPW, RR = MP * MB / 2;
+    if constexpr (GGeo<KIND, MP, MB>::DENSE) {
+        // a run of up to kGgMaxRun tile pairs per workgroup (op.run pairs; the
+        // last run of an op may be shorter)
+        const uint32_t pair0 = (blockIdx.x - op.block_begin) * op.run;
+        const uint32_t cnt = min(op.run, (N + kRows * TPW - 1) / (kRows * TPW) - pair0);
+        GEngine<KIND, MP, MB> e(lds);
+        f32x4 acc[kGgMaxRun][TPW];
+        e.template run_runs<kGgMaxRun>(op, pair0, cnt, op.m, kb->status, acc);
+#pragma unroll
+        for (int r = 0; r < kGgMaxRun; ++r) {
+            if ((uint32_t)r >= cnt) break;
+            __syncthreads();  // the results overwrite the code stage / the previous pair's results
+            const uint32_t j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4, wave = threadIdx.x >> 6;
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {  // real rows 2kq and 2kq+1 of column j
+                lds.red[tt][wave][2 * kq][j] = acc[r][tt][0];
+                lds.red[tt][wave][2 * kq + 1][j] = acc[r][tt][1];
+            }
+            __syncthreads();
+            const uint32_t t0 = kRows * TPW * (pair0 + r);
+            for (uint32_t t = threadIdx.x; t < (uint32_t)(TPW * RR * kRows); t += kWg) {
+                const uint32_t tt = t / (RR * kRows), m = (t / kRows) % RR, rr = t % kRows;
+                const uint32_t n = min(t0 + kRows * tt, N - kRows) + rr;
+                if (m >= op.m || n < t0 + kRows * tt) continue;
+                const float v = (lds.red[tt][0][m][rr] + lds.red[tt][1][m][rr]) +
+                                (lds.red[tt][2][m][rr] + lds.red[tt][3][m][rr]);
+                store_from_f32(op.d, op.d_dt, (size_t)m * N + n, v);
+            }
+        }
+        return;
+    }
     // tile tt covers rows n0[tt] .. +15 and writes those from t0 + 16 tt on; a
     // tile past N moves back to end at N, so every row is written once
     const uint32_t t0 = (blockIdx.x - op.block_begin) * kRows * TPW;
@@ -570,13 +669,36 @@ stark_qmm_status launch_mfma(const GgufOp* ops, uint32_t count, uint32_t* status
     // longest K first: the workgroups with the most passes are dispatched first
     std::vector<GgufOp> sorted(ops, ops + count);
     std::stable_sort(sorted.begin(), sorted.end(), [](const GgufOp& a, const GgufOp& b) { return a.k > b.k; });
+    using G = GGeo<KIND, MP, MB>;
     GgufBatch batch{};
     batch.status = status;
+    // Dense form: runs of tile pairs, so that one activation conversion serves
+    // up to kGgMaxRun pairs. The run length of an op is the launch's pass
+    // count per resident workgroup (two per CU) over the op's passes, as in
+    // the small-M kernel: a launch with fewer pairs than workgroup slots (one
+    // product of N = 12288) keeps one pair per workgroup.
+    uint64_t per_wg = 1;
+    if constexpr (G::DENSE) {
+        int dev = 0, cus = 0;
+        QMM_HIP_CHECK(hipGetDevice(&dev));
+        QMM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        uint64_t units = 0;
+        for (uint32_t i = 0; i < count; ++i)
+            units += (uint64_t)((sorted[i].n + kRows * G::TPW - 1) / (kRows * G::TPW)) *
+                     ((sorted[i].k + G::PASS - 1) / G::PASS);
+        const uint64_t slots = 2 * (uint64_t)std::max(cus, 1);
+        per_wg = (units + slots - 1) / slots;
+    }
     uint32_t blocks = 0;
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = sorted[i];
         batch.op[i].block_begin = blocks;
-        blocks += (sorted[i].n + kRows * GGeo<KIND, MP, MB>::TPW - 1) / (kRows * GGeo<KIND, MP, MB>::TPW);
+        const uint32_t pairs = (sorted[i].n + kRows * G::TPW - 1) / (kRows * G::TPW);
+        uint32_t run = 1;
+        if (G::DENSE && sorted[i].k % G::PASS == 0)
+            run = (uint32_t)std::min<uint64_t>(kGgMaxRun, std::max<uint64_t>(1, per_wg / (sorted[i].k / G::PASS)));
+        batch.op[i].run = run;
+        blocks += (pairs + run - 1) / run;
     }
     batch.count = count;
     if (blocks) hipLaunchKernelGGL((gguf_mfma<KIND, MP, MB>), dim3(blocks), dim3(kWg), 0, stream, batch);

@@ -64,6 +64,35 @@ def test_packed_small_m_ragged(qmm, oracle, kind, n, k, m):
 
 
 @pytest.mark.parametrize("kind", [8, 12])
+@pytest.mark.parametrize("m", [4, 8])
+def test_packed_small_m_runs(qmm, oracle, kind, m):
+    """More tile pairs than workgroup slots (N = 39990, K = 1024): a workgroup
+    runs three pairs under one activation conversion; the last run holds two
+    pairs, the last one shifted back to end at N."""
+    _run_packed(qmm, oracle, kind, 39990, 1024, m, seed=500 + m + kind)
+
+
+@pytest.mark.parametrize("kind", [8, 12])
+def test_packed_runs_batch_matches_single(qmm, oracle, kind):
+    """Two products of 8 rows in one mapped_many call (runs sized for the
+    whole launch) give the bits of two calls of one product each."""
+    rng = np.random.default_rng(61 + kind)
+    made = []
+    for n, k in [(12288, 4096), (24576, 1024)]:
+        blocks = _packed(oracle, rng, kind, n, k)
+        x = torch.from_numpy(_x(rng, 8, k).ravel()).cuda()
+        made.append((n, k, H.to_dev(blocks.ravel()), x))
+
+    def op(n, k, codes, x):
+        return qmm.MappedOperation(matrices=[qmm.MappedMatrix(codes=codes)] * 8, inputs=x, rows=n, columns=k,
+                                   format=("packed", kind))
+    both = qmm.mapped_many([op(*t) for t in made])
+    alone = [qmm.mapped_many([op(*t)])[0] for t in made]
+    for (n, k, _, _), a, b in zip(made, both, alone):
+        assert torch.equal(a, b), f"kind{kind} n{n} k{k}"
+
+
+@pytest.mark.parametrize("kind", [8, 12])
 def test_packed_batch_of_mixed_k(qmm, oracle, kind):
     """One mapped_many call with products of different K and M (the launch
     orders them longest K first; every output goes to its own operation)."""
