@@ -570,6 +570,38 @@ def config2(args, torch, Q):
                                      "bytes_per_step": nbytes, "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)},
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
+    # GGUF layer sets: the Qwen3-8B projection set (q, k, v, o, gate, up, down) in Q8_0 and
+    # Q4_K as one mapped_many call at M = 8 (the hybrid engine's batched products), rotating
+    # more than 1 GiB of copies, graph-timed like the lines above
+    m = 8
+    for kind, name, block, bsize in ((Q.KIND_Q8_0, "gguf_q8_0", 32, 34), (Q.KIND_Q4_K, "gguf_q4_k", 256, 144)):
+        wbytes = sum(n * (k // block) * bsize for _, n, k in SHAPES)
+        copies = int(-(-ROTATION_BYTES // wbytes))
+        xs = {k: torch.randn(m, k, generator=gen, device="cuda").contiguous() for k in (4096, 12288)}
+        status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        preps = []
+        for _ in range(copies):
+            mats = []
+            for _, n, k in SHAPES:
+                mats.append(quantize_gguf_gpu(torch, torch.randn(n, k, generator=gen, device="cuda") * 0.02, kind))
+            ops = [Q.MappedOperation(matrices=[Q.MappedMatrix(codes=v)] * m, inputs=xs[k].view(-1), rows=n, columns=k,
+                                     format=("packed", kind)) for (_, n, k), v in zip(SHAPES, mats)]
+            preps.append((Q.mapped_prepare(ops)[0], mats))
+        ms, ran = graph_timed(torch, lambda i, st: Q.mapped_many_async(preps[i][0], status, st), copies, args.steps)
+        assert int(status.item()) == 0
+        nbytes = wbytes + sum(m * 4 * (k + n) for _, n, k in SHAPES)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        emit({"metric": f"{name} layer-set matvec HBM GB/s at M={m}", "value": round(gbs, 1), "unit": "GB/s",
+              "n_gpus": 1, "steps": ran, "warmup": copies, "ms_per_step": round(ms, 5), "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+              "data": "synthetic: N(0,0.02) weights quantized by the format's rule, N(0,1) activations",
+              "config": {"workload": f"{name} Qwen3-8B projection set (7 products) in one mapped_many call, M={m}, "
+                                     f"{copies} rotating copies ({copies * wbytes / 2 ** 30:.2f} GiB), one captured "
+                                     f"HIP graph over the copies, replayed",
+                         "bytes_per_step": nbytes, "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2)},
+              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
+        del preps
 
 
 def config3(args, torch, Q):
