@@ -7,11 +7,12 @@
 // threadgroup memory in the activation type and multiplies there; the CPU
 // twin of that rounding is reference_affine_linear_bf16
 // (backends/cpu/kernel/matmul/vision.rs:249-336): w = bf16_rne(f32(q)*s + b).
-// Here: a workgroup (8 waves) owns a 256x128 output tile; per 64-wide K step
-// the X tile is staged in LDS as is and the W tile is dequantised into LDS as
-// bf16 (w = s*q + bias_term rounded to nearest even), double-buffered so the
-// next step's global loads overlap the current step's v_mfma_f32_16x16x32_bf16
-// work (each wave: a 64x64 block = 4x4 MFMA tiles, 32 MFMAs per K step). The
+// Here: a workgroup (8 waves) owns a 256x128 or 128x128 output tile; per
+// 64-wide K step the X tile is staged in LDS as is and the W tile is
+// dequantised into LDS as bf16 (w = s*q + bias_term rounded to nearest even),
+// double-buffered so the next steps' global loads overlap the current step's
+// v_mfma_f32_16x16x32_bf16 work (each wave: a 64x64 block = 4x4 MFMA tiles,
+// 32 MFMAs per K step, or 32x64 in the 128-row tile). The
 // D-ops (ab_scale, accumulate, bias, soft-cap) and the output rounding follow
 // kernel.rs:270-281.
 #include "qmm_common.h"
@@ -24,9 +25,20 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Tiles of BM rows (256: eight waves; 128: four waves, for products of at
-// most 128 rows) x kBN columns; kBM is the taller of the two.
-constexpr int kBM = 256, kBN = 128, kBK = 64;
+// Tiles of BM rows (256, or 128 for products of at most kBM128Rows rows) x
+// kBN columns, eight waves each; kBM is the taller of the two.
+constexpr int kBM = 256, kBN = 128, kBK = 64, kThreads = 512;
+// Products of few rows have few tiles, and the serial K loop of the deepest
+// (the Qwen3-8B down product's, K = 12288) sets their time. The 128-row
+// tile keeps eight waves (two per SIMD, so one wave's dequantisation and LDS
+// traffic overlap the other's MFMAs) and three register stages of loads in
+// flight. Qwen3-8B set at 65 / 128 / 256 / 384 rows: 161 / 165 / 183 / 240
+// us with 256-row tiles above 128 rows and 128-row tiles of four waves and
+// two stages; 124 / 132 / 153 / 223 us now (eight waves alone 135 / 150 at
+// 65 / 128; four or six stages 128-136; three stages in the 256-row tile
+// lost 6% at 256 and 2048 rows). From 512 rows the 256-row tile is faster.
+constexpr uint32_t kBM128Rows = 384;
+__host__ __device__ constexpr uint32_t gemm_bm(uint32_t m) { return m <= kBM128Rows ? 128 : 256; }
 
 // LDS tiles: rows of 64 bf16 (128 bytes, 8 chunks of 16 bytes), chunk c of
 // row r stored at chunk c ^ (r & 7). Every access here moves 16 bytes per
@@ -50,7 +62,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p, uint6
 // BITS: 4 or 8. CORR: 0 symmetric, 1 biases. BF: bf16 (else f16) planes.
 template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
 __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint32_t by) {
-    constexpr int kThreads = 2 * BM;
+    constexpr int XI = BM * 8 / kThreads;  // X chunks per thread
+    constexpr int MI = BM / 64;            // 16-row blocks per wave
+    constexpr int NS = BM == 128 ? 3 : 2;  // register stages of loads
     __shared__ GemmLds<BM> lds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -59,7 +73,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     const uint32_t row_bytes = K * BITS / 8;
 
     // ---- per-thread load assignment
-    // X tile [256][64] bf16: 4 x 16 B per thread (row v / 8, column 8 * (v % 8)).
+    // X tile [BM][64] bf16: XI x 16 B per thread (row v / 8, column 8 * (v % 8)).
     // W tile: 128 rows x (64*BITS/8) bytes, 4 threads per row, 16 codes each
     // (8 bytes of 4-bit codes, 16 of 8-bit). Each dequantised weight serves the
     // tile's 256 rows: against 128x128 tiles of four waves (two workgroups per
@@ -71,7 +85,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     constexpr int WPASS = CB > 16 ? CB / 16 : 1;         // passes over the rows
     constexpr int WW = WPT * BITS / 32;  // code words per thread
     struct Stage {
-        u32x4 xa[4];
+        u32x4 xa[XI];
         uint32_t wc[WPASS][4];
         float ws[WPASS], wb[WPASS];
     };
@@ -87,9 +101,9 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(op.scales, 0x7fffffffu);
     const __amdgpu_buffer_rsrc_t rb = gemm_rsrc(op.corr, 0x7fffffffu);
     const uint32_t lgs = 31 - __builtin_clz(op.group_size);
-    uint32_t xo[4], wo[WPASS], po[WPASS];
+    uint32_t xo[XI], wo[WPASS], po[WPASS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XI; ++i) {
         const uint32_t v = tid + kThreads * i, r = v / 8, c = (v % 8) * 8;
         xo[i] = ((m0 + r) * K + c) * 2;
     }
@@ -102,7 +116,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     }
     auto load_step = [&](Stage& st, uint32_t k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < XI; ++i)
             st.xa[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[i] + k0 * 2, 0, 0));
         const uint32_t pg = (k0 >> lgs) * op.gs * 2;  // bytes of the step's first plane group
 #pragma unroll
@@ -129,7 +143,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     // s times a <= 8-bit q), rounded to bf16 by v_cvt_pk_bf16_f32 (nearest even).
     auto store_step = [&](const Stage& st, int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < XI; ++i) {
             const uint32_t v = tid + kThreads * i, r = v / 8, c = (v % 8) * 8;
             lds.a[buf][r][swz(r, c / 8)] = st.xa[i];
         }
@@ -174,21 +188,21 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         }
     };
 
-    // wave (wm, wn) owns rows wm*64.., cols wn*64.. of the tile
+    // wave (wm, wn) owns rows wm*16MI.., cols wn*64.. of the tile
     const int wm = wave >> 1, wn = wave & 1;  // wm 0..3
     const uint32_t li = lane & 15, lk = (lane >> 4) * 8;
-    f32x4 acc[4][4];
+    f32x4 acc[MI][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
     auto compute = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 32) {
-            u32x4 af[4], bfr[4];
+            u32x4 af[MI], bfr[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t r = wm * 64 + 16 * i + li;
+            for (int i = 0; i < MI; ++i) {
+                const uint32_t r = wm * (16 * MI) + 16 * i + li;
                 af[i] = lds.a[buf][r][swz(r, (kk + lk) / 8)];
             }
 #pragma unroll
@@ -197,7 +211,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
                 bfr[j] = lds.b[buf][r][swz(r, (kk + lk) / 8)];
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -205,10 +219,10 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         }
     };
 
-    // Two register stages: step s computes from LDS buffer s%2 while step s+1
-    // (loaded during step s-1) is dequantised into the other buffer and step
-    // s+2's global loads fly; the barriers order LDS only, so those loads stay
-    // in flight across them.
+    // NS register stages: step s computes from LDS buffer s%2 while step s+1
+    // (loaded NS - 1 steps earlier) is dequantised into the other buffer and
+    // the loads of steps s+2 .. s+NS fly; the barriers order LDS only, so
+    // those loads stay in flight across them.
     const auto lds_barrier = [] {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
@@ -219,23 +233,54 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     // every load before the next dequantisation): the step indices of the
     // prefetches are clamped, so the last ones re-read the final step's tile
     // into a buffer that is not computed again.
-    Stage sa, sb;
-    load_step(sa, 0);
-    load_step(sb, min(1u, steps - 1) * kBK);
-    store_step(sa, 0);
-    lds_barrier();
-    uint32_t s = 0;
-    for (; s + 2 <= steps; s += 2) {
-        load_step(sa, min(s + 2, steps - 1) * kBK);
-        compute(0);
-        store_step(sb, 1);
-        lds_barrier();
-        load_step(sb, min(s + 3, steps - 1) * kBK);
-        compute(1);
+    if constexpr (NS == 2) {
+        Stage sa, sb;
+        load_step(sa, 0);
+        load_step(sb, min(1u, steps - 1) * kBK);
         store_step(sa, 0);
         lds_barrier();
+        uint32_t s = 0;
+        for (; s + 2 <= steps; s += 2) {
+            load_step(sa, min(s + 2, steps - 1) * kBK);
+            compute(0);
+            store_step(sb, 1);
+            lds_barrier();
+            load_step(sb, min(s + 3, steps - 1) * kBK);
+            compute(1);
+            store_step(sa, 0);
+            lds_barrier();
+        }
+        if (s < steps) compute(0);  // odd step count: the last step sits in buffer 0
+    } else {
+        // step s + u of an unrolled block uses stage u % NS and LDS buffer
+        // u % 2, constants (a run-time stage index makes the compiler join
+        // the stages with copies that wait for their loads); fewer than U
+        // steps left take the same bodies, their extra loads clamped
+        constexpr int U = NS % 2 ? 2 * NS : NS;
+        Stage st[NS];
+#pragma unroll
+        for (int i = 0; i < NS; ++i) load_step(st[i], min((uint32_t)i, steps - 1) * kBK);
+        store_step(st[0], 0);
+        lds_barrier();
+        uint32_t s = 0;
+        for (; s + U <= steps; s += U) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                load_step(st[u % NS], min(s + u + NS, steps - 1) * kBK);
+                compute(u % 2);
+                store_step(st[(u + 1) % NS], (u + 1) % 2);
+                lds_barrier();
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U - 1; ++u) {
+            if (s + u >= steps) break;
+            load_step(st[u % NS], min(s + u + NS, steps - 1) * kBK);
+            compute(u % 2);
+            store_step(st[(u + 1) % NS], (u + 1) % 2);
+            lds_barrier();
+        }
     }
-    if (s < steps) compute(0);  // odd step count: the last step sits in buffer 0
 
     // ---- epilogue: C[i][j] of a 16x16 block sits in lane j + 16*(i/4), element i%4
     // Full tiles with a plain bf16 store (no D-op past ab_scale): one row
@@ -244,10 +289,10 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         m0 + BM <= M && n0 + kBN <= N) {
         uint16_t* const d = (uint16_t*)op.d;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
+                const uint32_t m = m0 + wm * (16 * MI) + 16 * i + 4 * (lane >> 4) + e;
                 uint16_t* const row = d + (size_t)m * N + n0 + wn * 64 + (lane & 15);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) row[16 * j] = f32_to_bf16_bits(op.ab_scale * acc[i][j][e]);
@@ -255,12 +300,12 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + e;
+                const uint32_t m = m0 + wm * (16 * MI) + 16 * i + 4 * (lane >> 4) + e;
                 const uint32_t n = n0 + wn * 64 + 16 * j + (lane & 15);
                 if (m >= M || n >= N) continue;
                 const size_t o = (size_t)m * N + n;
@@ -273,7 +318,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
 }
 
 template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
-__global__ __launch_bounds__(2 * BM) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
     gemm_tile<BITS, CORR, SIGNED, BF, BM>(op, blockIdx.x, blockIdx.y);
 }
 
@@ -287,7 +332,7 @@ __host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o, uint32_t bm) {
 // while the op's column-block count is a multiple of 8. Ops come longest K
 // first, so the costliest tiles are dispatched first.
 template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
-__global__ __launch_bounds__(2 * BM) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
     (void)batch;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
     uint32_t t = blockIdx.x, i = 0;
@@ -342,17 +387,15 @@ stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t st
 }
 
 stark_qmm_status launch_affine_gemm_rows(const AffineOp& op, int bits, hipStream_t stream) {
-    // products of at most 128 rows take 128-row tiles of four waves (half
-    // the idle rows of a 256-row tile)
-    const uint32_t bm = op.m <= 128 ? 128 : 256;
+    const uint32_t bm = gemm_bm(op.m);
     const dim3 grid((op.n + kBN - 1) / kBN, (op.m + bm - 1) / bm);
     if (grid.x == 0 || grid.y == 0) return STARK_QMM_OK;
     const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     const bool bf = op.w_dt == STARK_QMM_BF16;
 #define QMM_G(B, C, S, F)                                                                        \
     do {                                                                                         \
-        if (bm == 128) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 128>), grid, dim3(256), 0, stream, op); \
-        else hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 256>), grid, dim3(512), 0, stream, op);          \
+        if (bm == 128) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 128>), grid, dim3(kThreads), 0, stream, op); \
+        else hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 256>), grid, dim3(kThreads), 0, stream, op);          \
     } while (0)
 #define QMM_G_BITS(B)                                                      \
     if (bi) {                                                              \
@@ -388,7 +431,7 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
     AffineBatch batch{};
     uint32_t mmax = 0;
     for (uint32_t i = 0; i < count; ++i) mmax = std::max(mmax, sorted[i].m);
-    const uint32_t bm = mmax <= 128 ? 128 : 256;  // as launch_affine_gemm_rows
+    const uint32_t bm = gemm_bm(mmax);  // as launch_affine_gemm_rows
     uint64_t tiles = 0;
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = sorted[i];
@@ -404,8 +447,8 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
     const dim3 grid((uint32_t)tiles);
 #define QMM_GG(B, C, S, F)                                                                          \
     do {                                                                                            \
-        if (bm == 128) hipLaunchKernelGGL((qgemm_group<B, C, S, F, 128>), grid, dim3(256), 0, stream, batch); \
-        else hipLaunchKernelGGL((qgemm_group<B, C, S, F, 256>), grid, dim3(512), 0, stream, batch);          \
+        if (bm == 128) hipLaunchKernelGGL((qgemm_group<B, C, S, F, 128>), grid, dim3(kThreads), 0, stream, batch); \
+        else hipLaunchKernelGGL((qgemm_group<B, C, S, F, 256>), grid, dim3(kThreads), 0, stream, batch);          \
     } while (0)
 #define QMM_GG_BITS(B)                                                                 \
     if (bi) {                                                                          \

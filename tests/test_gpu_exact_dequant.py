@@ -225,12 +225,12 @@ def test_zero_point_correction_exact(qmm, oracle, bits):
 
 # ------------------------------------------------------------ prefill dequant-GEMM
 
-def _gemm_exact(Q, O, *, n, k, bits, correction=1, signed=False, layout=0, seed=0, m=64, label="qgemm_mfma"):
+def _gemm_exact(Q, O, *, n, k, bits, correction=1, signed=False, layout=0, seed=0, m=72, label="qgemm_mfma"):
     rng = np.random.default_rng(seed)
     gs = 64
     codes, s, b = _weights(O, rng, n, k, bits, gs, layout, correction, H.BF16)
     cols = _columns(rng, k, 40)
-    cols = np.resize(cols, m)  # M = 64 takes the GEMM, 17 .. 32 (4-bit) the skinny product
+    cols = np.resize(cols, m)  # M > 64 takes the GEMM, 17 .. 64 (4-bit g64, K % 512 == 0) the skinny product
     x = H.store(O, _one_hot(k, cols, H.BF16).ravel(), H.BF16)
     G = k // gs
     if correction == 1 and not signed and bits in (4, 8):
@@ -268,6 +268,18 @@ def test_gemm_exact_against_bf16_effective_oracle(qmm, oracle, bits, layout):
 @pytest.mark.parametrize("correction,signed", [(0, False), (1, True), (0, True)])
 def test_gemm_exact_variants(qmm, oracle, correction, signed):
     _gemm_exact(qmm, oracle, n=128, k=256, bits=4, correction=correction, signed=signed, seed=180 + correction)
+
+
+@pytest.mark.parametrize("m,k", [(65, 64), (130, 384), (200, 448), (384, 512), (96, 576), (300, 640), (128, 704),
+                                 (72, 3136), (385, 448), (520, 320)])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gemm_exact_tile_classes(qmm, oracle, m, k, bits):
+    """Both GEMM tile classes (128-row tiles of eight waves with three load
+    stages up to 384 rows, 256-row tiles above) at 64-value step counts that
+    leave every remainder of the six-step unrolled blocks (1, 6 .. 11 and 49
+    steps; odd and even counts in the 256-row class), ragged N: the bf16
+    weight tiles stay bit-exact."""
+    _gemm_exact(qmm, oracle, n=136, k=k, bits=bits, seed=200 + m + bits, m=m)
 
 
 @pytest.mark.parametrize("m", [17, 32, 40])
