@@ -386,7 +386,7 @@ def config1(args, torch, Q):
             others.append({"metric": what, "error": f"{type(e).__name__}: {e}"[:300]})
         print(f"bench: {what} done in {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
 
-    collect("config 1 verify M=2,4,8,16,32,64", lambda: verify_lines(args, torch, Q, gen, kern, layers, stream))
+    collect("config 1 verify M=2,4,8,16,32,64,128,256", lambda: verify_lines(args, torch, Q, gen, kern, layers, stream))
     del all_args, layers, outs
     torch.cuda.empty_cache()
     sub = argparse.Namespace(**{**vars(args), "steps": 200, "warmup": 40, "decode_tokens": 0})
@@ -403,11 +403,12 @@ def config1(args, torch, Q):
 
 
 def verify_lines(args, torch, Q, gen, kern, layers, stream):
-    """Config 1 at M = 2, 4, 8, 16 (speculative verify) and 32, 64 (short
-    prefill chunks, the skinny dequant product): the same layer set and
+    """Config 1 at M = 2, 4, 8, 16 (speculative verify), 32, 64 (short
+    prefill chunks, the skinny dequant product) and 128, 256 (the
+    dequant-GEMM's 128-row tiles): the same layer set and
     rotating copies, M activation rows per product (q/k/v and gate/up share
     theirs), one line each (attached to the default run's line)."""
-    for m in (2, 4, 8, 16, 32, 64):
+    for m in (2, 4, 8, 16, 32, 64, 128, 256):
         xs = {}
         for name, n, k in SHAPES:
             key = {"k_proj": "q_proj", "v_proj": "q_proj", "up_proj": "gate_proj"}.get(name, name)
@@ -425,7 +426,8 @@ def verify_lines(args, torch, Q, gen, kern, layers, stream):
                    args.warmup, stream)
         nbytes = algorithmic_bytes(m)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        what = "speculative verify" if m <= 16 else "short prefill, bf16-effective weights"
+        what = ("speculative verify" if m <= 16 else "short prefill, bf16-effective weights" if m <= 64
+                else "short prefill, dequant-GEMM")
         emit({"metric": f"q4 matvec HBM GB/s at M={m} ({what})", "value": round(gbs, 1),
                           "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
@@ -435,7 +437,8 @@ def verify_lines(args, torch, Q, gen, kern, layers, stream):
                                                  f"{args.copies} rotating layer copies, one launch per step",
                                      "bytes_per_step": nbytes,
                                      "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
-                                     "tokens_per_s": round(m * 1000.0 / ms, 1)},
+                                     "tokens_per_s": round(m * 1000.0 / ms, 1),
+                                     "tflop_s": round(2.0 * m * sum(n * k for _, n, k in SHAPES) / (ms * 1e-3) / 1e12, 1)},
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                        "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
 
@@ -893,7 +896,7 @@ def main():
                          "decode measurement (0 skips it)")
     ap.add_argument("--decode-only", action="store_true", help="only the end-to-end decode line (config 4)")
     ap.add_argument("--headline-only", action="store_true",
-                    help="config 1: print the headline line alone (the default run also measures verify M=2..64, "
+                    help="config 1: print the headline line alone (the default run also measures verify M=2..256, "
                          "configs 2 and 3 and the config-4 prefill and attaches them as other_configs)")
     ap.add_argument("--decode-form", choices=("chain", "fused"), default="fused",
                     help="decode stand-in: products after attention as one chained launch per layer (chain) or one "
