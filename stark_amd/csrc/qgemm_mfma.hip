@@ -7,12 +7,12 @@
 // threadgroup memory in the activation type and multiplies there; the CPU
 // twin of that rounding is reference_affine_linear_bf16
 // (backends/cpu/kernel/matmul/vision.rs:249-336): w = bf16_rne(f32(q)*s + b).
-// Here: a workgroup (8 waves) owns a 256x128 or 128x128 output tile; per
+// Here: a workgroup (8 waves) owns a 256x128, 128x128 or 128x64 output tile; per
 // 64-wide K step the X tile is staged in LDS as is and the W tile is
 // dequantised into LDS as bf16 (w = s*q + bias_term rounded to nearest even),
 // double-buffered so the next steps' global loads overlap the current step's
 // v_mfma_f32_16x16x32_bf16 work (each wave: a 64x64 block = 4x4 MFMA tiles,
-// 32 MFMAs per K step, or 32x64 in the 128-row tile). The
+// 32 MFMAs per K step, or 32x64 / 32x32 in the 128-row tiles). The
 // D-ops (ab_scale, accumulate, bias, soft-cap) and the output rounding follow
 // kernel.rs:270-281.
 #include "qmm_common.h"
@@ -26,7 +26,8 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Tiles of BM rows (256, or 128 for products of at most kBM128Rows rows) x
-// kBN columns, eight waves each; kBM is the taller of the two.
+// BN columns (128, or 64 for products of at most kBN64Rows rows), eight
+// waves each; kBM and kBN are the largest.
 constexpr int kBM = 256, kBN = 128, kBK = 64, kThreads = 512;
 // Products of few rows have few tiles, and the serial K loop of the deepest
 // (the Qwen3-8B down product's, K = 12288) sets their time. The 128-row
@@ -37,8 +38,12 @@ constexpr int kBM = 256, kBN = 128, kBK = 64, kThreads = 512;
 // two stages; 124 / 132 / 153 / 223 us now (eight waves alone 135 / 150 at
 // 65 / 128; four or six stages 128-136; three stages in the 256-row tile
 // lost 6% at 256 and 2048 rows). From 512 rows the 256-row tile is faster.
-constexpr uint32_t kBM128Rows = 384;
+// Up to 128 rows, 64-column tiles halve each step's dequantisation and MFMA
+// work and double the tiles: 125 / 134 -> 97 / 112 us at 65 / 128 rows
+// (151 -> 169 us at 256 rows, where the 128-column tile stays).
+constexpr uint32_t kBM128Rows = 384, kBN64Rows = 128;
 __host__ __device__ constexpr uint32_t gemm_bm(uint32_t m) { return m <= kBM128Rows ? 128 : 256; }
+__host__ __device__ constexpr uint32_t gemm_bn(uint32_t m) { return m <= kBN64Rows ? 64 : 128; }
 
 // LDS tiles: rows of 64 bf16 (128 bytes, 8 chunks of 16 bytes), chunk c of
 // row r stored at chunk c ^ (r & 7). Every access here moves 16 bytes per
@@ -47,10 +52,10 @@ __host__ __device__ constexpr uint32_t gemm_bm(uint32_t m) { return m <= kBM128R
 // and the dequantised W stores (4 rows x 2 chunks). (Measured against
 // c ^ ((r >> 1) & 7), which spreads 16 lanes over 64 banks: 611 vs 604
 // TFLOP/s on the Qwen3-8B prefill set; 144-byte padded rows: 597.)
-template <int BM>
+template <int BM, int BN>
 struct GemmLds {
     u32x4 a[2][BM][kBK / 8];
-    u32x4 b[2][kBN][kBK / 8];
+    u32x4 b[2][BN][kBK / 8];
 };
 __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) { return c ^ (r & 7); }
 
@@ -58,28 +63,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p, uint6
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)min(bytes, (uint64_t)0x7fffffffu), 0x00020000);
 }
 
-// Output tile (bx, by) of one product: columns 128 bx.., rows 256 by...
+// Output tile (bx, by) of one product: columns BN bx.., rows BM by...
 // BITS: 4 or 8. CORR: 0 symmetric, 1 biases. BF: bf16 (else f16) planes.
-template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
+template <int BITS, int CORR, bool SIGNED, bool BF, int BM, int BN>
 __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint32_t by) {
     constexpr int XI = BM * 8 / kThreads;  // X chunks per thread
     constexpr int MI = BM / 64;            // 16-row blocks per wave
     constexpr int NS = BM == 128 ? 3 : 2;  // register stages of loads
-    __shared__ GemmLds<BM> lds;
+    constexpr int MJ = BN / 32;            // 16-column blocks per wave
+    __shared__ GemmLds<BM, BN> lds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t M = op.m, N = op.n, K = op.k;
-    const uint32_t m0 = by * BM, n0 = bx * kBN;
+    const uint32_t m0 = by * BM, n0 = bx * BN;
     const uint32_t row_bytes = K * BITS / 8;
 
     // ---- per-thread load assignment
     // X tile [BM][64] bf16: XI x 16 B per thread (row v / 8, column 8 * (v % 8)).
-    // W tile: 128 rows x (64*BITS/8) bytes, 4 threads per row, 16 codes each
-    // (8 bytes of 4-bit codes, 16 of 8-bit). Each dequantised weight serves the
+    // W tile: BN rows x (64*BITS/8) bytes, 4 threads per row, 16 codes each
+    // (8 bytes of 4-bit codes, 16 of 8-bit; 64-column tiles: 8 threads per
+    // row, 8 codes each). Each dequantised weight serves the
     // tile's 256 rows: against 128x128 tiles of four waves (two workgroups per
     // CU), half the dequantisation per MFMA, 869-871 vs 792-795 TFLOP/s on the
     // Qwen3-8B prefill set.
-    constexpr int CB = kBN * kBK * BITS / 8 / kThreads;  // code bytes per thread
+    constexpr int CB = BN * kBK * BITS / 8 / kThreads;  // code bytes per thread
     constexpr int WPT = (CB > 16 ? 16 : CB) * 8 / BITS;  // codes per thread per pass
     constexpr int TPR = kBK / WPT;                       // threads per row
     constexpr int WPASS = CB > 16 ? CB / 16 : 1;         // passes over the rows
@@ -121,7 +128,10 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         const uint32_t pg = (k0 >> lgs) * op.gs * 2;  // bytes of the step's first plane group
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
-            if constexpr (WW == 4) {
+            if constexpr (WW == 1) {
+                st.wc[p][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, wo[p] + k0 * BITS / 8, 0, 2);
+                st.wc[p][1] = st.wc[p][2] = st.wc[p][3] = 0;
+            } else if constexpr (WW == 4) {
                 const u32x4 t = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo[p] + k0 * BITS / 8, 0, 2));
                 st.wc[p][0] = t[0]; st.wc[p][1] = t[1]; st.wc[p][2] = t[2]; st.wc[p][3] = t[3];
             } else {
@@ -154,7 +164,7 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
             // branch keeps the dequantisation below the MFMA block in its
             // schedule: removing it measured 746 vs 791-797 TFLOP/s, a
             // sched_barrier in its place 712-721, with 128x128 tiles)
-            if (r >= (uint32_t)kBN) continue;
+            if (r >= (uint32_t)BN) continue;
             const float s = st.ws[p];
             // bias term: biases, or -s * 2^(bits-1) for the symmetric correction
             const float b = CORR == 1 ? st.wb[p] : -s * (float)(1 << (BITS - 1));
@@ -188,32 +198,32 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
         }
     };
 
-    // wave (wm, wn) owns rows wm*16MI.., cols wn*64.. of the tile
+    // wave (wm, wn) owns rows wm*16MI.., cols wn*BN/2.. of the tile
     const int wm = wave >> 1, wn = wave & 1;  // wm 0..3
     const uint32_t li = lane & 15, lk = (lane >> 4) * 8;
-    f32x4 acc[MI][4];
+    f32x4 acc[MI][MJ];
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+        for (int j = 0; j < MJ; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
     auto compute = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 32) {
-            u32x4 af[MI], bfr[4];
+            u32x4 af[MI], bfr[MJ];
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
                 const uint32_t r = wm * (16 * MI) + 16 * i + li;
                 af[i] = lds.a[buf][r][swz(r, (kk + lk) / 8)];
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t r = wn * 64 + 16 * j + li;
+            for (int j = 0; j < MJ; ++j) {
+                const uint32_t r = wn * (BN / 2) + 16 * j + li;
                 bfr[j] = lds.b[buf][r][swz(r, (kk + lk) / 8)];
             }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < MJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, af[i]), __builtin_bit_cast(bf16x8, bfr[j]), acc[i][j], 0, 0, 0);
         }
@@ -286,27 +296,27 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     // Full tiles with a plain bf16 store (no D-op past ab_scale): one row
     // pointer per (i, e), the column blocks at fixed offsets from it.
     if (!(op.flags & (FLAG_ACCUMULATE | FLAG_SOFT_CAP)) && !op.bias && op.d_dt == STARK_QMM_BF16 &&
-        m0 + BM <= M && n0 + kBN <= N) {
+        m0 + BM <= M && n0 + BN <= N) {
         uint16_t* const d = (uint16_t*)op.d;
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t m = m0 + wm * (16 * MI) + 16 * i + 4 * (lane >> 4) + e;
-                uint16_t* const row = d + (size_t)m * N + n0 + wn * 64 + (lane & 15);
+                uint16_t* const row = d + (size_t)m * N + n0 + wn * (BN / 2) + (lane & 15);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) row[16 * j] = f32_to_bf16_bits(op.ab_scale * acc[i][j][e]);
+                for (int j = 0; j < MJ; ++j) row[16 * j] = f32_to_bf16_bits(op.ab_scale * acc[i][j][e]);
             }
         return;
     }
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < MJ; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t m = m0 + wm * (16 * MI) + 16 * i + 4 * (lane >> 4) + e;
-                const uint32_t n = n0 + wn * 64 + 16 * j + (lane & 15);
+                const uint32_t n = n0 + wn * (BN / 2) + 16 * j + (lane & 15);
                 if (m >= M || n >= N) continue;
                 const size_t o = (size_t)m * N + n;
                 float v = op.ab_scale * acc[i][j][e];
@@ -317,13 +327,13 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
             }
 }
 
-template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
+template <int BITS, int CORR, bool SIGNED, bool BF, int BM, int BN>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(AffineOp op) {
-    gemm_tile<BITS, CORR, SIGNED, BF, BM>(op, blockIdx.x, blockIdx.y);
+    gemm_tile<BITS, CORR, SIGNED, BF, BM, BN>(op, blockIdx.x, blockIdx.y);
 }
 
-__host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o, uint32_t bm) {
-    return ((o.n + kBN - 1) / kBN) * ((o.m + bm - 1) / bm);
+__host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o, uint32_t bm, uint32_t bn) {
+    return ((o.n + bn - 1) / bn) * ((o.m + bm - 1) / bm);
 }
 
 // Several products in one grid (ops of one template class): the tiles of op
@@ -331,19 +341,19 @@ __host__ __device__ inline uint32_t gemm_tiles(const AffineOp& o, uint32_t bm) {
 // block), so that the column blocks that share a weight tile keep one XCD
 // while the op's column-block count is a multiple of 8. Ops come longest K
 // first, so the costliest tiles are dispatched first.
-template <int BITS, int CORR, bool SIGNED, bool BF, int BM>
+template <int BITS, int CORR, bool SIGNED, bool BF, int BM, int BN>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_group(AffineBatch batch) {
     (void)batch;
     const AffineBatch* kb = (const AffineBatch*)__builtin_amdgcn_kernarg_segment_ptr();
     uint32_t t = blockIdx.x, i = 0;
     for (; i + 1 < kb->count; ++i) {
-        const uint32_t nt = gemm_tiles(kb->op[i], BM);
+        const uint32_t nt = gemm_tiles(kb->op[i], BM, BN);
         if (t < nt) break;
         t -= nt;
     }
     const AffineOp& op = kb->op[i];
-    const uint32_t gx = (op.n + kBN - 1) / kBN;
-    gemm_tile<BITS, CORR, SIGNED, BF, BM>(op, t % gx, t / gx);
+    const uint32_t gx = (op.n + BN - 1) / BN;
+    gemm_tile<BITS, CORR, SIGNED, BF, BM, BN>(op, t % gx, t / gx);
 }
 
 }  // namespace
@@ -387,15 +397,16 @@ stark_qmm_status launch_affine_gemm(const AffineOp& op, int bits, hipStream_t st
 }
 
 stark_qmm_status launch_affine_gemm_rows(const AffineOp& op, int bits, hipStream_t stream) {
-    const uint32_t bm = gemm_bm(op.m);
-    const dim3 grid((op.n + kBN - 1) / kBN, (op.m + bm - 1) / bm);
+    const uint32_t bm = gemm_bm(op.m), bn = gemm_bn(op.m);
+    const dim3 grid((op.n + bn - 1) / bn, (op.m + bm - 1) / bm);
     if (grid.x == 0 || grid.y == 0) return STARK_QMM_OK;
     const bool sg = (op.flags & FLAG_SIGNED) != 0, bi = op.corr_kind == STARK_QMM_CORRECTION_BIASES;
     const bool bf = op.w_dt == STARK_QMM_BF16;
 #define QMM_G(B, C, S, F)                                                                        \
     do {                                                                                         \
-        if (bm == 128) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 128>), grid, dim3(kThreads), 0, stream, op); \
-        else hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 256>), grid, dim3(kThreads), 0, stream, op);          \
+        if (bm == 256) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 256, 128>), grid, dim3(kThreads), 0, stream, op); \
+        else if (bn == 64) hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 128, 64>), grid, dim3(kThreads), 0, stream, op); \
+        else hipLaunchKernelGGL((qgemm_mfma<B, C, S, F, 128, 128>), grid, dim3(kThreads), 0, stream, op);        \
     } while (0)
 #define QMM_G_BITS(B)                                                      \
     if (bi) {                                                              \
@@ -431,11 +442,11 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
     AffineBatch batch{};
     uint32_t mmax = 0;
     for (uint32_t i = 0; i < count; ++i) mmax = std::max(mmax, sorted[i].m);
-    const uint32_t bm = gemm_bm(mmax);  // as launch_affine_gemm_rows
+    const uint32_t bm = gemm_bm(mmax), bn = gemm_bn(mmax);  // as launch_affine_gemm_rows
     uint64_t tiles = 0;
     for (uint32_t i = 0; i < count; ++i) {
         batch.op[i] = sorted[i];
-        tiles += gemm_tiles(sorted[i], bm);
+        tiles += gemm_tiles(sorted[i], bm, bn);
     }
     batch.count = count;
     batch.total = (uint32_t)tiles;
@@ -447,8 +458,9 @@ stark_qmm_status launch_affine_gemm_group(const AffineOp* ops, uint32_t count, i
     const dim3 grid((uint32_t)tiles);
 #define QMM_GG(B, C, S, F)                                                                          \
     do {                                                                                            \
-        if (bm == 128) hipLaunchKernelGGL((qgemm_group<B, C, S, F, 128>), grid, dim3(kThreads), 0, stream, batch); \
-        else hipLaunchKernelGGL((qgemm_group<B, C, S, F, 256>), grid, dim3(kThreads), 0, stream, batch);          \
+        if (bm == 256) hipLaunchKernelGGL((qgemm_group<B, C, S, F, 256, 128>), grid, dim3(kThreads), 0, stream, batch); \
+        else if (bn == 64) hipLaunchKernelGGL((qgemm_group<B, C, S, F, 128, 64>), grid, dim3(kThreads), 0, stream, batch); \
+        else hipLaunchKernelGGL((qgemm_group<B, C, S, F, 128, 128>), grid, dim3(kThreads), 0, stream, batch);        \
     } while (0)
 #define QMM_GG_BITS(B)                                                                 \
     if (bi) {                                                                          \

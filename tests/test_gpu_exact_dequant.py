@@ -274,11 +274,11 @@ def test_gemm_exact_variants(qmm, oracle, correction, signed):
                                  (72, 3136), (385, 448), (520, 320)])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_gemm_exact_tile_classes(qmm, oracle, m, k, bits):
-    """Both GEMM tile classes (128-row tiles of eight waves with three load
-    stages up to 384 rows, 256-row tiles above) at 64-value step counts that
-    leave every remainder of the six-step unrolled blocks (1, 6 .. 11 and 49
-    steps; odd and even counts in the 256-row class), ragged N: the bf16
-    weight tiles stay bit-exact."""
+    """The three GEMM tile classes (128x64 tiles up to 128 rows, 128x128 up
+    to 384, both of eight waves with three load stages; 256x128 above) at
+    64-value step counts that leave every remainder of the six-step unrolled
+    blocks (1, 6 .. 11 and 49 steps; odd and even counts in the 256-row
+    class), ragged N: the bf16 weight tiles stay bit-exact."""
     _gemm_exact(qmm, oracle, n=136, k=k, bits=bits, seed=200 + m + bits, m=m)
 
 
