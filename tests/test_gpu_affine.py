@@ -754,8 +754,9 @@ def test_encode_many_row_classes_in_graph_replays(qmm, oracle):
 
 @pytest.mark.parametrize("correction,signed,w_dt,gs", [(0, False, H.BF16, 64), (1, True, H.F16, 32),
                                                        (0, True, H.BF16, 128), (1, False, H.F16, 64)])
-def test_prefill_gemm_corrections(qmm, oracle, correction, signed, w_dt, gs):
-    m, n, k = 40, 160, 512
+@pytest.mark.parametrize("m", [40, 200])  # 40: skinny (group 64) or 128x64 GEMM tiles; 200: 128x128 tiles
+def test_prefill_gemm_corrections(qmm, oracle, correction, signed, w_dt, gs, m):
+    n, k = 160, 512
     rng = np.random.default_rng(gs + correction)
     for layout in (0, 1):
         W = H.affine_weights(oracle, rng, n, k, 4, gs, layout, correction, w_dt, quantizer=False)
