@@ -102,7 +102,12 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
     // zeros (with no branch around the load); a W row past N takes its plane
     // entries from row N - 1 (its outputs are never stored). The plane group
     // of a thread's codes is k0 / gs + (its offset in the step) / gs: group
-    // sizes are 32, 64 or 128 and k0 a multiple of 64.
+    // sizes are 32, 64 or 128 and k0 a multiple of 64. A step reads 32 bytes
+    // (4-bit) or 64 bytes (8-bit) of each W row's 128-byte line and the next
+    // steps the rest, so the W loads are ordinary (cached) loads: with the
+    // nontemporal hint L2 dropped the line between steps and fetched it again
+    // (Qwen3-8B set: 253 -> 167 MB fetched at 128 rows, 115 -> 102 us; 929 ->
+    // 993 TFLOP/s at 2048 rows).
     const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(op.x, (uint64_t)M * K * 2);
     const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(op.codes, (uint64_t)N * row_bytes);
     const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(op.scales, 0x7fffffffu);
@@ -129,14 +134,14 @@ __device__ __forceinline__ void gemm_tile(const AffineOp& op, uint32_t bx, uint3
 #pragma unroll
         for (int p = 0; p < WPASS; ++p) {
             if constexpr (WW == 1) {
-                st.wc[p][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, wo[p] + k0 * BITS / 8, 0, 2);
+                st.wc[p][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, wo[p] + k0 * BITS / 8, 0, 0);
                 st.wc[p][1] = st.wc[p][2] = st.wc[p][3] = 0;
             } else if constexpr (WW == 4) {
-                const u32x4 t = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo[p] + k0 * BITS / 8, 0, 2));
+                const u32x4 t = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo[p] + k0 * BITS / 8, 0, 0));
                 st.wc[p][0] = t[0]; st.wc[p][1] = t[1]; st.wc[p][2] = t[2]; st.wc[p][3] = t[3];
             } else {
                 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-                const u32x2v t = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rw, wo[p] + k0 * BITS / 8, 0, 2));
+                const u32x2v t = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rw, wo[p] + k0 * BITS / 8, 0, 0));
                 st.wc[p][0] = t[0]; st.wc[p][1] = t[1]; st.wc[p][2] = 0; st.wc[p][3] = 0;
             }
             const uint32_t hs = __builtin_amdgcn_raw_buffer_load_b16(rs, po[p], pg, 0);
